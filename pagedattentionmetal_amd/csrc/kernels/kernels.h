@@ -1,0 +1,101 @@
+// kernels.h - launch interface of the gfx950 kernels (host side).
+//
+// The runtime (engine.cpp) fills these parameter blocks and calls the launchers;
+// every launcher enqueues on the given HIP stream and returns the launch status.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pam {
+
+enum DType : int32_t { kF32 = 0, kF16 = 1, kFP8 = 2 };
+
+constexpr float kLog2eHost = 1.4426950408889634f;
+
+// How a work row (one query token) finds its keys.
+enum RowMode : int32_t {
+    kRowDecode = 0,   // row r = sequence r of a batch; keys [L - W, L) of seq_lengths[r]
+    kRowPrefill = 1,  // row r = query position q_offset + r of one sequence (causal / fixed window)
+    kRowRagged = 2,   // row r described by row_info[r] = {bt_row, k_lo, k_hi, out_row}
+};
+
+struct AttnParams {
+    const void *q;             // [rows][H][d] (f32 for f32 caches, f16 otherwise)
+    void *out;                 // [rows][H][d] same type as q
+    const void *k_pool;        // [nb][bs][Hkv][d]
+    const void *v_pool;
+    const uint16_t *k_scale;   // fp8 only: half per physical block
+    const uint16_t *v_scale;
+    const int32_t *block_tables;   // [bt_rows][bt_stride]
+    const uint32_t *seq_lengths;   // decode mode
+    const int4 *row_info;          // ragged mode
+    float *part_o;             // [rows][H][max_parts][d] split-context partial outputs
+    float *part_ml;            // [rows][H][max_parts][2] (max in log2 units, sum)
+    int32_t rows;
+    int32_t bt_stride;
+    int32_t max_num_blocks;    // decode: logical blocks readable per row
+    int32_t num_heads, num_kv_heads, head_dim, block_size, window;
+    int32_t q_offset, causal, mode;
+    int32_t part_tokens;       // tokens per split-context partition (multiple of 16)
+    int32_t max_parts;
+    int32_t heads_per_wave;    // VALU kernel: query heads handled by one wave
+    float scale_log2;          // log2(e) / sqrt(d)
+};
+
+// Paged attention over rows (decode / prefill-as-rows / ragged).  Chooses the
+// MFMA kernel for 4 <= H/Hkv <= 16 with f16/fp8 KV and d in {64,128,256},
+// otherwise the VALU kernel.  Launches the split-context reduce when max_parts > 1.
+hipError_t launch_attention(const AttnParams &p, int32_t dtype, bool use_mfma, hipStream_t stream,
+                            hipEvent_t after_main = nullptr);
+bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group);
+
+// KV append into the paged pools.
+struct AppendParams {
+    const void *keys;          // [n][Hkv][d] (f32 for f32 caches, f16 for f16 and fp8)
+    const void *values;
+    void *k_pool;
+    void *v_pool;
+    uint16_t *k_scale;         // fp8: per-block half scales (read-modify-write)
+    uint16_t *v_scale;
+    const int32_t *block_table;   // one sequence's table (token_offset mode)
+    const int64_t *slot_mapping;  // optional: explicit slot per token (overrides the table)
+    int32_t token_offset;
+    int32_t num_tokens;
+    int32_t num_kv_heads, head_dim, block_size;
+};
+hipError_t launch_append(const AppendParams &p, int32_t dtype, hipStream_t stream);
+
+// Batched append for a mixed step.  f32/f16: token t goes to position
+// token_pos[t].y of sequence token_pos[t].x through that sequence's block-table
+// row.  fp8: one workgroup per work entry (sequence, logical block); the
+// sequence's tokens are keys[cu_tokens[s] .. cu_tokens[s+1]) at positions
+// token_offsets[s] + i.
+struct AppendBatchParams {
+    const void *keys;
+    const void *values;
+    void *k_pool;
+    void *v_pool;
+    uint16_t *k_scale;
+    uint16_t *v_scale;
+    const int32_t *block_tables;  // [seqs][bt_stride]
+    const int32_t *cu_tokens;     // [seqs + 1] prefix sums of tokens per sequence
+    const int32_t *token_offsets; // [seqs]
+    const int4 *work;             // fp8: one entry per touched block {seq, logical block, 0, 0}
+    int32_t num_work;
+    const int2 *token_pos;        // f32/f16: per input token {sequence, position}
+    int32_t seqs, bt_stride, total_tokens;
+    int32_t num_kv_heads, head_dim, block_size;
+};
+hipError_t launch_append_batch(const AppendBatchParams &p, int32_t dtype, hipStream_t stream);
+
+// Exhaustive codec entry points (used by the codec tests through the C ABI).
+hipError_t launch_fp8_quantize(const uint16_t *values, const uint16_t *scales, uint8_t *out, int64_t n,
+                               hipStream_t stream);
+hipError_t launch_fp8_dequant(const uint8_t *codes, const uint16_t *scales, uint16_t *out, int64_t n,
+                              hipStream_t stream);
+
+// Dense chunked-prefill (MFMA, f16): rows [q_offset, q_offset + T) of one sequence.
+hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream);
+bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group);
+
+}  // namespace pam

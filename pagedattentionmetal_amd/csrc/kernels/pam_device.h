@@ -1,0 +1,88 @@
+// pam_device.h - device-side helpers shared by the gfx950 kernels.
+//
+// Vector types for MFMA operands, the e4m3 KV codec (bit-exact with the
+// reference's kernels.metal:553-601 quantize_fp8 / dequant_fp8) and wave64
+// shuffles.  Compiled only for gfx950.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pam {
+
+typedef _Float16 f16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ f16 bits_to_f16(uint16_t b) { return __builtin_bit_cast(f16, b); }
+__device__ __forceinline__ uint16_t f16_to_bits(f16 h) { return __builtin_bit_cast(uint16_t, h); }
+
+// ---------------------------------------------------------------- e4m3 codec
+// dequant_fp8 (kernels.metal:553-562) evaluated in half, left to right:
+//   e == 0: (+-scale * (m/8)) * 2^-6 ;  else (+-scale * (1 + m/8)) * 2^(e-7).
+// Both products are single IEEE binary16 multiplies (round to nearest even),
+// matching the reference's half arithmetic bit for bit.
+__device__ __forceinline__ f16 fp8_dequant(uint32_t code, f16 scale) {
+    const uint32_t e = (code >> 3) & 0xFu, m = code & 7u;
+    if ((code & 0x7Fu) == 0u) return (f16)0.0f;
+    f16 s = (code & 0x80u) ? -scale : scale;
+    // mantissa factor as an exact half: 1 + m/8 (bits 0x3C00 | m<<7) or m/8
+    f16 mx = e ? bits_to_f16((uint16_t)(0x3C00u | (m << 7))) : (f16)((float)m * 0.125f);
+    // power of two 2^(max(e,1)-7): half exponent field max(e,1) + 8
+    f16 p2 = bits_to_f16((uint16_t)(((e ? e : 1u) + 8u) << 10));
+    f16 t = s * mx;
+    return t * p2;
+}
+
+// quantize_fp8 (kernels.metal:564-601): value/scale in float (IEEE division),
+// clamp to +-448, subnormal codes below 2^-6 from round(v*512) clamped to 7,
+// otherwise a 3-bit mantissa rounded half away from zero; saturates at 0x7E.
+__device__ __forceinline__ uint32_t fp8_quantize(f16 value, f16 scale) {
+    float v = (float)value / (float)scale;
+    v = fminf(fmaxf(v, -448.0f), 448.0f);
+    const uint32_t sign = v < 0.0f ? 0x80u : 0u;
+    v = fabsf(v);
+    if (v == 0.0f) return 0u;
+    if (v < 0x1p-6f) {
+        int mi = (int)roundf(v * 512.0f);
+        mi = mi > 7 ? 7 : (mi < 0 ? 0 : mi);
+        return sign | (uint32_t)mi;
+    }
+    int ex;
+    float mant = frexpf(v, &ex);
+    mant *= 2.0f;
+    ex -= 1;
+    if (ex > 8) return sign | 0x7Eu;
+    int eb = ex + 7;
+    int mi = (int)roundf((mant - 1.0f) * 8.0f);
+    if (mi > 7) {
+        mi = 0;
+        eb++;
+    }
+    if (eb > 0xF) return sign | 0x7Eu;
+    if (eb == 0xF && mi > 6) mi = 6;
+    return sign | ((uint32_t)eb << 3) | (uint32_t)mi;
+}
+
+// per-block scale rule (kernels.metal:1944-1957)
+__device__ __forceinline__ f16 fp8_scale_rule(float new_max_abs, f16 old_scale) {
+    float mk = fmaxf(new_max_abs, (float)old_scale * 448.0f);
+    return mk > 0.0f ? (f16)(mk / 448.0f) : (f16)1.0f;
+}
+
+// ---------------------------------------------------------------- wave64 shuffles
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+__device__ __forceinline__ float wave_max_xor(float v, int lo, int hi) {
+    for (int m = lo; m < hi; m <<= 1) v = fmaxf(v, shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ float wave_sum_xor(float v, int lo, int hi) {
+    for (int m = lo; m < hi; m <<= 1) v += shfl_xor(v, m);
+    return v;
+}
+
+}  // namespace pam

@@ -1,0 +1,604 @@
+// engine.cpp - PagedAttentionEngine on HIP: validation, kernel choice, launch,
+// retry / circuit breaker, graceful degradation and stats.
+//
+// Reference: Sources/PagedAttentionMetal/PagedAttentionEngine.swift
+//   prefill / decode / appendToCache entry points  :405-418, :533-546, :585-597
+//   withRetry (3 attempts, 10 ms * 2^k backoff, breaker at 2*maxRetries)  :375-400
+//   validatePrefill / validateDecode / validateAppend  :1897-1950
+//   PagedLayerSpec.validate  PagedAttentionTypes.swift:126-142
+#include <unistd.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+
+#include "runtime.h"
+
+namespace pam {
+
+void hip_check(hipError_t e, const char *what) {
+    if (e != hipSuccess)
+        throw ExecutionError(std::string("GPU command execution failed: ") + what + ": " + hipGetErrorString(e));
+}
+
+// ------------------------------------------------------------------ helpers
+
+static int32_t elem_bytes(int32_t dtype) { return dtype == kF32 ? 4 : (dtype == kF16 ? 2 : 1); }
+static int32_t io_bytes(int32_t dtype) { return dtype == kF32 ? 4 : 2; }  // Q / O / new K,V element
+
+static void validate_layer(const pam_layer_spec &l) {
+    if (l.head_dim <= 0) throw invalid_configuration("headDim must be positive.");
+    if (l.num_heads <= 0) throw invalid_configuration("numHeads must be positive.");
+    if (l.num_kv_heads <= 0) throw invalid_configuration("numKVHeads must be positive.");
+    if (l.num_heads % l.num_kv_heads != 0)
+        throw invalid_configuration("numHeads must be divisible by numKVHeads for GQA/MQA mapping.");
+    if (l.block_size <= 0) throw invalid_configuration("blockSize must be positive.");
+    if (l.data_type < 0 || l.data_type > 2) throw invalid_configuration("unknown dtype");
+    if (l.window_size < 0) throw invalid_configuration("windowSize must be non-negative.");
+    // kernel envelope: 4-element slices per lane, at most 64 lanes per token row
+    if (l.head_dim % 4 != 0 || l.head_dim > 256)
+        throw PamError("Unsupported paged attention path: headDim must be a multiple of 4 and at most 256.");
+}
+
+static void require(size_t actual, const char *name, int64_t expected) {
+    if (actual != 0 && (int64_t)actual < expected) throw buffer_too_small(name, expected, (int64_t)actual);
+}
+
+static int64_t q_bytes_per_token(const pam_layer_spec &l) { return (int64_t)l.num_heads * l.head_dim * io_bytes(l.data_type); }
+static int64_t kv_bytes_per_token(const pam_layer_spec &l) {
+    return (int64_t)l.num_kv_heads * l.head_dim * elem_bytes(l.data_type);
+}
+static int64_t pool_bytes_for(int64_t blocks, const pam_layer_spec &l) { return blocks * l.block_size * kv_bytes_per_token(l); }
+static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------------------------ context
+
+Context::Context() {}
+
+Context::~Context() {
+    if (!device_ready_) return;
+    (void)hipSetDevice(device_);
+    if (own_stream_) (void)hipStreamSynchronize(own_stream_);
+    if (workspace_.ptr) (void)hipFree(workspace_.ptr);
+    for (auto &s : scratch_)
+        if (s.ptr) (void)hipFree(s.ptr);
+    if (pinned_) (void)hipHostFree(pinned_);
+    if (ev0_) (void)hipEventDestroy(ev0_);
+    if (ev1_) (void)hipEventDestroy(ev1_);
+    if (evmid_) (void)hipEventDestroy(evmid_);
+    if (staged_) (void)hipEventDestroy(staged_);
+    if (own_stream_) (void)hipStreamDestroy(own_stream_);
+}
+
+void Context::ensure_device() {
+    if (device_ready_) return;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) throw PamError("GPU device or stream could not be initialized.");
+    hip_check(hipGetDevice(&device_), "hipGetDevice");
+    hip_check(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking), "hipStreamCreate");
+    hip_check(hipEventCreate(&ev0_), "hipEventCreate");
+    hip_check(hipEventCreate(&ev1_), "hipEventCreate");
+    hip_check(hipEventCreate(&evmid_), "hipEventCreate");
+    hip_check(hipEventCreateWithFlags(&staged_, hipEventDisableTiming), "hipEventCreate");
+    device_ready_ = true;
+}
+
+hipStream_t Context::stream() { return ext_stream_ ? ext_stream_ : own_stream_; }
+
+void Context::finish(const char *what) {
+    hip_check(hipGetLastError(), what);
+    if (synchronous) hip_check(hipStreamSynchronize(stream()), what);
+}
+
+void Context::reserve_workspace(size_t bytes) {
+    ensure_device();
+    if (bytes <= workspace_.bytes) return;
+    hip_check(hipStreamSynchronize(stream()), "workspace resize");
+    if (workspace_.ptr) (void)hip_check(hipFree(workspace_.ptr), "hipFree");
+    workspace_.ptr = nullptr;
+    workspace_.bytes = 0;
+    hip_check(hipMalloc(&workspace_.ptr, bytes), "hipMalloc workspace");
+    workspace_.bytes = bytes;
+}
+
+void *Context::device_scratch(int slot, size_t bytes) {
+    DeviceBuffer &b = scratch_[slot];
+    if (bytes > b.bytes) {
+        hip_check(hipStreamSynchronize(stream()), "scratch resize");
+        if (b.ptr) hip_check(hipFree(b.ptr), "hipFree");
+        b.ptr = nullptr;
+        b.bytes = 0;
+        size_t want = std::max<size_t>(bytes, 4096);
+        hip_check(hipMalloc(&b.ptr, want), "hipMalloc scratch");
+        b.bytes = want;
+    }
+    return b.ptr;
+}
+
+// Host bytes -> pinned staging -> device memory, ordered on the stream.  The
+// pinned arena is reused once the copies staged from it have completed.
+void *Context::stage_into(void *dst, const void *host, size_t bytes) {
+    if (bytes == 0) return dst;
+    const size_t need = (bytes + 255) & ~(size_t)255;
+    if (pinned_used_ + need > pinned_bytes_) {
+        hip_check(hipEventSynchronize(staged_), "staging wait");
+        pinned_used_ = 0;
+        if (need > pinned_bytes_) {
+            if (pinned_) hip_check(hipHostFree(pinned_), "hipHostFree");
+            pinned_ = nullptr;
+            pinned_bytes_ = 0;
+            size_t want = std::max<size_t>(need, 1 << 20);
+            hip_check(hipHostMalloc(&pinned_, want, hipHostMallocDefault), "hipHostMalloc");
+            pinned_bytes_ = want;
+        }
+    }
+    char *src = static_cast<char *>(pinned_) + pinned_used_;
+    std::memcpy(src, host, bytes);
+    pinned_used_ += need;
+    hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream()), "hipMemcpyAsync staging");
+    hip_check(hipEventRecord(staged_, stream()), "hipEventRecord");
+    return dst;
+}
+
+void *Context::stage(int slot, const void *host, size_t bytes) {
+    return stage_into(device_scratch(slot, bytes), host, bytes);
+}
+
+template <class F>
+void Context::with_retry(const char *op, F &&fn) {
+    std::string last = std::string("operation '") + op + "' failed";
+    for (int32_t attempt = 0; attempt < max_retries; attempt++) {
+        try {
+            fn();
+            consecutive_failures = 0;
+            return;
+        } catch (const ExecutionError &) {
+            // work that reached the GPU and failed there is not replayed
+            consecutive_failures += 1;
+            throw;
+        } catch (const PamError &e) {
+            last = e.what();
+            consecutive_failures += 1;
+            if (consecutive_failures >= max_retries * 2)
+                throw PamError(std::string("Recurring failure in '") + op + "' after " +
+                               std::to_string(consecutive_failures) + " attempts - circuit breaker engaged.");
+            if (attempt > 0) usleep((useconds_t)(10000u << attempt));
+        }
+    }
+    throw PamError(last);
+}
+
+void Context::check_launch(hipError_t e, const char *what) {
+    if (fail_next_launches > 0) {
+        fail_next_launches--;
+        throw PamError(std::string("GPU command encoding failed: injected launch failure in ") + what);
+    }
+    if (e != hipSuccess) throw PamError(std::string("GPU command encoding failed: ") + what + ": " + hipGetErrorString(e));
+}
+
+void Context::zero_output(void *ptr, size_t bytes) {
+    if (ptr == nullptr || bytes == 0) return;
+    (void)hipMemsetAsync(ptr, 0, bytes, stream());
+    (void)hipStreamSynchronize(stream());
+}
+
+void Context::record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t blocks, int64_t tmp, bool split,
+                           bool has_mid) {
+    last_stats.operation = op;
+    last_stats.batch_size = batch;
+    last_stats.sequence_length = seq_len;
+    last_stats.num_blocks = blocks;
+    last_stats.temporary_bytes = tmp;
+    last_stats.used_split_pass = split ? 1 : 0;
+    last_stats.elapsed_ms = last_stats.kernel_ms = last_stats.reduce_ms = -1.0;
+    stats_pending_ = true;
+    stats_has_mid_ = has_mid;
+    if (synchronous) stats();
+}
+
+pam_stats Context::stats() {
+    if (stats_pending_ && device_ready_) {
+        stats_pending_ = false;
+        if (hipEventSynchronize(ev1_) == hipSuccess) {
+            float ms = -1.0f;
+            if (hipEventElapsedTime(&ms, ev0_, ev1_) == hipSuccess) last_stats.elapsed_ms = ms;
+            if (stats_has_mid_) {
+                float a = -1.0f, b = -1.0f;
+                if (hipEventElapsedTime(&a, ev0_, evmid_) == hipSuccess) last_stats.kernel_ms = a;
+                if (hipEventElapsedTime(&b, evmid_, ev1_) == hipSuccess) last_stats.reduce_ms = b;
+            } else {
+                last_stats.kernel_ms = last_stats.elapsed_ms;
+                last_stats.reduce_ms = 0.0;
+            }
+        }
+    }
+    return last_stats;
+}
+
+// Tokens per split-context partition.  Partitions are 16-token tiles; the grid
+// should hold a few thousand waves so all 256 CUs stay busy and ragged rows do
+// not leave a long tail.
+int32_t Context::choose_part_tokens(int64_t waves_per_part, int64_t max_tiles) {
+    if (max_tiles <= 0) return 16;
+    if (part_tokens_override > 0) return std::max<int32_t>(16, part_tokens_override / 16 * 16);
+    if (waves_per_part >= 8192) return (int32_t)(max_tiles * 16);  // enough rows: one partition per row
+    int64_t tpp = 16;
+    while (tpp > 4 && waves_per_part * ceil_div(max_tiles, tpp) < 4096) tpp /= 2;
+    if (tpp >= max_tiles) tpp = max_tiles;
+    return (int32_t)(tpp * 16);
+}
+
+static int32_t heads_per_wave(int32_t group) {
+    for (int32_t nh : {8, 4, 2})
+        if (group % nh == 0) return nh;
+    return 1;
+}
+
+// ------------------------------------------------------------------ decode
+
+void Context::decode(const pam_decode_request &r) {
+    validate_layer(r.layer);
+    // validateDecode (PagedAttentionEngine.swift:1916-1934)
+    if (r.batch_size <= 0) throw invalid_configuration("batchSize must be positive.");
+    if (r.max_num_blocks <= 0) throw invalid_configuration("maxNumBlocks must be positive.");
+    if (r.block_tables_bytes != 0 &&
+        (int64_t)r.max_num_blocks > (int64_t)(r.block_tables_bytes / ((size_t)r.batch_size * 4)))
+        throw invalid_configuration("maxNumBlocks exceeds blockTables buffer capacity");
+    const pam_layer_spec &l = r.layer;
+    require(r.q_bytes, "Q", r.batch_size * q_bytes_per_token(l));
+    require(r.block_tables_bytes, "blockTables", (int64_t)r.batch_size * r.max_num_blocks * 4);
+    require(r.seq_lengths_bytes, "seqLengths", (int64_t)r.batch_size * 4);
+    require(r.output_bytes, "output", r.batch_size * q_bytes_per_token(l));
+    require(r.k_pool_bytes, "K pool", pool_bytes_for(r.max_num_blocks, l));
+    require(r.v_pool_bytes, "V pool", pool_bytes_for(r.max_num_blocks, l));
+    if (l.data_type == kFP8 && (r.k_scale == nullptr || r.v_scale == nullptr))
+        throw invalid_configuration("FP8 decode needs the K and V scale pools.");
+    if (!r.q || !r.k_pool || !r.v_pool || !r.block_tables || !r.seq_lengths || !r.output)
+        throw invalid_configuration("decode request has a null buffer.");
+    ensure_device();
+    if (graceful_degradation) {
+        try {
+            decode_gpu(r);
+        } catch (const PamError &e) {
+            std::fprintf(stderr, "[pam] decode failed: %s\n", e.what());
+            zero_output(r.output, (size_t)(r.batch_size * q_bytes_per_token(l)));
+        }
+    } else {
+        decode_gpu(r);
+    }
+}
+
+void Context::decode_gpu(const pam_decode_request &r) {
+    const pam_layer_spec &l = r.layer;
+    const int32_t G = l.num_heads / l.num_kv_heads;
+    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && G >= 4;
+    if (decode_kernel_choice == 1) use_mfma = false;
+    if (decode_kernel_choice == 2) use_mfma = mfma_supported(l.data_type, l.head_dim, G);
+    const int32_t nh = heads_per_wave(G);
+
+    AttnParams p{};
+    p.q = r.q;
+    p.out = r.output;
+    p.k_pool = r.k_pool;
+    p.v_pool = r.v_pool;
+    p.k_scale = r.k_scale;
+    p.v_scale = r.v_scale;
+    p.block_tables = r.block_tables;
+    p.seq_lengths = r.seq_lengths;
+    p.rows = r.batch_size;
+    p.bt_stride = r.max_num_blocks;
+    p.max_num_blocks = r.max_num_blocks;
+    p.num_heads = l.num_heads;
+    p.num_kv_heads = l.num_kv_heads;
+    p.head_dim = l.head_dim;
+    p.block_size = l.block_size;
+    p.window = l.window_size;
+    p.mode = kRowDecode;
+    p.heads_per_wave = nh;
+    p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
+
+    const int64_t cap_tokens = (int64_t)r.max_num_blocks * l.block_size;
+    int64_t max_tiles = ceil_div(cap_tokens, 16);
+    if (l.window_size > 0) max_tiles = std::min<int64_t>(max_tiles, l.window_size / 16 + 2);
+    const int64_t waves = (int64_t)r.batch_size * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
+    p.part_tokens = choose_part_tokens(waves, max_tiles);
+    p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles, p.part_tokens / 16));
+    int64_t tmp = 0;
+    if (p.max_parts > 1) {
+        const int64_t slots = (int64_t)r.batch_size * l.num_heads * p.max_parts;
+        tmp = slots * ((int64_t)l.head_dim + 2) * 4;
+        reserve_workspace((size_t)tmp);
+        p.part_o = static_cast<float *>(workspace_.ptr);
+        p.part_ml = p.part_o + slots * l.head_dim;
+    }
+    with_retry("decodeFlat", [&] {
+        (void)hipEventRecord(ev0_, stream());
+        check_launch(launch_attention(p, l.data_type, use_mfma, stream(), evmid_), "decode");
+        (void)hipEventRecord(ev1_, stream());
+        finish("decode");
+    });
+    record_stats(PAM_OP_DECODE, r.batch_size, 0, r.max_num_blocks, tmp, p.max_parts > 1, true);
+}
+
+// ------------------------------------------------------------------ prefill
+
+void Context::prefill(const pam_prefill_request &r) {
+    validate_layer(r.layer);
+    // validatePrefill (PagedAttentionEngine.swift:1897-1914)
+    if (r.seq_len <= 0) throw invalid_configuration("seqLen must be positive.");
+    if (r.q_offset < 0) throw invalid_configuration("qOffset must be non-negative.");
+    const pam_layer_spec &l = r.layer;
+    const int64_t kv_len = (int64_t)r.q_offset + r.seq_len;
+    const int64_t nb = ceil_div(kv_len, l.block_size);
+    require(r.q_bytes, "Q", r.seq_len * q_bytes_per_token(l));
+    require(r.block_table_bytes, "blockTable", nb * 4);
+    require(r.output_bytes, "output", r.seq_len * q_bytes_per_token(l));
+    require(r.k_pool_bytes, "K pool", pool_bytes_for(nb, l));
+    require(r.v_pool_bytes, "V pool", pool_bytes_for(nb, l));
+    if (l.data_type == kFP8 && (r.k_scale == nullptr || r.v_scale == nullptr))
+        throw invalid_configuration("FP8 prefill needs the K and V scale pools.");
+    if (!r.q || !r.k_pool || !r.v_pool || !r.block_table || !r.output)
+        throw invalid_configuration("prefill request has a null buffer.");
+    ensure_device();
+    if (graceful_degradation) {
+        try {
+            prefill_gpu(r);
+        } catch (const PamError &e) {
+            std::fprintf(stderr, "[pam] prefill failed: %s\n", e.what());
+            zero_output(r.output, (size_t)(r.seq_len * q_bytes_per_token(l)));
+        }
+    } else {
+        prefill_gpu(r);
+    }
+}
+
+void Context::prefill_gpu(const pam_prefill_request &r) {
+    const pam_layer_spec &l = r.layer;
+    const int32_t G = l.num_heads / l.num_kv_heads;
+    AttnParams p{};
+    p.q = r.q;
+    p.out = r.output;
+    p.k_pool = r.k_pool;
+    p.v_pool = r.v_pool;
+    p.k_scale = r.k_scale;
+    p.v_scale = r.v_scale;
+    p.block_tables = r.block_table;
+    p.rows = r.seq_len;
+    p.num_heads = l.num_heads;
+    p.num_kv_heads = l.num_kv_heads;
+    p.head_dim = l.head_dim;
+    p.block_size = l.block_size;
+    p.window = l.window_size;
+    p.q_offset = r.q_offset;
+    p.causal = r.causal ? 1 : 0;
+    p.mode = kRowPrefill;
+    p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
+
+    const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G) && decode_kernel_choice != 1;
+    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && decode_kernel_choice != 1;
+    const int32_t nh = heads_per_wave(G);
+    p.heads_per_wave = nh;
+    const int64_t kv_len = (int64_t)r.q_offset + r.seq_len;
+    const int64_t max_tiles = ceil_div(kv_len, 16) + 1;
+    int64_t tmp = 0;
+    if (dense) {
+        p.part_tokens = (int32_t)(max_tiles * 16);
+        p.max_parts = 1;
+    } else {
+        const int64_t waves = (int64_t)r.seq_len * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
+        p.part_tokens = choose_part_tokens(waves, max_tiles);
+        p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles, p.part_tokens / 16));
+        if (p.max_parts > 1) {
+            const int64_t slots = (int64_t)r.seq_len * l.num_heads * p.max_parts;
+            tmp = slots * ((int64_t)l.head_dim + 2) * 4;
+            reserve_workspace((size_t)tmp);
+            p.part_o = static_cast<float *>(workspace_.ptr);
+            p.part_ml = p.part_o + slots * l.head_dim;
+        }
+    }
+    with_retry("prefill", [&] {
+        (void)hipEventRecord(ev0_, stream());
+        if (dense)
+            check_launch(launch_prefill_mfma(p, stream()), "prefill");
+        else
+            check_launch(launch_attention(p, l.data_type, use_mfma, stream(), evmid_), "prefill");
+        (void)hipEventRecord(ev1_, stream());
+        finish("prefill");
+    });
+    const int32_t op = (dense || use_mfma) ? PAM_OP_PREFILL_MMA : PAM_OP_PREFILL_TILED_PASS;
+    record_stats(op, 1, r.seq_len, (int32_t)ceil_div(kv_len, l.block_size), tmp, p.max_parts > 1, !dense);
+}
+
+// ------------------------------------------------------------------ append
+
+void Context::append(const pam_append_request &r) {
+    validate_layer(r.layer);
+    // validateAppend (PagedAttentionEngine.swift:1936-1950)
+    if (r.token_offset < 0) throw invalid_configuration("tokenOffset must be non-negative.");
+    if (r.num_new_tokens <= 0) throw invalid_configuration("numNewTokens must be positive.");
+    const pam_layer_spec &l = r.layer;
+    const int64_t final_len = (int64_t)r.token_offset + r.num_new_tokens;
+    const int64_t nb = ceil_div(final_len, l.block_size);
+    const int64_t in_row = (int64_t)l.num_kv_heads * l.head_dim * io_bytes(l.data_type);
+    require(r.keys_bytes, "new keys", r.num_new_tokens * in_row);
+    require(r.values_bytes, "new values", r.num_new_tokens * in_row);
+    if (!r.slot_mapping) require(r.block_table_bytes, "blockTable", nb * 4);
+    require(r.k_pool_bytes, "K pool", pool_bytes_for(nb, l));
+    require(r.v_pool_bytes, "V pool", pool_bytes_for(nb, l));
+    if (l.data_type == kFP8 && (r.k_scale == nullptr || r.v_scale == nullptr))
+        throw invalid_configuration("FP8 append needs the K and V scale pools.");
+    if (l.data_type == kFP8 && r.slot_mapping)
+        throw PamError("Unsupported paged attention path: FP8 append takes a block table, not a slot mapping.");
+    if (!r.keys || !r.values || !r.k_pool || !r.v_pool || (!r.block_table && !r.slot_mapping))
+        throw invalid_configuration("append request has a null buffer.");
+    ensure_device();
+    if (graceful_degradation) {
+        try {
+            append_gpu(r);
+        } catch (const PamError &e) {
+            std::fprintf(stderr, "[pam] appendToCache failed: %s\n", e.what());
+        }
+    } else {
+        append_gpu(r);
+    }
+}
+
+void Context::append_gpu(const pam_append_request &r) {
+    const pam_layer_spec &l = r.layer;
+    AppendParams p{};
+    p.keys = r.keys;
+    p.values = r.values;
+    p.k_pool = r.k_pool;
+    p.v_pool = r.v_pool;
+    p.k_scale = r.k_scale;
+    p.v_scale = r.v_scale;
+    p.block_table = r.block_table;
+    p.slot_mapping = r.slot_mapping;
+    p.token_offset = r.token_offset;
+    p.num_tokens = r.num_new_tokens;
+    p.num_kv_heads = l.num_kv_heads;
+    p.head_dim = l.head_dim;
+    p.block_size = l.block_size;
+    with_retry(l.data_type == kFP8 ? "appendToCacheCheckedFP8" : "appendToCacheFlat", [&] {
+        (void)hipEventRecord(ev0_, stream());
+        check_launch(launch_append(p, l.data_type, stream()), "append");
+        (void)hipEventRecord(ev1_, stream());
+        finish("append");
+    });
+    record_stats(PAM_OP_APPEND, 1, r.num_new_tokens, 0, 0, false, false);
+}
+
+// ------------------------------------------------------------------ mixed step
+
+void Context::mixed_step(const pam_mixed_request &r) {
+    const pam_layer_spec &l = r.layer;
+    validate_layer(l);
+    if (r.num_seqs <= 0) throw invalid_configuration("numSeqs must be positive.");
+    if (!r.context_lens || !r.query_lens) throw invalid_configuration("mixed step needs host context/query lengths.");
+    if (!r.q || !r.output || !r.k_pool || !r.v_pool || !r.block_tables)
+        throw invalid_configuration("mixed step request has a null buffer.");
+    if (l.data_type == kFP8 && (!r.k_scale || !r.v_scale))
+        throw invalid_configuration("FP8 mixed step needs the K and V scale pools.");
+    ensure_device();
+    const int32_t bs = l.block_size, W = l.window_size;
+    std::vector<int4> rows;
+    std::vector<int32_t> cu(r.num_seqs + 1, 0);
+    int64_t max_tiles = 1;
+    for (int32_t s = 0; s < r.num_seqs; s++) {
+        const int64_t c = r.context_lens[s], T = r.query_lens[s];
+        if (c < 0 || T < 0) throw invalid_configuration("negative context or query length");
+        const int64_t kv_len = c + T;
+        if (ceil_div(kv_len, bs) > r.bt_stride) throw buffer_too_small("blockTables row", ceil_div(kv_len, bs) * 4, (int64_t)r.bt_stride * 4);
+        const int64_t ws = W > 0 ? std::max<int64_t>(0, kv_len - W) : 0;
+        for (int64_t i = 0; i < T; i++) {
+            int4 ri;
+            ri.x = s;
+            ri.y = (int32_t)ws;
+            ri.z = (int32_t)(c + i + 1);
+            ri.w = (int32_t)rows.size();
+            rows.push_back(ri);
+        }
+        max_tiles = std::max<int64_t>(max_tiles, ceil_div(kv_len, 16) - ws / 16);
+        cu[s + 1] = cu[s] + (int32_t)T;
+    }
+    const int32_t total = (int32_t)rows.size();
+    if (total == 0) return;
+    const int32_t G = l.num_heads / l.num_kv_heads;
+    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && G >= 4;
+    if (decode_kernel_choice == 1) use_mfma = false;
+    const int32_t nh = heads_per_wave(G);
+
+    // device-side descriptors
+    const int4 *d_rows = static_cast<const int4 *>(stage(0, rows.data(), rows.size() * sizeof(int4)));
+    AppendBatchParams ab{};
+    std::vector<int2> tok;
+    std::vector<int4> work;
+    if (r.new_keys && r.new_values) {
+        ab.keys = r.new_keys;
+        ab.values = r.new_values;
+        ab.k_pool = r.k_pool;
+        ab.v_pool = r.v_pool;
+        ab.k_scale = r.k_scale;
+        ab.v_scale = r.v_scale;
+        ab.block_tables = r.block_tables;
+        ab.bt_stride = r.bt_stride;
+        ab.seqs = r.num_seqs;
+        ab.total_tokens = total;
+        ab.num_kv_heads = l.num_kv_heads;
+        ab.head_dim = l.head_dim;
+        ab.block_size = bs;
+        ab.cu_tokens = static_cast<const int32_t *>(stage(1, cu.data(), cu.size() * 4));
+        ab.token_offsets = static_cast<const int32_t *>(stage(2, r.context_lens, (size_t)r.num_seqs * 4));
+        if (l.data_type == kFP8) {
+            for (int32_t s = 0; s < r.num_seqs; s++) {
+                const int64_t c = r.context_lens[s], T = r.query_lens[s];
+                if (T <= 0) continue;
+                for (int64_t lb = c / bs; lb <= (c + T - 1) / bs; lb++) work.push_back(make_int4(s, (int)lb, 0, 0));
+            }
+            ab.work = static_cast<const int4 *>(stage(3, work.data(), work.size() * sizeof(int4)));
+            ab.num_work = (int32_t)work.size();
+        } else {
+            // per-token (sequence, position); the kernel resolves slots from the device table
+            for (int32_t s = 0; s < r.num_seqs; s++)
+                for (int64_t i = 0; i < r.query_lens[s]; i++) tok.push_back(make_int2(s, (int)(r.context_lens[s] + i)));
+            ab.token_pos = static_cast<const int2 *>(stage(3, tok.data(), tok.size() * sizeof(int2)));
+        }
+    }
+
+    AttnParams p{};
+    p.q = r.q;
+    p.out = r.output;
+    p.k_pool = r.k_pool;
+    p.v_pool = r.v_pool;
+    p.k_scale = r.k_scale;
+    p.v_scale = r.v_scale;
+    p.block_tables = r.block_tables;
+    p.row_info = d_rows;
+    p.rows = total;
+    p.bt_stride = r.bt_stride;
+    p.max_num_blocks = r.bt_stride;
+    p.num_heads = l.num_heads;
+    p.num_kv_heads = l.num_kv_heads;
+    p.head_dim = l.head_dim;
+    p.block_size = bs;
+    p.window = W;
+    p.mode = kRowRagged;
+    p.heads_per_wave = nh;
+    p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
+    const int64_t waves = (int64_t)total * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
+    p.part_tokens = choose_part_tokens(waves, max_tiles + 1);
+    p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles + 1, p.part_tokens / 16));
+    int64_t tmp = 0;
+    if (p.max_parts > 1) {
+        const int64_t slots = (int64_t)total * l.num_heads * p.max_parts;
+        tmp = slots * ((int64_t)l.head_dim + 2) * 4;
+        reserve_workspace((size_t)tmp);
+        p.part_o = static_cast<float *>(workspace_.ptr);
+        p.part_ml = p.part_o + slots * l.head_dim;
+    }
+    with_retry("mixedStep", [&] {
+        (void)hipEventRecord(ev0_, stream());
+        if (ab.keys) check_launch(launch_append_batch(ab, l.data_type, stream()), "mixed append");
+        check_launch(launch_attention(p, l.data_type, use_mfma, stream(), evmid_), "mixed attention");
+        (void)hipEventRecord(ev1_, stream());
+        finish("mixed step");
+    });
+    record_stats(PAM_OP_DECODE, r.num_seqs, total, r.bt_stride, tmp, p.max_parts > 1, true);
+}
+
+// ------------------------------------------------------------------ codec
+
+void Context::fp8_quantize(const uint16_t *v, const uint16_t *s, uint8_t *o, int64_t n) {
+    ensure_device();
+    check_launch(launch_fp8_quantize(v, s, o, n, stream()), "fp8 quantize");
+    finish("fp8 quantize");
+}
+
+void Context::fp8_dequant(const uint8_t *c, const uint16_t *s, uint16_t *o, int64_t n) {
+    ensure_device();
+    check_launch(launch_fp8_dequant(c, s, o, n, stream()), "fp8 dequant");
+    finish("fp8 dequant");
+}
+
+}  // namespace pam

@@ -1,0 +1,128 @@
+// runtime.h - host runtime of libpam: the engine context and the device KV cache.
+//
+// Context  ~ PagedAttentionEngine (Sources/PagedAttentionMetal/PagedAttentionEngine.swift):
+//            request validation (:1897-2006), kernel selection, launch on one HIP
+//            stream, retry with backoff + circuit breaker (:375-400), graceful
+//            degradation that zero-fills the output (:405-418, :533-546), lastStats.
+// KVCache  ~ KVCacheManager / BatchKVCacheManager (KVCacheManager.swift): a
+//            BlockAllocator plus K/V pools (and FP8 scale pools) resident in HBM.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../../include/pam.h"
+#include "../kernels/kernels.h"
+#include "block_allocator.h"
+
+namespace pam {
+
+void hip_check(hipError_t e, const char *what);
+
+// A growable device buffer owned by a context.
+struct DeviceBuffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+class Context;
+
+class KVCache {
+   public:
+    KVCache(Context *ctx, int32_t max_blocks, int32_t block_size, int32_t head_dim, int32_t num_kv_heads,
+            int32_t dtype, bool with_device);
+    ~KVCache();
+
+    std::mutex mu;
+    BlockAllocator alloc;
+    int32_t head_dim, num_kv_heads, dtype;
+    bool has_device;
+    int device = 0;
+    void *k_pool = nullptr, *v_pool = nullptr;
+    uint16_t *k_scale = nullptr, *v_scale = nullptr;
+    size_t pool_bytes = 0;
+
+    size_t bytes_per_block() const;  // one pool (K or V)
+    // perform copy-on-write block copies in HBM on the given stream
+    void copy_blocks(const BlockCopies &copies, hipStream_t stream);
+};
+
+class Context {
+   public:
+    Context();
+    ~Context();
+
+    std::mutex mu;
+    std::string last_error;
+    bool has_error = false;
+
+    void set_error(const std::string &m) {
+        last_error = m;
+        has_error = true;
+    }
+    void clear_error() {
+        last_error.clear();
+        has_error = false;
+    }
+
+    // --- device state (created on first GPU use)
+    void ensure_device();
+    hipStream_t stream();
+    void set_stream(hipStream_t s) { ext_stream_ = s; }
+    bool synchronous = true;
+    void finish(const char *what);  // synchronise when synchronous, surface GPU errors
+
+    // --- engine (PagedAttentionEngine)
+    void decode(const pam_decode_request &r);
+    void prefill(const pam_prefill_request &r);
+    void append(const pam_append_request &r);
+    void mixed_step(const pam_mixed_request &r);
+    void fp8_quantize(const uint16_t *v, const uint16_t *s, uint8_t *o, int64_t n);
+    void fp8_dequant(const uint8_t *c, const uint16_t *s, uint16_t *o, int64_t n);
+
+    pam_stats last_stats{};
+    pam_stats stats();  // last_stats with event timings resolved
+    bool graceful_degradation = true;
+    int32_t max_retries = 3;
+    int32_t consecutive_failures = 0;
+    int32_t fail_next_launches = 0;
+    int32_t part_tokens_override = 0;
+    int32_t decode_kernel_choice = 0;
+
+    // --- scratch
+    void reserve_workspace(size_t bytes);
+    // stage host bytes into a context-owned device region (slot selects one of
+    // several independent regions); returns the device pointer
+    void *stage(int slot, const void *host, size_t bytes);
+    void *stage_into(void *device_dst, const void *host, size_t bytes);
+    void *device_scratch(int slot, size_t bytes);
+
+   private:
+    template <class F>
+    void with_retry(const char *op, F &&fn);
+    void check_launch(hipError_t e, const char *what);
+    void zero_output(void *ptr, size_t bytes);
+    void decode_gpu(const pam_decode_request &r);
+    void prefill_gpu(const pam_prefill_request &r);
+    void append_gpu(const pam_append_request &r);
+    int32_t choose_part_tokens(int64_t waves_per_part, int64_t max_tiles);
+    void record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t blocks, int64_t tmp, bool split,
+                      bool has_mid);
+
+    bool device_ready_ = false;
+    int device_ = 0;
+    hipStream_t own_stream_ = nullptr, ext_stream_ = nullptr;
+    hipEvent_t ev0_ = nullptr, ev1_ = nullptr, evmid_ = nullptr, staged_ = nullptr;
+    bool stats_pending_ = false;
+    bool stats_has_mid_ = false;
+    DeviceBuffer workspace_;
+    DeviceBuffer scratch_[6];
+    void *pinned_ = nullptr;
+    size_t pinned_bytes_ = 0;
+    size_t pinned_used_ = 0;
+};
+
+}  // namespace pam

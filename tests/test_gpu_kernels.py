@@ -1,0 +1,315 @@
+"""GPU parity: libpam's HIP kernels against the CPU oracle (same seeded inputs).
+
+Bit-exact: FP8 codec, FP8 bytes and scales after append, f32/f16 append bytes.
+Tolerance (per output row, max|a-ref| / max|ref|): 1e-5 fp32, 2e-3 fp16 and
+FP8-KV (the oracle computes on the dequantised pool).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from helpers import TOL, make_case, row_rel_err, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def engine():
+    from pagedattentionmetal_amd import PagedAttentionEngine
+    e = PagedAttentionEngine()
+    e.set_graceful_degradation(False)
+    return e
+
+
+def layer(H, hkv, d, bs, dtype, window=0):
+    from pagedattentionmetal_amd import PagedLayerSpec
+    return PagedLayerSpec(d, H, hkv, bs, dtype, window)
+
+
+# ---------------------------------------------------------------- codec
+
+def test_fp8_quantize_exhaustive(engine):
+    import torch
+    rng = np.random.default_rng(7)
+    vals = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    vals = vals[(vals & 0x7C00) != 0x7C00]  # finite halves
+    scales = [1.0, 0.5, 2.0, 1 / 448, 0.0078125, 3.0, 65504 / 448]
+    scales += list(rng.uniform(1e-3, 10, 5))
+    for s in scales:
+        sh = np.full(vals.shape, np.float16(s)).view(np.uint16)
+        ref = oracle.quantize_fp8(vals.view(np.float16), sh.view(np.float16))
+        out = torch.empty(vals.size, dtype=torch.uint8, device="cuda")
+        engine.fp8_quantize(to_dev(vals.view(np.int16)), to_dev(sh.view(np.int16)), out)
+        got = to_host(out)
+        assert np.array_equal(got, ref), f"scale {s}: {np.count_nonzero(got != ref)} mismatches"
+
+
+def test_fp8_dequant_exhaustive(engine):
+    import torch
+    rng = np.random.default_rng(8)
+    codes = np.tile(np.arange(256, dtype=np.uint8), 4096)
+    sc = np.repeat(rng.uniform(0, 1, 4096).astype(np.float16), 256)
+    sc[:256 * 64] = np.repeat(np.arange(1, 65, dtype=np.uint16).view(np.float16), 256)  # subnormal scales
+    ref = oracle.dequant_fp8(codes, sc)
+    out = torch.empty(codes.size, dtype=torch.int16, device="cuda")
+    engine.fp8_dequant(to_dev(codes), to_dev(sc.view(np.int16)), out)
+    got = to_host(out).view(np.uint16)
+    assert np.array_equal(got, ref.view(np.uint16))
+
+
+# ---------------------------------------------------------------- append
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("bs,offset,n", [(16, 0, 37), (16, 5, 40), (4, 3, 9), (32, 31, 2)])
+def test_append_bit_exact(engine, dtype, bs, offset, n):
+    rng = np.random.default_rng(100 + bs + offset)
+    hkv, d = 2, 64
+    nb = 16
+    dt = np.float32 if dtype == 0 else np.float16
+    kp = rng.standard_normal((nb, bs, hkv, d)).astype(dt)
+    vp = rng.standard_normal((nb, bs, hkv, d)).astype(dt)
+    bt = rng.permutation(nb).astype(np.int32)
+    keys = rng.standard_normal((n, hkv, d)).astype(dt)
+    vals = rng.standard_normal((n, hkv, d)).astype(dt)
+    kd, vd = to_dev(kp), to_dev(vp)
+    engine.append_to_cache(to_dev(keys), to_dev(vals), kd, vd, to_dev(bt), offset, n, layer(hkv, hkv, d, bs, dtype))
+    oracle.append(dtype, keys, vals, kp, vp, bt, offset)
+    assert np.array_equal(to_host(kd).view(np.uint8), kp.view(np.uint8))
+    assert np.array_equal(to_host(vd).view(np.uint8), vp.view(np.uint8))
+
+
+def test_append_slot_mapping(engine):
+    rng = np.random.default_rng(5)
+    hkv, d, bs, nb, n = 8, 128, 16, 64, 50
+    kp = np.zeros((nb, bs, hkv, d), np.float16)
+    vp = np.zeros_like(kp)
+    slots = rng.choice(nb * bs, n, replace=False).astype(np.int64)
+    keys = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    vals = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    kd, vd = to_dev(kp), to_dev(vp)
+    engine.append_to_cache(to_dev(keys), to_dev(vals), kd, vd, None, 0, n, layer(hkv, hkv, d, bs, 1),
+                           slot_mapping=to_dev(slots))
+    kp.reshape(nb * bs, hkv, d)[slots] = keys
+    vp.reshape(nb * bs, hkv, d)[slots] = vals
+    assert np.array_equal(to_host(kd), kp) and np.array_equal(to_host(vd), vp)
+
+
+def test_append_fp8_bit_exact_sticky_scales(engine):
+    """Several appends into the same blocks: scales only grow, old bytes stay."""
+    rng = np.random.default_rng(11)
+    hkv, d, bs, nb = 2, 64, 16, 12
+    kp = np.zeros((nb, bs, hkv, d), np.uint8)
+    vp = np.zeros_like(kp)
+    ks = np.zeros(nb, np.float16)
+    vs = np.zeros(nb, np.float16)
+    bt = rng.permutation(nb).astype(np.int32)
+    kd, vd, ksd, vsd = to_dev(kp), to_dev(vp), to_dev(ks), to_dev(vs)
+    off = 0
+    for step, n in enumerate([7, 20, 1, 1, 33, 5]):
+        mult = [1.0, 4.0, 0.01, 100.0, 0.5, 0.0][step]
+        keys = (rng.standard_normal((n, hkv, d)) * mult).astype(np.float16)
+        vals = (rng.standard_normal((n, hkv, d)) * mult).astype(np.float16)
+        engine.append_to_cache(to_dev(keys), to_dev(vals), kd, vd, to_dev(bt), off, n, layer(hkv, hkv, d, bs, 2),
+                               k_scale=ksd, v_scale=vsd)
+        oracle.append(2, keys, vals, kp, vp, bt, off, ks.view(np.uint16), vs.view(np.uint16))
+        off += n
+        assert np.array_equal(to_host(kd), kp), f"K bytes differ after append {step}"
+        assert np.array_equal(to_host(vd), vp), f"V bytes differ after append {step}"
+        assert np.array_equal(to_host(ksd).view(np.uint16), ks.view(np.uint16)), f"K scales differ {step}"
+        assert np.array_equal(to_host(vsd).view(np.uint16), vs.view(np.uint16)), f"V scales differ {step}"
+
+
+# ---------------------------------------------------------------- decode
+
+DECODE_CASES = [
+    # B, H, Hkv, d, bs, dtype, lens, window, kernel(0 auto, 1 valu, 2 mfma), part_tokens
+    (4, 8, 8, 128, 16, 0, [17, 64, 129, 200], 0, 0, 0),           # c1 shape, fp32, VALU
+    (3, 32, 8, 128, 16, 1, [1, 15, 333], 0, 0, 0),                # GQA 4 fp16, MFMA
+    (3, 32, 8, 128, 16, 1, [1, 15, 333], 0, 1, 0),                # same on VALU
+    (5, 64, 8, 128, 16, 1, [16, 17, 1000, 2049, 31], 0, 0, 64),   # GQA 8, forced splits
+    (2, 16, 1, 64, 8, 1, [100, 257], 0, 0, 0),                    # MQA 16, bs 8, d 64
+    (2, 8, 2, 256, 32, 1, [70, 300], 0, 0, 0),                    # d 256, bs 32
+    (3, 8, 8, 32, 4, 0, [5, 9, 40], 0, 0, 0),                     # tiny bs, d 32
+    (4, 32, 8, 128, 16, 1, [100, 5000, 4097, 4096], 4096, 0, 0),  # sliding window
+    (2, 8, 8, 128, 16, 0, [700, 33], 64, 0, 0),                   # window not block aligned, fp32
+    (3, 32, 8, 128, 16, 2, [3, 200, 1500], 0, 0, 0),              # fp8 MFMA
+    (3, 32, 8, 128, 16, 2, [3, 200, 1500], 0, 1, 0),              # fp8 VALU
+    (2, 24, 8, 128, 16, 1, [77, 1025], 0, 0, 0),                  # group 3 -> VALU
+]
+
+
+def build_fp8(engine, rng, k16, v16, bt, lens, hkv, d, bs):
+    """Quantise the f16 pools through the append kernel, sequence by sequence, and
+    check the bytes and scales against the oracle's append."""
+    import torch
+    nb = k16.shape[0]
+    kp = np.zeros((nb, bs, hkv, d), np.uint8)
+    vp = np.zeros_like(kp)
+    ks = np.zeros(nb, np.float16)
+    vs = np.zeros(nb, np.float16)
+    kd, vd, ksd, vsd = to_dev(kp), to_dev(vp), to_dev(ks), to_dev(vs)
+    for b, L in enumerate(lens):
+        L = int(L)
+        if L == 0:
+            continue
+        tok = np.arange(L)
+        keys = k16[bt[b, tok // bs], tok % bs]
+        vals = v16[bt[b, tok // bs], tok % bs]
+        engine.append_to_cache(to_dev(keys), to_dev(vals), kd, vd, to_dev(bt[b]), 0, L, layer(hkv, hkv, d, bs, 2),
+                               k_scale=ksd, v_scale=vsd)
+        oracle.append(2, keys, vals, kp, vp, bt[b], 0, ks.view(np.uint16), vs.view(np.uint16))
+    assert np.array_equal(to_host(kd), kp) and np.array_equal(to_host(vd), vp)
+    assert np.array_equal(to_host(ksd).view(np.uint16), ks.view(np.uint16))
+    torch.cuda.synchronize()
+    return kd, vd, ksd, vsd, kp, vp, ks, vs
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=[f"c{i}" for i in range(len(DECODE_CASES))])
+def test_decode_parity(engine, case):
+    import torch
+    B, H, hkv, d, bs, dtype, lens, window, kern, part = case
+    rng = np.random.default_rng(1000 + len(lens) * 7 + d + bs + dtype)
+    q, k, v, bt, lens = make_case(rng, B, H, hkv, d, bs, dtype, lens)
+    engine.set_decode_kernel(kern)
+    engine.set_partition_tokens(part)
+    try:
+        ks = vs = None
+        if dtype == 2:
+            kd, vd, ksd, vsd, kp, vp, ks, vs = build_fp8(engine, rng, k, v, bt, lens, hkv, d, bs)
+        else:
+            kd, vd, ksd, vsd = to_dev(k), to_dev(v), None, None
+            kp, vp = k, v
+        out = torch.zeros((B, H, d), dtype=torch.float32 if dtype == 0 else torch.float16, device="cuda")
+        engine.decode(to_dev(q), kd, vd, to_dev(bt), to_dev(lens), out, B, bt.shape[1], layer(H, hkv, d, bs, dtype, window),
+                      k_scale=ksd, v_scale=vsd)
+        ref = oracle.decode(dtype, q, kp, vp, bt, lens, H, window=window,
+                            k_scale=None if ks is None else ks.view(np.uint16),
+                            v_scale=None if vs is None else vs.view(np.uint16), n_threads=8)
+        err = row_rel_err(to_host(out), ref)
+        assert err <= TOL[dtype], f"rel err {err:.3e}"
+    finally:
+        engine.set_decode_kernel(0)
+        engine.set_partition_tokens(0)
+
+
+def test_decode_empty_sequence_is_nan(engine):
+    import torch
+    rng = np.random.default_rng(3)
+    q, k, v, bt, lens = make_case(rng, 2, 8, 8, 64, 16, 1, [0, 20])
+    out = torch.zeros((2, 8, 64), dtype=torch.float16, device="cuda")
+    engine.decode(to_dev(q), to_dev(k), to_dev(v), to_dev(bt), to_dev(lens), out, 2, bt.shape[1],
+                  layer(8, 8, 64, 16, 1))
+    o = to_host(out).astype(np.float64)
+    assert np.isnan(o[0]).all() and np.isfinite(o[1]).all()
+
+
+# ---------------------------------------------------------------- prefill rows
+
+PREFILL_CASES = [
+    # T, q_offset, H, Hkv, d, bs, dtype, causal, window
+    (16, 0, 4, 2, 64, 16, 0, False, 0),   # reference fusedPrefill / fp8Quantization shapes (f32)
+    (8, 0, 1, 1, 32, 16, 0, True, 0),     # causalMasking shape
+    (64, 0, 32, 8, 128, 16, 1, True, 0),
+    (40, 100, 32, 8, 128, 16, 1, True, 0),  # chunk with cached context
+    (33, 17, 8, 8, 128, 8, 0, True, 0),
+    (50, 30, 32, 8, 128, 16, 1, True, 48),  # fixed window start
+    (16, 0, 4, 2, 64, 16, 2, False, 0),     # fp8 prefill
+]
+
+
+@pytest.mark.parametrize("case", PREFILL_CASES, ids=[f"p{i}" for i in range(len(PREFILL_CASES))])
+def test_prefill_parity(engine, case):
+    import torch
+    T, off, H, hkv, d, bs, dtype, causal, window = case
+    rng = np.random.default_rng(2000 + T + off + d)
+    kv_len = off + T
+    q, k, v, bt, _ = make_case(rng, 1, H, hkv, d, bs, dtype, [kv_len])
+    q = rng.standard_normal((T, H, d)).astype(q.dtype)
+    ks = vs = None
+    if dtype == 2:
+        kd, vd, ksd, vsd, kp, vp, ks, vs = build_fp8(engine, rng, k, v, bt, [kv_len], hkv, d, bs)
+    else:
+        kd, vd, ksd, vsd = to_dev(k), to_dev(v), None, None
+        kp, vp = k, v
+    out = torch.zeros((T, H, d), dtype=torch.float32 if dtype == 0 else torch.float16, device="cuda")
+    engine.prefill(to_dev(q), kd, vd, to_dev(bt[0]), out, T, layer(H, hkv, d, bs, dtype, window), causal=causal,
+                   q_offset=off, k_scale=ksd, v_scale=vsd)
+    ref = oracle.prefill(dtype, q, kp, vp, bt[0], off, causal=causal, window=window,
+                         k_scale=None if ks is None else ks.view(np.uint16),
+                         v_scale=None if vs is None else vs.view(np.uint16), n_threads=8)
+    o = to_host(out).astype(np.float64)
+    fin = np.isfinite(ref).all(axis=-1)
+    assert np.isnan(o[~fin]).all()  # rows with no keys (window before the row) stay 0/0
+    err = row_rel_err(o[fin], ref[fin])
+    assert err <= TOL[dtype], f"rel err {err:.3e}"
+
+
+# ---------------------------------------------------------------- mixed step
+
+@pytest.mark.parametrize("dtype", [1, 2, 0])
+def test_mixed_step_parity(engine, dtype):
+    """Append new tokens of prefill chunks and decodes, then attend, in one call."""
+    import torch
+    rng = np.random.default_rng(300 + dtype)
+    H, hkv, d, bs = 32, 8, 128, 16
+    ctx = np.array([0, 37, 300, 15, 100, 1], np.int32)
+    ql = np.array([40, 25, 1, 1, 1, 64], np.int32)
+    total = ctx + ql
+    nblk = (total + bs - 1) // bs
+    nb = int(nblk.sum()) + 5
+    perm = rng.permutation(nb).astype(np.int32)
+    bt = np.zeros((len(ctx), int(nblk.max())), np.int32)
+    c = 0
+    for s, n in enumerate(nblk):
+        bt[s, :n] = perm[c:c + n]
+        c += n
+    dt = np.float32 if dtype == 0 else np.float16
+    src_k = rng.standard_normal((nb, bs, hkv, d)).astype(dt)
+    src_v = rng.standard_normal((nb, bs, hkv, d)).astype(dt)
+    rows = int(ql.sum())
+    q = rng.standard_normal((rows, H, d)).astype(dt)
+    new_k = rng.standard_normal((rows, hkv, d)).astype(dt)
+    new_v = rng.standard_normal((rows, hkv, d)).astype(dt)
+    # cached context: f32/f16 pools hold the source data; fp8 pools are quantised through append first
+    if dtype == 2:
+        kp = np.zeros((nb, bs, hkv, d), np.uint8)
+        vp = np.zeros_like(kp)
+        ks = np.zeros(nb, np.float16)
+        vs = np.zeros(nb, np.float16)
+        kd, vd, ksd, vsd = to_dev(kp), to_dev(vp), to_dev(ks), to_dev(vs)
+        for s in range(len(ctx)):
+            L = int(ctx[s])
+            if L == 0:
+                continue
+            tok = np.arange(L)
+            keys, vals = src_k[bt[s, tok // bs], tok % bs], src_v[bt[s, tok // bs], tok % bs]
+            engine.append_to_cache(to_dev(keys), to_dev(vals), kd, vd, to_dev(bt[s]), 0, L,
+                                   layer(hkv, hkv, d, bs, 2), k_scale=ksd, v_scale=vsd)
+            oracle.append(2, keys, vals, kp, vp, bt[s], 0, ks.view(np.uint16), vs.view(np.uint16))
+    else:
+        kp, vp = src_k.copy(), src_v.copy()
+        kd, vd, ksd, vsd, ks, vs = to_dev(kp), to_dev(vp), None, None, None, None
+    out = torch.zeros((rows, H, d), dtype=torch.float32 if dtype == 0 else torch.float16, device="cuda")
+    engine.mixed_step(to_dev(q), out, kd, vd, to_dev(bt), ctx, ql, layer(H, hkv, d, bs, dtype),
+                      new_keys=to_dev(new_k), new_values=to_dev(new_v), k_scale=ksd, v_scale=vsd)
+    # oracle: append then per-sequence prefill rows
+    r0 = 0
+    refs = []
+    for s in range(len(ctx)):
+        T = int(ql[s])
+        oracle.append(dtype, new_k[r0:r0 + T], new_v[r0:r0 + T], kp, vp, bt[s], int(ctx[s]),
+                      None if ks is None else ks.view(np.uint16), None if vs is None else vs.view(np.uint16))
+        r0 += T
+    r0 = 0
+    for s in range(len(ctx)):
+        T = int(ql[s])
+        refs.append(oracle.prefill(dtype, q[r0:r0 + T], kp, vp, bt[s], int(ctx[s]), causal=True,
+                                   k_scale=None if ks is None else ks.view(np.uint16),
+                                   v_scale=None if vs is None else vs.view(np.uint16), n_threads=8))
+        r0 += T
+    ref = np.concatenate(refs)
+    assert np.array_equal(to_host(kd).view(np.uint8), kp.view(np.uint8)), "pool bytes differ after mixed append"
+    if dtype == 2:
+        assert np.array_equal(to_host(ksd).view(np.uint16), ks.view(np.uint16))
+    err = row_rel_err(to_host(out), ref)
+    assert err <= TOL[dtype], f"rel err {err:.3e}"
