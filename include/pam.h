@@ -251,8 +251,10 @@ void pam_buffer_free(void *context, void *ptr);
 int32_t pam_buffer_upload(void *context, void *device_dst, const void *host_src, size_t bytes);
 int32_t pam_buffer_download(void *context, void *host_dst, const void *device_src, size_t bytes);
 int32_t pam_buffer_zero(void *context, void *device_ptr, size_t bytes);
-/* Launch on an external hipStream_t (NULL = the context's own stream). */
+/* Launch on an external hipStream_t (NULL = the device's default stream). */
 int32_t pam_set_stream(void *context, void *hip_stream);
+/* Go back to launching on the context's own (non-blocking) stream. */
+int32_t pam_use_own_stream(void *context);
 /* true (default): calls wait for their GPU work; false: calls return once enqueued. */
 int32_t pam_set_synchronous(void *context, bool synchronous);
 int32_t pam_synchronize(void *context);
@@ -291,6 +293,12 @@ int32_t pam_engine_mixed_step(void *context, const pam_mixed_request *request);
  * pair of kernels.metal:553-601 with a per-element half scale. */
 int32_t pam_fp8_quantize(void *context, const uint16_t *values, const uint16_t *scales, uint8_t *out, int64_t n);
 int32_t pam_fp8_dequant(void *context, const uint8_t *codes, const uint16_t *scales, uint16_t *out, int64_t n);
+
+/* Calibration streams of known size on the context's stream, timed with hipEvents
+ * (ms written to *ms): every byte of src read once / copied once with 16-byte
+ * accesses by `blocks` workgroups of 256 threads (0 = 4 per CU).  bytes % 16 == 0. */
+int32_t pam_calib_stream_read(void *context, const void *src, size_t bytes, int32_t blocks, float *ms);
+int32_t pam_calib_stream_copy(void *context, const void *src, void *dst, size_t bytes, int32_t blocks, float *ms);
 
 /* Test hook: the next n kernel launches of this context report a launch failure
  * (host-side; no GPU work is faulted). */

@@ -116,6 +116,7 @@ SIGNATURES = {
     "pam_buffer_download": (I32, [P, P, P, SZ]),
     "pam_buffer_zero": (I32, [P, P, SZ]),
     "pam_set_stream": (I32, [P, P]),
+    "pam_use_own_stream": (I32, [P]),
     "pam_set_synchronous": (I32, [P, C.c_bool]),
     "pam_synchronize": (I32, [P]),
     "pam_reserve_workspace": (I32, [P, SZ]),
@@ -124,6 +125,8 @@ SIGNATURES = {
     "pam_engine_mixed_step": (I32, [P, C.POINTER(MixedRequest)]),
     "pam_fp8_quantize": (I32, [P, P, P, P, I64]),
     "pam_fp8_dequant": (I32, [P, P, P, P, I64]),
+    "pam_calib_stream_read": (I32, [P, P, SZ, I32, P]),
+    "pam_calib_stream_copy": (I32, [P, P, P, SZ, I32, P]),
     "pam_debug_fail_next_launches": (I32, [P, I32]),
     "pam_version": (C.c_char_p, []),
 }

@@ -142,9 +142,13 @@ class PagedAttentionEngine:
 
     # --- configuration
     def set_stream(self, stream):
-        """Launch on a torch stream (or raw hipStream_t int); None -> own stream."""
-        raw = None if stream is None else (stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
-        self._check(lib().pam_set_stream(self._ctx, raw))
+        """Launch on a torch stream (or a raw hipStream_t int; 0 = default stream);
+        None -> the engine's own stream."""
+        if stream is None:
+            self._check(lib().pam_use_own_stream(self._ctx))
+            return
+        raw = stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+        self._check(lib().pam_set_stream(self._ctx, raw or None))
 
     @property
     def synchronous(self):
@@ -220,6 +224,18 @@ class PagedAttentionEngine:
             _ptr(v_scale), _ptr(block_tables), int(block_tables.shape[1]), len(cl),
             cl.ctypes.data_as(C.c_void_p), ql.ctypes.data_as(C.c_void_p), layer.c())
         self._check(lib().pam_engine_mixed_step(self._ctx, C.byref(r)))
+
+    # --- calibration streams (achievable HBM rates, counter scaling)
+    def calib_stream_read(self, src, blocks=0) -> float:
+        ms = C.c_float()
+        self._check(lib().pam_calib_stream_read(self._ctx, _ptr(src), _nbytes(src), int(blocks), C.byref(ms)))
+        return ms.value
+
+    def calib_stream_copy(self, src, dst, blocks=0) -> float:
+        ms = C.c_float()
+        self._check(lib().pam_calib_stream_copy(self._ctx, _ptr(src), _ptr(dst), _nbytes(src), int(blocks),
+                                                C.byref(ms)))
+        return ms.value
 
     # --- FP8 codec (kernels.metal:553-601), elementwise
     def fp8_quantize(self, values_f16, scales_f16, out_u8):

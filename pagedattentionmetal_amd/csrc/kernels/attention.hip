@@ -24,10 +24,11 @@
 
 namespace pam {
 
+// Token positions fit in 32 bits (sequence lengths are int32 at the boundary).
 struct RowCtx {
     const int32_t *bt;
-    int64_t k_lo, k_hi;
-    int64_t out_row;
+    int k_lo, k_hi;
+    int out_row;
 };
 
 __device__ __forceinline__ RowCtx row_ctx(const AttnParams &p, int r) {
@@ -40,15 +41,15 @@ __device__ __forceinline__ RowCtx row_ctx(const AttnParams &p, int r) {
         if (nlb > p.max_num_blocks) nlb = p.max_num_blocks;
         const int64_t cap = nlb * p.block_size;
         c.bt = p.block_tables + (int64_t)r * p.bt_stride;
-        c.k_lo = ws;
-        c.k_hi = L < cap ? L : cap;
+        c.k_lo = (int)ws;
+        c.k_hi = (int)(L < cap ? L : cap);
         c.out_row = r;
     } else if (p.mode == kRowPrefill) {
         // one fixed window start for every row (PagedAttentionEngine.swift:802)
         const int64_t kv_len = (int64_t)p.q_offset + p.rows;
         c.bt = p.block_tables;
-        c.k_lo = p.window > 0 ? (kv_len > p.window ? kv_len - p.window : 0) : 0;
-        c.k_hi = p.causal ? (int64_t)p.q_offset + r + 1 : kv_len;
+        c.k_lo = (int)(p.window > 0 ? (kv_len > p.window ? kv_len - p.window : 0) : 0);
+        c.k_hi = (int)(p.causal ? (int64_t)p.q_offset + r + 1 : kv_len);
         c.out_row = r;
     } else {
         const int4 ri = p.row_info[r];
@@ -61,18 +62,18 @@ __device__ __forceinline__ RowCtx row_ctx(const AttnParams &p, int r) {
 }
 
 struct PartRange {
-    int64_t t_begin, t_end;  // 16-token tiles
+    int t_begin, t_end;  // 16-token tiles
     int nparts;
 };
 
 __device__ __forceinline__ PartRange part_range(const RowCtx &c, int part, int part_tokens) {
     PartRange pr;
-    const int64_t tile0 = c.k_lo / 16;
-    const int64_t tile_end = (c.k_hi + 15) / 16;
-    const int64_t ntiles = c.k_hi > c.k_lo ? tile_end - tile0 : 0;
+    const int tile0 = c.k_lo / 16;
+    const int tile_end = (c.k_hi + 15) / 16;
+    const int ntiles = c.k_hi > c.k_lo ? tile_end - tile0 : 0;
     const int tpp = part_tokens / 16;
-    pr.nparts = (int)((ntiles + tpp - 1) / tpp);
-    pr.t_begin = tile0 + (int64_t)part * tpp;
+    pr.nparts = (ntiles + tpp - 1) / tpp;
+    pr.t_begin = tile0 + part * tpp;
     pr.t_end = pr.t_begin + tpp < tile_end ? pr.t_begin + tpp : tile_end;
     return pr;
 }
@@ -90,60 +91,115 @@ struct KvTraits<uint8_t> {
     static constexpr int kBytes = 1;
 };
 
-// Eight consecutive elements of a raw slice as halves (A operand chunk / LDS row).
-template <typename KV>
-__device__ __forceinline__ f16x8 slice_chunk(const uint4 *raw, int c, f16 scale);
-
-template <>
-__device__ __forceinline__ f16x8 slice_chunk<f16>(const uint4 *raw, int c, f16) {
-    return __builtin_bit_cast(f16x8, raw[c]);
-}
-
-template <>
-__device__ __forceinline__ f16x8 slice_chunk<uint8_t>(const uint4 *raw, int c, f16 scale) {
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(raw) + c * 2;
-    f16x8 o;
-#pragma unroll
-    for (int i = 0; i < 8; i++) o[i] = fp8_dequant((w[i >> 2] >> (8 * (i & 3))) & 0xFFu, scale);
-    return o;
-}
-
 // ------------------------------------------------------------------ MFMA body
 
-template <typename KV, int HD, bool BS16>
-__global__ __launch_bounds__(64) void attn_mfma_kernel(AttnParams p) {
-    constexpr int DPG = HD / 4;                 // dims held by one lane group (lane / 16)
-    constexpr int NC = HD / 32;                 // 16x16x32 chunks per S tile
-    constexpr int NO = HD / 16;                 // 16-dim output chunks
-    constexpr int RAW = DPG * KvTraits<KV>::kBytes / 16;  // 16-byte loads per slice
-    constexpr int LDS = HD + 8;                 // padded V row (halves)
-    __shared__ __attribute__((aligned(16))) f16 vt[16 * LDS];
+// e4m3 byte -> binary16 carrying the same sign / exponent / mantissa bits, i.e.
+// the exact e4m3 value times 2^-8 (subnormal codes land on f16 subnormals).
+// Two bytes per 32-bit word: perm places them in the high byte of each half,
+// then the magnitude moves down one bit under the sign.
+__device__ __forceinline__ uint32_t e4m3x2_to_f16x2_bits(uint32_t w, uint32_t sel) {
+    const uint32_t t = __builtin_amdgcn_perm(0u, w, sel);
+    return (t & 0x80008000u) | ((t >> 1) & 0x3F803F80u);
+}
+__device__ __forceinline__ f16x8 e4m3x8_to_f16x8(uint32_t w0, uint32_t w1) {
+    uint4 h;
+    h.x = e4m3x2_to_f16x2_bits(w0, 0x010C000Cu);
+    h.y = e4m3x2_to_f16x2_bits(w0, 0x030C020Cu);
+    h.z = e4m3x2_to_f16x2_bits(w1, 0x010C000Cu);
+    h.w = e4m3x2_to_f16x2_bits(w1, 0x030C020Cu);
+    return __builtin_bit_cast(f16x8, h);
+}
 
-    const int lane = threadIdx.x, row = lane & 15, grp = lane >> 4;
-    const int part = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z;
+// Chunk c (8 elements) of a lane's raw K/V slice as the MFMA operand / LDS row.
+//  f16: the bytes themselves.
+//  e4m3, per-tile scale (block size 16): exact value * 2^-8; the scale and 2^8
+//        are applied to S (keys) and folded into P (values) per tile.
+//  e4m3, per-token scale: the reference's half dequantisation per element.
+template <typename KV, bool kTileScale>
+__device__ __forceinline__ f16x8 operand_chunk(const uint4 *raw, int c, f16 scale) {
+    if constexpr (sizeof(KV) == 2) {
+        return __builtin_bit_cast(f16x8, raw[c]);
+    } else {
+        const uint32_t *w = reinterpret_cast<const uint32_t *>(raw) + c * 2;
+        if constexpr (kTileScale) {
+            return e4m3x8_to_f16x8(w[0], w[1]);
+        } else {
+            f16x8 o;
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[i] = fp8_dequant((w[i >> 2] >> (8 * (i & 3))) & 0xFFu, scale);
+            return o;
+        }
+    }
+}
+
+// Waves per workgroup of the MFMA kernel: they split one partition's tiles and
+// merge their softmax states in LDS.
+constexpr int kMfmaWaves = 4;
+// Rows the persistent form can index from LDS (its item table).
+constexpr int kPersistentMaxRows = 2048;
+
+template <typename KV, int HD>
+struct MfmaShape {
+    static constexpr int NC = HD / 32;                 // 16x16x32 chunks per S tile
+    static constexpr int NO = HD / 16;                 // 16-dim output chunks
+    static constexpr int EPL = 16 / KvTraits<KV>::kBytes;  // elements per 16-byte load
+    static constexpr int RAW = HD / (4 * EPL);         // 16-byte loads per lane per token row
+    static constexpr int CPL = EPL / 8;                // 8-element operand chunks per load
+    static constexpr int LDS = HD + 8;                 // padded V row (halves)
+    static constexpr int NW = kMfmaWaves;
+    static constexpr int VT = 16 * LDS;                // halves of one wave's V tile
+    // per-wave V tiles during the tile loop, per-wave partial outputs in the merge
+    static constexpr int kSmemBytes = NW * VT * 2 > NW * 16 * HD * 4 ? NW * VT * 2 : NW * 16 * HD * 4;
+};
+
+// One work item: (row r, split-context partition `part`, kv head kvh) on the
+// whole workgroup.  Returns uniformly across the workgroup.
+template <typename KV, int HD, bool BS16>
+__device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, int kvh, char *smem,
+                                          float (*sm_ml)[16][2]) {
+    using S = MfmaShape<KV, HD>;
+    constexpr int NC = S::NC, NO = S::NO, EPL = S::EPL, RAW = S::RAW, CPL = S::CPL, LDS = S::LDS, NW = S::NW,
+                  VT = S::VT;
+    constexpr bool kFp8 = sizeof(KV) == 1;
+    constexpr bool kTileScale = kFp8 && BS16;   // one block per tile: scale folded out of the products
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
     const int H = p.num_heads;
     const int G = H / p.num_kv_heads;
     const RowCtx c = row_ctx(p, r);
-    const PartRange pr = part_range(c, part, p.part_tokens);
-    if (part >= (pr.nparts > 1 ? pr.nparts : 1)) return;
+    const PartRange wg = part_range(c, part, p.part_tokens);
+    if (part >= (wg.nparts > 1 ? wg.nparts : 1)) return;
 
     const int h = kvh * G + row;  // this lane's query head (N column)
     const bool head_ok = row < G;
     f16 *out = static_cast<f16 *>(p.out);
-    if (pr.nparts == 0) {
+    if (wg.nparts == 0) {
         // no keys: 0/0 as in the reference's m/l bookkeeping
-        if (head_ok)
-            for (int d = grp; d < HD; d += 4) out[(c.out_row * H + h) * (int64_t)HD + d] = (f16)__builtin_nanf("");
+        for (int idx = threadIdx.x; idx < G * HD; idx += 64 * NW)
+            out[(c.out_row * H + kvh * G) * (int64_t)HD + idx] = (f16)__builtin_nanf("");
         return;
     }
+    // this wave's contiguous share of the workgroup's tiles (possibly empty)
+    PartRange pr = wg;
+    {
+        const int per = (wg.t_end - wg.t_begin + NW - 1) / NW;
+        pr.t_begin = wg.t_begin + wave * per;
+        pr.t_end = pr.t_begin + per < wg.t_end ? pr.t_begin + per : wg.t_end;
+    }
+    f16 *vt = reinterpret_cast<f16 *>(smem) + wave * VT;
 
-    // Q^T B operand: lane holds Q[h][grp*DPG + 8c .. +8]
+    // Contraction order: load u of lane group g covers row bytes [64u + 16g, +16),
+    // so one load instruction reads 64 contiguous bytes of each of the 16 token
+    // rows; operand chunk c holds dims dim_of(c) .. +8 of that slice.
+    auto dim_of = [&](int cidx) { return (cidx / CPL) * 4 * EPL + grp * EPL + (cidx % CPL) * 8; };
+
+    // Q^T B operand: lane holds Q[h][dim_of(c) .. +8] for chunk c
     f16x8 qv[NC];
     {
-        const f16 *qp = static_cast<const f16 *>(p.q) + ((int64_t)r * H + (head_ok ? h : 0)) * HD + grp * DPG;
+        const f16 *qp = static_cast<const f16 *>(p.q) + ((int64_t)r * H + (head_ok ? h : 0)) * HD;
 #pragma unroll
         for (int i = 0; i < NC; i++) {
-            f16x8 v = *reinterpret_cast<const f16x8 *>(qp + 8 * i);
+            f16x8 v = *reinterpret_cast<const f16x8 *>(qp + dim_of(i));
             qv[i] = head_ok ? v : (f16x8)(f16)0.0f;
         }
     }
@@ -153,28 +209,64 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(AttnParams p) {
     const char *vbase = static_cast<const char *>(p.v_pool);
     const int bs = p.block_size;
 
-    auto load_tile = [&](int64_t tile, uint4 *kr, uint4 *vr, f16 &ks, f16 &vs) {
-        const int64_t j = tile * 16 + row;
-        const bool valid = j >= c.k_lo && j < c.k_hi;
-        int64_t phys = 0, slot = 0;
+    // Raw loads stay untouched until they are consumed: any arithmetic on them
+    // right after the load would make the wave wait for it there.  Lanes whose
+    // token lies outside the key range read a zero page instead of the pool, so
+    // no masking of loaded data is needed (their S entries become -inf anyway).
+    struct Tile {
+        uint4 k[RAW], v[RAW];
+        uint16_t ksb, vsb;
+    };
+
+    // Block size 16: one physical block per tile.  Table entries for 64 tiles
+    // from window_base sit in one VGPR (lane i = tile window_base + i), refreshed
+    // once per 16-tile chunk, so a tile's address never waits on a table load.
+    int window_base = pr.t_begin;
+    int32_t bt_window = 0;
+    auto refresh_window = [&](int base) {
+        window_base = base;
         if (BS16) {
-            phys = c.bt[tile];
-            slot = row;
-        } else if (valid) {
-            phys = c.bt[j / bs];
-            slot = j % bs;
+            const int idx = base + lane < pr.t_end ? base + lane : pr.t_end - 1;
+            bt_window = c.bt[idx];
         }
-        const int64_t off = ((phys * bs + slot) * row_stride + (int64_t)kvh * HD + grp * DPG) * KvTraits<KV>::kBytes;
-        const uint4 *kp = reinterpret_cast<const uint4 *>(kbase + off);
-        const uint4 *vp = reinterpret_cast<const uint4 *>(vbase + off);
+    };
+    if (pr.t_begin < pr.t_end) refresh_window(pr.t_begin);
+    auto tile_block = [&](int tile) -> int {
+        return __builtin_amdgcn_readlane(bt_window, tile - window_base);
+    };
+
+    // Tokens this wave may use: [k_lo, k_hi) cut to the partition.  Tiles past the
+    // partition end are still "loaded" (from its last tile, a cache hit) so that
+    // every step issues the same loads: with no load under a branch the compiler
+    // can wait for exactly the tile it needs instead of draining all of them.
+    const int j_hi = c.k_hi < pr.t_end * 16 ? c.k_hi : pr.t_end * 16;
+    auto load_tile = [&](int tile, Tile &t) {
+        const int lt = tile < pr.t_end ? tile : pr.t_end - 1;
+        const int j = tile * 16 + row;
+        const bool valid = j >= c.k_lo && j < j_hi;
+        int phys, slot;
+        if (BS16) {
+            phys = tile_block(lt);
+            slot = row;
+        } else {
+            const int jj = valid ? j : c.k_lo;
+            phys = c.bt[jj / bs];
+            slot = jj % bs;
+        }
+        const int64_t off = (((int64_t)phys * bs + slot) * row_stride + (int64_t)kvh * HD) * KvTraits<KV>::kBytes + grp * 16;
+        // Every lane loads unconditionally (loads under a branch would make the
+        // compiler drain every outstanding load before each use).
+        const char *zp = static_cast<const char *>(p.zero_page) + grp * 16;
+        const uint4 *kp = reinterpret_cast<const uint4 *>(valid ? kbase + off : zp);
+        const uint4 *vp = reinterpret_cast<const uint4 *>(valid ? vbase + off : zp);
 #pragma unroll
         for (int i = 0; i < RAW; i++) {
-            kr[i] = valid ? kp[i] : make_uint4(0, 0, 0, 0);
-            vr[i] = valid ? vp[i] : make_uint4(0, 0, 0, 0);
+            t.k[i] = kp[4 * i];
+            t.v[i] = vp[4 * i];
         }
-        if constexpr (KvTraits<KV>::kBytes == 1) {
-            ks = valid ? bits_to_f16(p.k_scale[phys]) : (f16)0.0f;
-            vs = valid ? bits_to_f16(p.v_scale[phys]) : (f16)0.0f;
+        if constexpr (kFp8) {  // phys is in bounds for every lane
+            t.ksb = p.k_scale[phys];
+            t.vsb = p.v_scale[phys];
         }
     };
 
@@ -183,31 +275,47 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < NO; i++) o[i] = (f32x4)0.0f;
 
-    uint4 kr[RAW], vr[RAW], kn[RAW], vn[RAW];
-    f16 ks = (f16)0.0f, vs = (f16)0.0f, ksn = (f16)0.0f, vsn = (f16)0.0f;
-    load_tile(pr.t_begin, kr, vr, ks, vs);
-
-    for (int64_t tile = pr.t_begin; tile < pr.t_end; tile++) {
-        if (tile + 1 < pr.t_end) load_tile(tile + 1, kn, vn, ksn, vsn);
-
+    // Two register tiles in flight per wave.  As soon as a tile's K has fed the S
+    // MFMAs and its V rows sit in LDS, its registers are refilled with the tile two
+    // ahead, so the next tile is always loading while this one's softmax and PV
+    // run, and the refill overlaps the following tile's work.
+    auto step = [&](int tile, Tile &t) {
+        // keep the scheduler from hoisting the next tile's MFMAs (and with them
+        // the wait for its loads) into this one
+        __builtin_amdgcn_sched_barrier(0);
+        // per-tile scales: block size 16 puts the whole tile in one block and 2^8
+        // undoes the operand shift; otherwise each lane's token has its own scale
+        f16 ks = (f16)0.0f, vs = (f16)0.0f;
+        if constexpr (kTileScale) {
+            ks = (f16)((float)bits_to_f16(t.ksb) * 256.0f);
+            vs = (f16)((float)bits_to_f16(t.vsb) * 256.0f);
+        } else if constexpr (kFp8) {
+            ks = bits_to_f16(t.ksb);
+            vs = bits_to_f16(t.vsb);
+        }
         // S^T[token][head] over HD dims
         f32x4 s = (f32x4)0.0f;
 #pragma unroll
         for (int i = 0; i < NC; i++)
-            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(slice_chunk<KV>(kr, i, ks), qv[i], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(operand_chunk<KV, kTileScale>(t.k, i, ks), qv[i], s, 0, 0, 0);
 
-        // stage V rows (token = row) for the transposed read
+        // stage V rows (token = row) for the transposed read; LDS ops of one wave
+        // execute in order, the wave barriers only pin the compiler's order
 #pragma unroll
         for (int i = 0; i < NC; i++)
-            *reinterpret_cast<f16x8 *>(&vt[row * LDS + grp * DPG + 8 * i]) = slice_chunk<KV>(vr, i, vs);
+            *reinterpret_cast<f16x8 *>(&vt[row * LDS + dim_of(i)]) = operand_chunk<KV, kTileScale>(t.v, i, vs);
+        const float sc = kTileScale ? p.scale_log2 * (float)ks : p.scale_log2;
+        const float pv_scale = kTileScale ? (float)vs : 1.0f;
+        __builtin_amdgcn_wave_barrier();
+        load_tile(tile + 2, t);
 
         // online softmax on this lane's 4 tokens of head `row`
         float sv[4];
         float mt = -INFINITY;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int64_t j = tile * 16 + 4 * grp + q;
-            sv[q] = (j >= c.k_lo && j < c.k_hi) ? s[q] * p.scale_log2 : -INFINITY;
+            const int j = tile * 16 + 4 * grp + q;
+            sv[q] = (j >= c.k_lo && j < j_hi) ? s[q] * sc : -INFINITY;
             mt = fmaxf(mt, sv[q]);
         }
         mt = fmaxf(mt, shfl_xor(mt, 16));
@@ -221,14 +329,13 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(AttnParams p) {
         for (int q = 0; q < 4; q++) {
             const float pq = exp2f(sv[q] - m_use);
             psum += pq;
-            pb[q] = (f16)pq;
+            pb[q] = (f16)(pq * pv_scale);
         }
         l_run = l_run * corr + psum;
         m_run = m_new;
 #pragma unroll
         for (int i = 0; i < NO; i++) o[i] *= corr;
 
-        __syncthreads();
 #pragma unroll
         for (int i = 0; i < NO; i++) {
             f16x4 a;
@@ -236,39 +343,133 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(AttnParams p) {
             for (int q = 0; q < 4; q++) a[q] = vt[(4 * grp + q) * LDS + 16 * i + row];
             o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[i], 0, 0, 0);
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
+    };
 
+    // 16-tile chunks run as straight-line code: inside a chunk the compiler can
+    // count outstanding loads exactly and waits only for the tile it consumes (a
+    // loop back edge makes it drain everything).  Exits are uniform branches.
+    if (pr.t_begin < pr.t_end) {
+    Tile ta, tb;
+    load_tile(pr.t_begin, ta);
+    load_tile(pr.t_begin + 1, tb);
+    for (int chunk = pr.t_begin; chunk < pr.t_end; chunk += 16) {
+        if (chunk != pr.t_begin) refresh_window(chunk);
 #pragma unroll
-        for (int i = 0; i < RAW; i++) {
-            kr[i] = kn[i];
-            vr[i] = vn[i];
+        for (int k2 = 0; k2 < 16; k2 += 2) {
+            const int tile = chunk + k2;
+            if (k2 > 0 && tile >= pr.t_end) break;
+            step(tile, ta);
+            step(tile + 1, tb);  // a tile past the partition end is fully masked
         }
-        ks = ksn;
-        vs = vsn;
+    }
     }
 
     float l_tot = l_run + shfl_xor(l_run, 16);
     l_tot += shfl_xor(l_tot, 32);
-    if (!head_ok) return;
-    if (pr.nparts == 1) {
-        const float inv = 1.0f / l_tot;
-        f16 *op = out + (c.out_row * H + h) * (int64_t)HD + 4 * grp;
+
+    // Merge the waves' states.  The merge area overlays the V tiles, so every
+    // wave must be done with its tiles first.
+    __syncthreads();
+    float *mo = reinterpret_cast<float *>(smem);  // [NW][16][HD]
+    if (head_ok) {
+        float *dst = mo + (wave * 16 + row) * HD + 4 * grp;
 #pragma unroll
-        for (int i = 0; i < NO; i++) {
+        for (int i = 0; i < NO; i++) *reinterpret_cast<f32x4 *>(dst + 16 * i) = o[i];
+        if (grp == 0) {
+            sm_ml[wave][row][0] = m_run;
+            sm_ml[wave][row][1] = l_tot;
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x * 4; idx < G * HD; idx += 64 * NW * 4) {
+        const int hh = idx / HD, d = idx % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_ml[w][hh][0]);
+        float den = 0.0f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float mw = sm_ml[w][hh][0];
+            const float wt = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+            den += wt * sm_ml[w][hh][1];
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(mo + (w * 16 + hh) * HD + d);
+#pragma unroll
+            for (int q = 0; q < 4; q++) acc[q] += wt * v[q];
+        }
+        const int hq = kvh * G + hh;
+        if (wg.nparts == 1) {
+            const float inv = 1.0f / den;
             f16x4 v;
 #pragma unroll
-            for (int q = 0; q < 4; q++) v[q] = (f16)(o[i][q] * inv);
-            *reinterpret_cast<f16x4 *>(op + 16 * i) = v;
+            for (int q = 0; q < 4; q++) v[q] = (f16)(acc[q] * inv);
+            *reinterpret_cast<f16x4 *>(out + (c.out_row * H + hq) * (int64_t)HD + d) = v;
+        } else {
+            const int64_t slot = ((int64_t)r * H + hq) * p.max_parts + part;
+            *reinterpret_cast<f32x4 *>(p.part_o + slot * HD + d) = (f32x4){acc[0], acc[1], acc[2], acc[3]};
+            if (d == 0) {
+                p.part_ml[slot * 2 + 0] = M;
+                p.part_ml[slot * 2 + 1] = den;
+            }
         }
-    } else {
-        const int64_t slot = ((int64_t)r * H + h) * p.max_parts + part;
-        float *po = p.part_o + slot * HD + 4 * grp;
-#pragma unroll
-        for (int i = 0; i < NO; i++) *reinterpret_cast<f32x4 *>(po + 16 * i) = o[i];
-        if (grp == 0) {
-            p.part_ml[slot * 2 + 0] = m_run;
-            p.part_ml[slot * 2 + 1] = l_tot;
+    }
+}
+
+template <typename KV, int HD, bool BS16>
+__global__ __launch_bounds__(64 * kMfmaWaves, HD >= 256 ? 1 : 3) void attn_mfma_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) char smem[MfmaShape<KV, HD>::kSmemBytes];
+    __shared__ float sm_ml[kMfmaWaves][16][2];
+    mfma_item<KV, HD, BS16>(p, blockIdx.z, blockIdx.x, blockIdx.y, smem, sm_ml);
+}
+
+// Persistent form: a grid sized to the resident capacity walks a compacted list
+// of items, (row, partition) major and kv head minor, so no workgroup is spent
+// on empty partitions of short rows and the wave slots stay full to the end.
+// Every workgroup builds the list's row prefix sums in LDS from the row ranges.
+template <typename KV, int HD, bool BS16>
+__global__ __launch_bounds__(64 * kMfmaWaves, HD >= 256 ? 1 : 3) void attn_mfma_persistent(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) char smem[MfmaShape<KV, HD>::kSmemBytes];
+    __shared__ float sm_ml[kMfmaWaves][16][2];
+    __shared__ int32_t prefix[kPersistentMaxRows + 1];
+    __shared__ int32_t chunk_sum[64 * kMfmaWaves];
+    constexpr int NT = 64 * kMfmaWaves;
+    const int tid = threadIdx.x;
+    const int rows = p.rows;
+    // each thread counts the items of a contiguous run of rows (a row with no
+    // keys still needs one item to write its 0/0 output)
+    const int per = (rows + NT - 1) / NT;
+    const int r0 = tid * per, r1 = r0 + per < rows ? r0 + per : rows;
+    int32_t run = 0;
+    for (int rr = r0; rr < r1; rr++) {
+        const int np = part_range(row_ctx(p, rr), 0, p.part_tokens).nparts;
+        prefix[rr] = run;
+        run += np > 1 ? np : 1;
+    }
+    chunk_sum[tid] = run;
+    __syncthreads();
+    // inclusive scan of the per-thread sums (Hillis-Steele)
+    for (int off = 1; off < NT; off <<= 1) {
+        const int32_t v = tid >= off ? chunk_sum[tid - off] : 0;
+        __syncthreads();
+        chunk_sum[tid] += v;
+        __syncthreads();
+    }
+    const int32_t base = tid > 0 ? chunk_sum[tid - 1] : 0;
+    for (int rr = r0; rr < r1; rr++) prefix[rr] += base;
+    if (tid == NT - 1) prefix[rows] = chunk_sum[NT - 1];
+    __syncthreads();
+    const int32_t total = prefix[rows] * p.num_kv_heads;
+    for (int32_t item = blockIdx.x; item < total; item += gridDim.x) {
+        const int32_t q = item / p.num_kv_heads;
+        const int kvh = item - q * p.num_kv_heads;
+        int lo = 0, hi = rows;  // last row with prefix[row] <= q
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (prefix[mid] <= q) lo = mid;
+            else hi = mid;
         }
+        __syncthreads();  // the previous item's LDS use is over
+        mfma_item<KV, HD, BS16>(p, lo, q - prefix[lo], kvh, smem, sm_ml);
     }
 }
 
@@ -365,8 +566,8 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnParams p, int lanes_p
     const KV *vpool = static_cast<const KV *>(p.v_pool);
     const int bs = p.block_size;
 
-    for (int64_t j0 = pr.t_begin * 16; j0 < pr.t_end * 16; j0 += TPI) {
-        const int64_t j = j0 + sub;
+    for (int j0 = pr.t_begin * 16; j0 < pr.t_end * 16; j0 += TPI) {
+        const int j = j0 + sub;
         const bool tok_ok = j >= c.k_lo && j < c.k_hi;
         float kv[4] = {0.f, 0.f, 0.f, 0.f}, vv[4] = {0.f, 0.f, 0.f, 0.f};
         if (tok_ok && dim_ok) {
@@ -465,11 +666,35 @@ bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group) {
 
 template <typename KV, int HD>
 static hipError_t launch_mfma_hd(const AttnParams &p, hipStream_t stream) {
-    dim3 grid(p.max_parts, p.num_kv_heads, p.rows);
+    const dim3 block(64 * kMfmaWaves);
+    if (p.rows <= kPersistentMaxRows) {
+        // resident capacity of the persistent kernel, queried once per instantiation
+        static int resident = 0;
+        if (resident == 0) {
+            int dev = 0, cus = 0, per_cu = 0;
+            hipError_t e = hipGetDevice(&dev);
+            if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+            if (e == hipSuccess)
+                e = p.block_size == 16 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                                             &per_cu, attn_mfma_persistent<KV, HD, true>, block.x, 0)
+                                       : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                                             &per_cu, attn_mfma_persistent<KV, HD, false>, block.x, 0);
+            if (e != hipSuccess) return e;
+            resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+        }
+        const int64_t upper = (int64_t)p.rows * p.max_parts * p.num_kv_heads;
+        const dim3 grid((unsigned)(upper < resident ? upper : resident));
+        if (p.block_size == 16)
+            hipLaunchKernelGGL((attn_mfma_persistent<KV, HD, true>), grid, block, 0, stream, p);
+        else
+            hipLaunchKernelGGL((attn_mfma_persistent<KV, HD, false>), grid, block, 0, stream, p);
+        return hipGetLastError();
+    }
+    const dim3 grid(p.max_parts, p.num_kv_heads, p.rows);
     if (p.block_size == 16)
-        hipLaunchKernelGGL((attn_mfma_kernel<KV, HD, true>), grid, dim3(64), 0, stream, p);
+        hipLaunchKernelGGL((attn_mfma_kernel<KV, HD, true>), grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL((attn_mfma_kernel<KV, HD, false>), grid, dim3(64), 0, stream, p);
+        hipLaunchKernelGGL((attn_mfma_kernel<KV, HD, false>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
 
@@ -503,6 +728,9 @@ static hipError_t launch_valu(const AttnParams &p, hipStream_t stream) {
 hipError_t launch_attention(const AttnParams &p, int32_t dtype, bool use_mfma, hipStream_t stream,
                             hipEvent_t after_main) {
     if (p.rows <= 0) return hipSuccess;
+    // masked lanes of the MFMA kernel read a lane-group slice of one token row
+    // from the zero page: it must exist and cover head_dim elements
+    if (p.zero_page == nullptr || (size_t)p.head_dim * 4 > kZeroPageBytes) return hipErrorInvalidValue;
     hipError_t e;
     if (use_mfma) {
         e = dtype == kF16 ? launch_mfma<f16>(p, stream) : launch_mfma<uint8_t>(p, stream);

@@ -11,6 +11,8 @@ namespace pam {
 enum DType : int32_t { kF32 = 0, kF16 = 1, kFP8 = 2 };
 
 constexpr float kLog2eHost = 1.4426950408889634f;
+// size of the all-zero device page the attention kernels read for masked lanes
+constexpr size_t kZeroPageBytes = 4096;
 
 // How a work row (one query token) finds its keys.
 enum RowMode : int32_t {
@@ -31,6 +33,7 @@ struct AttnParams {
     const int4 *row_info;          // ragged mode
     float *part_o;             // [rows][H][max_parts][d] split-context partial outputs
     float *part_ml;            // [rows][H][max_parts][2] (max in log2 units, sum)
+    const void *zero_page;     // >= 1 KiB of zeros: the source of masked lanes' loads
     int32_t rows;
     int32_t bt_stride;
     int32_t max_num_blocks;    // decode: logical blocks readable per row
@@ -93,6 +96,10 @@ hipError_t launch_fp8_quantize(const uint16_t *values, const uint16_t *scales, u
                                hipStream_t stream);
 hipError_t launch_fp8_dequant(const uint8_t *codes, const uint16_t *scales, uint16_t *out, int64_t n,
                               hipStream_t stream);
+
+// Calibration streams of known size (achievable HBM rates, counter scaling).
+hipError_t launch_stream_read(const void *src, size_t bytes, uint32_t *sink, int blocks, hipStream_t stream);
+hipError_t launch_stream_copy(const void *src, void *dst, size_t bytes, int blocks, hipStream_t stream);
 
 // Dense chunked-prefill (MFMA, f16): rows [q_offset, q_offset + T) of one sequence.
 hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream);

@@ -515,6 +515,10 @@ PAM_API int32_t pam_set_stream(void *context, void *hip_stream) {
     });
 }
 
+PAM_API int32_t pam_use_own_stream(void *context) {
+    return guarded(context, [&](Context *ctx) { ctx->use_own_stream(); });
+}
+
 PAM_API int32_t pam_set_synchronous(void *context, bool synchronous) {
     return guarded(context, [&](Context *ctx) { ctx->synchronous = synchronous; });
 }
@@ -557,6 +561,57 @@ PAM_API int32_t pam_fp8_quantize(void *context, const uint16_t *values, const ui
 PAM_API int32_t pam_fp8_dequant(void *context, const uint8_t *codes, const uint16_t *scales, uint16_t *out,
                                 int64_t n) {
     return guarded(context, [&](Context *ctx) { ctx->fp8_dequant(codes, scales, out, n); });
+}
+
+static int32_t calib_blocks(int32_t blocks) {
+    if (blocks > 0) return blocks;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                 hipSuccess)
+        cus = 256;
+    return 4 * cus;
+}
+
+PAM_API int32_t pam_calib_stream_read(void *context, const void *src, size_t bytes, int32_t blocks, float *ms) {
+    return guarded(context, [&](Context *ctx) {
+        ctx->ensure_device();
+        const int32_t nb = calib_blocks(blocks);
+        uint32_t *sink = static_cast<uint32_t *>(ctx->device_scratch(5, (size_t)nb * 4));
+        hipEvent_t a, b;
+        hip_check(hipEventCreate(&a), "hipEventCreate");
+        hip_check(hipEventCreate(&b), "hipEventCreate");
+        hip_check(hipEventRecord(a, ctx->stream()), "hipEventRecord");
+        hipError_t e = launch_stream_read(src, bytes, sink, nb, ctx->stream());
+        (void)hipEventRecord(b, ctx->stream());
+        (void)hipEventSynchronize(b);
+        float t = -1.0f;
+        (void)hipEventElapsedTime(&t, a, b);
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        hip_check(e, "stream read");
+        if (ms) *ms = t;
+    });
+}
+
+PAM_API int32_t pam_calib_stream_copy(void *context, const void *src, void *dst, size_t bytes, int32_t blocks,
+                                      float *ms) {
+    return guarded(context, [&](Context *ctx) {
+        ctx->ensure_device();
+        const int32_t nb = calib_blocks(blocks);
+        hipEvent_t a, b;
+        hip_check(hipEventCreate(&a), "hipEventCreate");
+        hip_check(hipEventCreate(&b), "hipEventCreate");
+        hip_check(hipEventRecord(a, ctx->stream()), "hipEventRecord");
+        hipError_t e = launch_stream_copy(src, dst, bytes, nb, ctx->stream());
+        (void)hipEventRecord(b, ctx->stream());
+        (void)hipEventSynchronize(b);
+        float t = -1.0f;
+        (void)hipEventElapsedTime(&t, a, b);
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        hip_check(e, "stream copy");
+        if (ms) *ms = t;
+    });
 }
 
 PAM_API int32_t pam_debug_fail_next_launches(void *context, int32_t n) {

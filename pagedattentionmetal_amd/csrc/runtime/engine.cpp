@@ -67,6 +67,7 @@ Context::~Context() {
     if (ev0_) (void)hipEventDestroy(ev0_);
     if (ev1_) (void)hipEventDestroy(ev1_);
     if (evmid_) (void)hipEventDestroy(evmid_);
+    if (zero_page_) (void)hipFree(zero_page_);
     if (staged_) (void)hipEventDestroy(staged_);
     if (own_stream_) (void)hipStreamDestroy(own_stream_);
 }
@@ -81,10 +82,13 @@ void Context::ensure_device() {
     hip_check(hipEventCreate(&ev1_), "hipEventCreate");
     hip_check(hipEventCreate(&evmid_), "hipEventCreate");
     hip_check(hipEventCreateWithFlags(&staged_, hipEventDisableTiming), "hipEventCreate");
+    // zeros that masked lanes of the attention kernels load instead of pool rows
+    hip_check(hipMalloc(&zero_page_, kZeroPageBytes), "hipMalloc zero page");
+    hip_check(hipMemset(zero_page_, 0, kZeroPageBytes), "hipMemset zero page");
     device_ready_ = true;
 }
 
-hipStream_t Context::stream() { return ext_stream_ ? ext_stream_ : own_stream_; }
+hipStream_t Context::stream() { return use_ext_stream_ ? ext_stream_ : own_stream_; }
 
 void Context::finish(const char *what) {
     hip_check(hipGetLastError(), what);
@@ -297,6 +301,7 @@ void Context::decode_gpu(const pam_decode_request &r) {
     p.mode = kRowDecode;
     p.heads_per_wave = nh;
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
+    p.zero_page = zero_page_;
 
     const int64_t cap_tokens = (int64_t)r.max_num_blocks * l.block_size;
     int64_t max_tiles = ceil_div(cap_tokens, 16);
@@ -374,6 +379,7 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
     p.causal = r.causal ? 1 : 0;
     p.mode = kRowPrefill;
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
+    p.zero_page = zero_page_;
 
     const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G) && decode_kernel_choice != 1;
     bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && decode_kernel_choice != 1;
@@ -566,6 +572,7 @@ void Context::mixed_step(const pam_mixed_request &r) {
     p.mode = kRowRagged;
     p.heads_per_wave = nh;
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
+    p.zero_page = zero_page_;
     const int64_t waves = (int64_t)total * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
     p.part_tokens = choose_part_tokens(waves, max_tiles + 1);
     p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles + 1, p.part_tokens / 16));

@@ -71,7 +71,14 @@ class Context {
     // --- device state (created on first GPU use)
     void ensure_device();
     hipStream_t stream();
-    void set_stream(hipStream_t s) { ext_stream_ = s; }
+    void set_stream(hipStream_t s) {
+        ext_stream_ = s;
+        use_ext_stream_ = true;
+    }
+    void use_own_stream() {
+        ext_stream_ = nullptr;
+        use_ext_stream_ = false;
+    }
     bool synchronous = true;
     void finish(const char *what);  // synchronise when synchronous, surface GPU errors
 
@@ -115,7 +122,9 @@ class Context {
     bool device_ready_ = false;
     int device_ = 0;
     hipStream_t own_stream_ = nullptr, ext_stream_ = nullptr;
+    bool use_ext_stream_ = false;
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr, evmid_ = nullptr, staged_ = nullptr;
+    void *zero_page_ = nullptr;
     bool stats_pending_ = false;
     bool stats_has_mid_ = false;
     DeviceBuffer workspace_;
