@@ -196,7 +196,7 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
     // Q^T B operand: lane holds Q[h][dim_of(c) .. +8] for chunk c
     f16x8 qv[NC];
     {
-        const f16 *qp = static_cast<const f16 *>(p.q) + ((int64_t)r * H + (head_ok ? h : 0)) * HD;
+        const f16 *qp = static_cast<const f16 *>(p.q) + ((int64_t)c.out_row * H + (head_ok ? h : 0)) * HD;
 #pragma unroll
         for (int i = 0; i < NC; i++) {
             f16x8 v = *reinterpret_cast<const f16x8 *>(qp + dim_of(i));
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnParams p, int lanes_p
 #pragma unroll
     for (int hh = 0; hh < NH; hh++) {
         if (dim_ok)
-            load4<QT>(static_cast<const QT *>(p.q) + ((int64_t)r * H + h0 + hh) * HD + d0, q[hh]);
+            load4<QT>(static_cast<const QT *>(p.q) + ((int64_t)c.out_row * H + h0 + hh) * HD + d0, q[hh]);
         else
             q[hh][0] = q[hh][1] = q[hh][2] = q[hh][3] = 0.0f;
     }

@@ -18,7 +18,7 @@ constexpr size_t kZeroPageBytes = 4096;
 enum RowMode : int32_t {
     kRowDecode = 0,   // row r = sequence r of a batch; keys [L - W, L) of seq_lengths[r]
     kRowPrefill = 1,  // row r = query position q_offset + r of one sequence (causal / fixed window)
-    kRowRagged = 2,   // row r described by row_info[r] = {bt_row, k_lo, k_hi, out_row}
+    kRowRagged = 2,   // row r described by row_info[r] = {bt_row, k_lo, k_hi, q/out row}
 };
 
 struct AttnParams {
@@ -43,6 +43,10 @@ struct AttnParams {
     int32_t max_parts;
     int32_t heads_per_wave;    // VALU kernel: query heads handled by one wave
     float scale_log2;          // log2(e) / sqrt(d)
+    // dense prefill kernel: one entry per sequence chunk {bt_row, q_offset, len, row_base}
+    const int4 *chunks;
+    int32_t num_chunks;
+    int32_t max_chunk_len;
 };
 
 // Paged attention over rows (decode / prefill-as-rows / ragged).  Chooses the

@@ -389,7 +389,11 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
     const int64_t max_tiles = ceil_div(kv_len, 16) + 1;
     int64_t tmp = 0;
     if (dense) {
-        p.part_tokens = (int32_t)(max_tiles * 16);
+        const int4 ch = make_int4(0, r.q_offset, r.seq_len, 0);
+        p.chunks = static_cast<const int4 *>(stage(4, &ch, sizeof(ch)));
+        p.num_chunks = 1;
+        p.max_chunk_len = r.seq_len;
+        p.bt_stride = 0;
         p.max_parts = 1;
     } else {
         const int64_t waves = (int64_t)r.seq_len * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
@@ -488,7 +492,11 @@ void Context::mixed_step(const pam_mixed_request &r) {
         throw invalid_configuration("FP8 mixed step needs the K and V scale pools.");
     ensure_device();
     const int32_t bs = l.block_size, W = l.window_size;
-    std::vector<int4> rows;
+    const int32_t G = l.num_heads / l.num_kv_heads;
+    // multi-token chunks go to the dense prefill kernel where it applies
+    const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G) && decode_kernel_choice != 1;
+    std::vector<int4> rows, chunks;
+    int64_t max_chunk = 0;
     std::vector<int32_t> cu(r.num_seqs + 1, 0);
     int64_t max_tiles = 1;
     for (int32_t s = 0; s < r.num_seqs; s++) {
@@ -497,26 +505,35 @@ void Context::mixed_step(const pam_mixed_request &r) {
         const int64_t kv_len = c + T;
         if (ceil_div(kv_len, bs) > r.bt_stride) throw buffer_too_small("blockTables row", ceil_div(kv_len, bs) * 4, (int64_t)r.bt_stride * 4);
         const int64_t ws = W > 0 ? std::max<int64_t>(0, kv_len - W) : 0;
+        if (dense && T > 1) {
+            chunks.push_back(make_int4(s, (int32_t)c, (int32_t)T, cu[s]));
+            max_chunk = std::max<int64_t>(max_chunk, T);
+            cu[s + 1] = cu[s] + (int32_t)T;
+            continue;
+        }
         for (int64_t i = 0; i < T; i++) {
             int4 ri;
             ri.x = s;
             ri.y = (int32_t)ws;
             ri.z = (int32_t)(c + i + 1);
-            ri.w = (int32_t)rows.size();
+            ri.w = cu[s] + (int32_t)i;
             rows.push_back(ri);
         }
         max_tiles = std::max<int64_t>(max_tiles, ceil_div(kv_len, 16) - ws / 16);
         cu[s + 1] = cu[s] + (int32_t)T;
     }
-    const int32_t total = (int32_t)rows.size();
+    const int32_t total = cu[r.num_seqs];
     if (total == 0) return;
-    const int32_t G = l.num_heads / l.num_kv_heads;
+    const int32_t ragged_rows = (int32_t)rows.size();
     bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && G >= 4;
     if (decode_kernel_choice == 1) use_mfma = false;
     const int32_t nh = heads_per_wave(G);
 
     // device-side descriptors
-    const int4 *d_rows = static_cast<const int4 *>(stage(0, rows.data(), rows.size() * sizeof(int4)));
+    const int4 *d_rows =
+        ragged_rows ? static_cast<const int4 *>(stage(0, rows.data(), rows.size() * sizeof(int4))) : nullptr;
+    const int4 *d_chunks =
+        chunks.empty() ? nullptr : static_cast<const int4 *>(stage(4, chunks.data(), chunks.size() * sizeof(int4)));
     AppendBatchParams ab{};
     std::vector<int2> tok;
     std::vector<int4> work;
@@ -561,7 +578,10 @@ void Context::mixed_step(const pam_mixed_request &r) {
     p.v_scale = r.v_scale;
     p.block_tables = r.block_tables;
     p.row_info = d_rows;
-    p.rows = total;
+    p.rows = ragged_rows;
+    p.chunks = d_chunks;
+    p.num_chunks = (int32_t)chunks.size();
+    p.max_chunk_len = (int32_t)max_chunk;
     p.bt_stride = r.bt_stride;
     p.max_num_blocks = r.bt_stride;
     p.num_heads = l.num_heads;
@@ -570,15 +590,16 @@ void Context::mixed_step(const pam_mixed_request &r) {
     p.block_size = bs;
     p.window = W;
     p.mode = kRowRagged;
+    p.causal = 1;  // prefill chunks are causal within the chunk (ragged rows carry it in k_hi)
     p.heads_per_wave = nh;
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
     p.zero_page = zero_page_;
-    const int64_t waves = (int64_t)total * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
+    const int64_t waves = (int64_t)ragged_rows * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
     p.part_tokens = choose_part_tokens(waves, max_tiles + 1);
     p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles + 1, p.part_tokens / 16));
     int64_t tmp = 0;
-    if (p.max_parts > 1) {
-        const int64_t slots = (int64_t)total * l.num_heads * p.max_parts;
+    if (ragged_rows > 0 && p.max_parts > 1) {
+        const int64_t slots = (int64_t)ragged_rows * l.num_heads * p.max_parts;
         tmp = slots * ((int64_t)l.head_dim + 2) * 4;
         reserve_workspace((size_t)tmp);
         p.part_o = static_cast<float *>(workspace_.ptr);
@@ -587,7 +608,11 @@ void Context::mixed_step(const pam_mixed_request &r) {
     with_retry("mixedStep", [&] {
         (void)hipEventRecord(ev0_, stream());
         if (ab.keys) check_launch(launch_append_batch(ab, l.data_type, stream()), "mixed append");
-        check_launch(launch_attention(p, l.data_type, use_mfma, stream(), evmid_), "mixed attention");
+        if (!chunks.empty()) check_launch(launch_prefill_mfma(p, stream()), "mixed prefill");
+        if (ragged_rows > 0)
+            check_launch(launch_attention(p, l.data_type, use_mfma, stream(), evmid_), "mixed attention");
+        else
+            (void)hipEventRecord(evmid_, stream());
         (void)hipEventRecord(ev1_, stream());
         finish("mixed step");
     });

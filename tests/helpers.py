@@ -16,6 +16,16 @@ def row_rel_err(out, ref):
     return float((num / den).max())
 
 
+def worst_rows(out, ref, rows_of=None, k=5):
+    """Indices (of [..., H, d] rows flattened to [N, H]) with the largest relative errors."""
+    h, d = ref.shape[-2], ref.shape[-1]
+    out = np.asarray(out, np.float64).reshape(-1, h, d)
+    ref = np.asarray(ref, np.float64).reshape(-1, h, d)
+    e = np.abs(out - ref).max(axis=2) / np.maximum(np.abs(ref).max(axis=2), 1e-6)
+    idx = np.argsort(e, axis=None)[::-1][:k]
+    return [(int(i // h), int(i % h), float(e.flat[i])) for i in idx]
+
+
 def np_dtype(dtype):
     return {0: np.float32, 1: np.float16, 2: np.float16}[dtype]
 

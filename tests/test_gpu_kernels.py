@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import TOL, make_case, row_rel_err, to_dev, to_host
+from helpers import TOL, make_case, row_rel_err, to_dev, to_host, worst_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -186,7 +186,7 @@ def test_decode_parity(engine, case):
                             k_scale=None if ks is None else ks.view(np.uint16),
                             v_scale=None if vs is None else vs.view(np.uint16), n_threads=8)
         err = row_rel_err(to_host(out), ref)
-        assert err <= TOL[dtype], f"rel err {err:.3e}"
+        assert err <= TOL[dtype], f"rel err {err:.3e}; worst (row, head, err): {worst_rows(to_host(out), ref)}"
     finally:
         engine.set_decode_kernel(0)
         engine.set_partition_tokens(0)
@@ -214,6 +214,12 @@ PREFILL_CASES = [
     (33, 17, 8, 8, 128, 8, 0, True, 0),
     (50, 30, 32, 8, 128, 16, 1, True, 48),  # fixed window start
     (16, 0, 4, 2, 64, 16, 2, False, 0),     # fp8 prefill
+    # dense MFMA prefill kernel (f16, d=128): long chunks, every group size
+    (300, 1000, 32, 8, 128, 16, 1, True, 0),
+    (130, 0, 16, 1, 128, 16, 1, True, 0),   # G = 16
+    (77, 5, 8, 8, 128, 16, 1, False, 0),    # G = 1, full attention
+    (200, 64, 64, 8, 128, 32, 1, True, 100),  # G = 8, window cuts inside the chunk
+    (97, 13, 16, 8, 128, 16, 1, True, 0),   # G = 2
 ]
 
 
@@ -312,4 +318,4 @@ def test_mixed_step_parity(engine, dtype):
     if dtype == 2:
         assert np.array_equal(to_host(ksd).view(np.uint16), ks.view(np.uint16))
     err = row_rel_err(to_host(out), ref)
-    assert err <= TOL[dtype], f"rel err {err:.3e}"
+    assert err <= TOL[dtype], f"rel err {err:.3e}; worst (row, head, err): {worst_rows(to_host(out), ref)}"
