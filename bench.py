@@ -96,6 +96,64 @@ def time_decode(torch, eng, w, t, steps, warmup):
     return ms, kern_ms, red_ms
 
 
+def mixed_setup(torch, api, workloads):
+    """Device tensors for the c3 mixed step: cached context in the pool, new tokens to append."""
+    w = workloads.mixed_config()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(w.seed)
+    shape = (w.pool_blocks, w.block_size, w.num_kv_heads, w.head_dim)
+    kp = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
+    vp = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
+    rows = w.total_rows
+    q = torch.randn((rows, w.num_heads, w.head_dim), generator=g, device="cuda", dtype=torch.float32).half()
+    nk = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
+    nv = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
+    bt = torch.from_numpy(w.block_tables).cuda()
+    out = torch.empty_like(q)
+    eng = api.PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    layer = api.PagedLayerSpec(w.head_dim, w.num_heads, w.num_kv_heads, w.block_size, 1)
+    return w, eng, (q, kp, vp, bt, nk, nv, out, layer)
+
+
+def time_mixed(torch, eng, w, t, steps, warmup):
+    """Whole mixed step (append + prefill chunks + decode rows), then the prefill
+    chunks alone (the dense prefill kernel, timed by the engine's HIP events)."""
+    q, kp, vp, bt, nk, nv, out, layer = t
+    stream = torch.cuda.current_stream()
+    eng.set_stream(stream)
+    eng.synchronous = False
+    ctx, ql = w.context_lens, w.query_lens
+    nch = int((ql > 1).sum())
+    rows_ch = int(ql[:nch].sum())
+
+    def step():
+        eng.mixed_step(q, out, kp, vp, bt, ctx, ql, layer, new_keys=nk, new_values=nv)
+
+    def prefill_only():
+        eng.mixed_step(q[:rows_ch], out[:rows_ch], kp, vp, bt[:nch], ctx[:nch], ql[:nch], layer)
+
+    assert (ql[:nch] > 1).all() and (ql[nch:] == 1).all()
+    for _ in range(max(warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    for _ in range(max(warmup, 1)):
+        prefill_only()
+    kern = []
+    for _ in range(steps):
+        prefill_only()
+        kern.append(eng.last_stats["kernel_ms"])
+    torch.cuda.synchronize()
+    return ms, sum(kern) / len(kern)
+
+
 def cpu_baseline_decode(torch, w, t, threads):
     """The oracle (C restatement of the reference's paged attention) on host cores."""
     import numpy as np
@@ -141,6 +199,15 @@ def main():
     achieved = kv / (kern_ms * 1e-3) / 1e9
     log(f"bench: c2 {ms:.4f} ms/step ({gbs:.1f} GB/s), decode kernel {kern_ms:.4f} ms, reduce {red_ms:.4f} ms")
 
+    log("bench: c3 mixed step setup")
+    w3, e3, t3 = mixed_setup(torch, api, workloads)
+    ms3, pk_ms = time_mixed(torch, e3, w3, t3, args.steps, args.warmup)
+    pflops = w3.prefill_flops()
+    tflops = pflops / (pk_ms * 1e-3) / 1e12
+    log(f"bench: c3 mixed step {ms3:.4f} ms; prefill kernel {pk_ms:.4f} ms = {tflops:.1f} TFLOP/s")
+    del t3, e3
+    torch.cuda.empty_cache()
+
     traffic = None
     tp = os.path.join(ROOT, "profiles", "decode_c2_traffic.json")
     if os.path.exists(tp):
@@ -180,6 +247,14 @@ def main():
                      "kernel": "attn_mfma_kernel<f16,128,bs16>", "kernel_ms": round(kern_ms, 5),
                      "reduce_ms": round(red_ms, 5)},
         "cpu_baseline": cpu,
+        "prefill": {"workload": "c3: mixed continuous-batching step, 8 chunks x 512 new tokens (context "
+                                "U[0,3584], causal) + 56 decodes (context U[256,4096]), 32 q / 8 kv heads, "
+                                "d=128, bs=16, fp16, append of the new K/V included in the step",
+                    "mixed_step_ms": round(ms3, 5),
+                    "tokens_per_s": round(w3.total_rows / (ms3 * 1e-3), 1),
+                    "prefill_kernel": "prefill_mfma_kernel<128>", "prefill_kernel_ms": round(pk_ms, 5),
+                    "flops_per_launch": pflops, "tflops": round(tflops, 2), "peak_tflops": FP16_PEAK_TFLOPS,
+                    "frac": round(tflops / FP16_PEAK_TFLOPS, 4)},
     }
 
     if args.all:

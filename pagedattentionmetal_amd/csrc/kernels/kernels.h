@@ -107,6 +107,6 @@ hipError_t launch_stream_copy(const void *src, void *dst, size_t bytes, int bloc
 
 // Dense chunked-prefill (MFMA, f16): rows [q_offset, q_offset + T) of one sequence.
 hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream);
-bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group);
+bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size);
 
 }  // namespace pam

@@ -381,7 +381,7 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
     p.zero_page = zero_page_;
 
-    const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G) && decode_kernel_choice != 1;
+    const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G, l.block_size) && decode_kernel_choice != 1;
     bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && decode_kernel_choice != 1;
     const int32_t nh = heads_per_wave(G);
     p.heads_per_wave = nh;
@@ -494,7 +494,7 @@ void Context::mixed_step(const pam_mixed_request &r) {
     const int32_t bs = l.block_size, W = l.window_size;
     const int32_t G = l.num_heads / l.num_kv_heads;
     // multi-token chunks go to the dense prefill kernel where it applies
-    const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G) && decode_kernel_choice != 1;
+    const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G, l.block_size) && decode_kernel_choice != 1;
     std::vector<int4> rows, chunks;
     int64_t max_chunk = 0;
     std::vector<int32_t> cu(r.num_seqs + 1, 0);
@@ -524,6 +524,9 @@ void Context::mixed_step(const pam_mixed_request &r) {
     }
     const int32_t total = cu[r.num_seqs];
     if (total == 0) return;
+    // longest chunks first: their workgroups are the slowest to finish
+    std::stable_sort(chunks.begin(), chunks.end(),
+                     [](const int4 &a, const int4 &b) { return a.y + a.z > b.y + b.z; });
     const int32_t ragged_rows = (int32_t)rows.size();
     bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && G >= 4;
     if (decode_kernel_choice == 1) use_mfma = false;

@@ -220,6 +220,7 @@ PREFILL_CASES = [
     (77, 5, 8, 8, 128, 16, 1, False, 0),    # G = 1, full attention
     (200, 64, 64, 8, 128, 32, 1, True, 100),  # G = 8, window cuts inside the chunk
     (97, 13, 16, 8, 128, 16, 1, True, 0),   # G = 2
+    (40, 9000, 8, 2, 128, 4, 1, True, 0),   # bs 4: block table streamed through LDS in segments
 ]
 
 
