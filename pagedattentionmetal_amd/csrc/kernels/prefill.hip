@@ -27,25 +27,51 @@
 namespace pam {
 
 constexpr int kPrefillWaves = 4;
+constexpr int kPrefillKT = 32;        // keys per tile
+constexpr int kPrefillBufs = 3;       // LDS ring: tile t computed, t+1 scored, t+2 being written
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 constexpr int kBtCache = 2048;        // block-table entries a workgroup keeps in LDS
 
-template <int HD, int NB, int KT>
-__global__ __launch_bounds__(64 * kPrefillWaves, NB >= 4 ? 1 : 2) void prefill_mfma_kernel(AttnParams p) {
+typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+// ds_read_b64_tr_b16: the 16 lanes of a group each address 4 consecutive halves
+// a[i][0..3]; lane o receives a[4j + o/4][o%4] for j = 0..3.
+__device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
+    const fp16x4_raw v =
+        __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) fp16x4_raw *)(p));
+    return __builtin_bit_cast(f16x4, v);
+}
+
+// LDS tiles.  K: rows of KL = HD + 8 halves (17 16-byte units), 16-byte piece
+// p of row r stored at p ^ 4*bit4(r): the 16 rows one S operand load touches
+// (rows 4h + n%4 + 8*(n/4)) then fall on 16 distinct bank groups.  V: rows of
+// VL = HD + 16 halves (18 units), piece p of row r at p ^ 8*bit3(r): the 8 rows
+// x 2 pieces each half-wave of a transposed load touches (rows 8g + 4r' + i/4)
+// fall on 16 distinct bank groups.  Both permutations flip a single address
+// bit, so every read is one of two per-lane bases plus an immediate offset.
+constexpr int kPrefillKL = 128 + 8;
+constexpr int kPrefillVL = 128 + 16;
+__device__ __forceinline__ int k_lds_at(int key, int piece) {
+    return key * kPrefillKL + ((piece ^ (((key >> 4) & 1) << 2)) << 3);
+}
+__device__ __forceinline__ int v_lds_at(int key, int piece) {
+    return key * kPrefillVL + ((piece ^ (((key >> 3) & 1) << 3)) << 3);
+}
+
+template <int HD, int NB>
+__global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_mfma_kernel(AttnParams p) {
+    static_assert(HD == 128, "the LDS swizzle assumes 16 pieces per row");
+    constexpr int KT = kPrefillKT;
     constexpr int NC = HD / 32;       // 16x16x32 chunks over d (S)
     constexpr int NO = HD / 16;       // 16-dim output chunks (PV)
     constexpr int SQ = KT / 16;       // 16-key quarters per tile (S)
-    constexpr int PH = KT / 32;       // 32-key halves per tile (PV)
-    constexpr int KL = HD + 8;        // K row in LDS (halves): 17 16-byte units for d = 128
-    constexpr int VS = KT + 8;        // V^T row in LDS (halves): an odd number of 16-byte units
     constexpr int PIECES = HD / 8;    // 16-byte pieces per token row
     constexpr int THREADS = 64 * kPrefillWaves;
     constexpr int PER_THREAD = KT * PIECES / THREADS;
-    static_assert(KT * PIECES % THREADS == 0, "tile must split evenly over the threads");
-    static_assert(KT == 32 || KT == 64, "tile of 32 or 64 keys");
     constexpr int ROWS = 16 * NB * kPrefillWaves;
-    __shared__ __attribute__((aligned(16))) f16 k_lds[2][KT * KL];
-    __shared__ __attribute__((aligned(16))) f16 v_lds[2][HD * VS];
+    static_assert(KT == 32 && THREADS % PIECES == 0 && KT * PIECES % THREADS == 0, "tile shape");
+    __shared__ __attribute__((aligned(16))) f16 k_lds[kPrefillBufs][KT * kPrefillKL];
+    __shared__ __attribute__((aligned(16))) f16 v_lds[kPrefillBufs][KT * kPrefillVL];
     __shared__ int32_t bt_lds[kBtCache];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, grp = lane >> 4;
@@ -83,40 +109,60 @@ __global__ __launch_bounds__(64 * kPrefillWaves, NB >= 4 ? 1 : 2) void prefill_m
         for (int c = 0; c < NC; c++) qv[b][c] = *reinterpret_cast<const f16x8 *>(qp + 32 * c);
     }
 
-    // staging map: element e = tid + i*THREADS -> key e % KT, piece e / KT
+    // staging map: element e = tid + i*THREADS -> key e / PIECES, piece e % PIECES
+    // (16 lanes read one key's 256 contiguous bytes)
     const int64_t row_stride = (int64_t)p.num_kv_heads * HD;
     const f16 *kpool = static_cast<const f16 *>(p.k_pool) + (int64_t)kvh * HD;
     const f16 *vpool = static_cast<const f16 *>(p.v_pool) + (int64_t)kvh * HD;
-    // K piece swizzle: rows 16..31 of every 32 use piece ^ 4, which spreads the
-    // 16 rows one S operand load touches over all 64 banks
-    auto kswz = [](int row, int piece) { return piece ^ (((row >> 4) & 1) << 2); };
+    const int my_piece = tid % PIECES;
     f16x8 kreg[PER_THREAD], vreg[PER_THREAD];
-    // the thread's key within a tile is the same for all its pieces (THREADS % KT == 0)
-    static_assert(THREADS % KT == 0, "one key per thread per tile");
-    const int my_key = tid % KT, my_piece = tid / KT;
     int blk0 = 0;  // first block of the block-table segment held in bt_lds
     auto fetch = [&](int tile) {
-        int j = tile * KT + my_key;
-        // keys outside [ws, kv_len) read the nearest key inside instead: finite
-        // data whose probability is zero after masking (and a block-table entry
-        // of the current segment)
-        j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
-        const uint32_t slot = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
-        const int64_t off = (int64_t)slot * row_stride + my_piece * 8;
 #pragma unroll
         for (int i = 0; i < PER_THREAD; i++) {
-            kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off + i * (THREADS / KT) * 8);
-            vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off + i * (THREADS / KT) * 8);
+            int j = tile * KT + tid / PIECES + i * (THREADS / PIECES);
+            // keys outside [ws, kv_len) read the nearest key inside instead: finite
+            // data whose probability is zero after masking (and a block-table entry
+            // of the current segment)
+            j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
+            const uint32_t slot = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
+            const int64_t off = (int64_t)slot * row_stride + my_piece * 8;
+            kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off);
+            vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off);
         }
     };
-    auto stage = [&](int s) {
+    auto stage = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < PER_THREAD; i++) {
-            const int e = tid + i * THREADS;
-            const int key = e % KT, piece = e / KT;
-            *reinterpret_cast<f16x8 *>(&k_lds[s][key * KL + kswz(key, piece) * 8]) = kreg[i];
+            const int key = tid / PIECES + i * (THREADS / PIECES);
+            *reinterpret_cast<f16x8 *>(&k_lds[buf][k_lds_at(key, my_piece)]) = kreg[i];
+            *reinterpret_cast<f16x8 *>(&v_lds[buf][v_lds_at(key, my_piece)]) = vreg[i];
+        }
+    };
+
+    // S^T for one tile: A-operand row n of quarter h holds key 8*(n/4) + 4h + n%4,
+    // so lane group g of that accumulator holds keys 8g + 4h + r: P slot 4h + r
+    const int krow0 = 8 * (n >> 2) + (n & 3);
+    // piece 4c + g of row krow0 + 4h: c even at base_e + 32c, c odd at base_o + 32c
+    const int kb4 = (krow0 >> 4) & 1;
+    const int k_base_e = krow0 * kPrefillKL + 8 * grp + 32 * kb4;
+    const int k_base_o = krow0 * kPrefillKL + 8 * grp - 32 * kb4;
+    auto score = [&](int buf, f32x4 (&sacc)[NB][SQ]) {
+        const f16 *kt = k_lds[buf];
 #pragma unroll
-            for (int q = 0; q < 8; q++) v_lds[s][(piece * 8 + q) * VS + key] = vreg[i][q];
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int q4 = 0; q4 < SQ; q4++) sacc[b][q4] = (f32x4)0.0f;
+#pragma unroll
+        for (int q4 = 0; q4 < SQ; q4++) {
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const int at = ((c & 1) ? k_base_o : k_base_e) + 4 * q4 * kPrefillKL + 32 * c;
+                const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[at]);
+#pragma unroll
+                for (int b = 0; b < NB; b++)
+                    sacc[b][q4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qv[b][c], sacc[b][q4], 0, 0, 0);
+            }
         }
     };
 
@@ -129,88 +175,17 @@ __global__ __launch_bounds__(64 * kPrefillWaves, NB >= 4 ? 1 : 2) void prefill_m
 #pragma unroll
         for (int i = 0; i < NO; i++) o[b][i] = (f32x4)0.0f;
     }
-
-    // A-operand row n of quarter (32-key half hh, sub-half h) holds key
-    // 32hh + 8*(n/4) + 4h + n%4, so lane group g of that accumulator holds keys
-    // 32hh + 8g + 4h + r: P slot 4h + r of half hh
-    const int krow0 = 8 * (n >> 2) + (n & 3);
     const float sl2 = p.scale_log2;
+    // transposed V loads: lane (n, g) addresses row 8g + 4r + n/4, dims
+    // 16i + 4*(n%4), i.e. piece 2i + (n%4)/2 at half offset 4*(n%2); pieces of
+    // i < 4 sit at v_base_lo + 16i, the others at v_base_hi + 16i (+ 4r rows)
+    const int vb3 = grp & 1;
+    const int v_row0 = (8 * grp + (n >> 2)) * kPrefillVL + 8 * ((n & 3) >> 1) + 4 * (n & 1);
+    const int v_base_lo = v_row0 + 64 * vb3;
+    const int v_base_hi = v_row0 - 64 * vb3;
+    const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 
-    auto body = [&](int tile, int s, auto masked) {
-        constexpr bool MASK = decltype(masked)::value;
-        const f16 *kt = k_lds[s];
-        const f16 *vt = v_lds[s];
-        f32x4 sacc[NB][SQ];
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int q4 = 0; q4 < SQ; q4++) sacc[b][q4] = (f32x4)0.0f;
-#pragma unroll
-        for (int q4 = 0; q4 < SQ; q4++) {
-            const int row = 32 * (q4 >> 1) + 4 * (q4 & 1) + krow0;
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[row * KL + kswz(row, 4 * c + grp) * 8]);
-#pragma unroll
-                for (int b = 0; b < NB; b++)
-                    sacc[b][q4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qv[b][c], sacc[b][q4], 0, 0, 0);
-            }
-        }
-
-        f16x8 pb[NB][PH];
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            if constexpr (MASK) {
-#pragma unroll
-                for (int q4 = 0; q4 < SQ; q4++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int j = tile * KT + 32 * (q4 >> 1) + 8 * grp + 4 * (q4 & 1) + r;
-                        const bool ok = j >= ws && j < kv_len && (!p.causal || j <= qpos[b]);
-                        sacc[b][q4][r] = ok ? sacc[b][q4][r] : -INFINITY;
-                    }
-            }
-            float lmax = sacc[b][0][0];
-#pragma unroll
-            for (int q4 = 0; q4 < SQ; q4++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) lmax = fmaxf(lmax, sacc[b][q4][r]);
-            // only when a score passes the reference by 2^8 (or there is none yet)
-            // is the row max formed and the reference raised
-            if (__any(lmax * sl2 > m_use[b] + kRescaleLog2)) {
-                float mt = lmax * sl2;
-                mt = fmaxf(mt, shfl_xor(mt, 16));
-                mt = fmaxf(mt, shfl_xor(mt, 32));
-                const float m_new = fmaxf(m_use[b], mt);
-                const float corr = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use[b] - m_new);
-                l_run[b] *= corr;
-#pragma unroll
-                for (int i = 0; i < NO; i++) o[b][i] *= corr;
-                m_use[b] = m_new;
-            }
-            const float mref = MASK ? (m_use[b] == -INFINITY ? 0.0f : m_use[b]) : m_use[b];
-            float psum = 0.0f;
-#pragma unroll
-            for (int q4 = 0; q4 < SQ; q4++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float pq = __builtin_amdgcn_exp2f(fmaf(sacc[b][q4][r], sl2, -mref));
-                    psum += pq;
-                    pb[b][q4 >> 1][4 * (q4 & 1) + r] = (f16)pq;
-                }
-            l_run[b] += psum;
-        }
-#pragma unroll
-        for (int i = 0; i < NO; i++)
-#pragma unroll
-            for (int hh = 0; hh < PH; hh++) {
-                const f16x8 va = *reinterpret_cast<const f16x8 *>(&vt[(16 * i + n) * VS + 32 * hh + 8 * grp]);
-#pragma unroll
-                for (int b = 0; b < NB; b++)
-                    o[b][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[b][hh], o[b][i], 0, 0, 0);
-            }
-    };
-
+    f32x4 sacc[NB][SQ], snext[NB][SQ];
     // tiles run in segments whose block-table entries fit in bt_lds (one segment
     // covers kBtCache * block_size keys, so long contexts only)
     const int seg_tiles = ((kBtCache - 1) << bsh) / KT;
@@ -218,22 +193,99 @@ __global__ __launch_bounds__(64 * kPrefillWaves, NB >= 4 ? 1 : 2) void prefill_m
         const int seg_end = min(t_hi, seg + seg_tiles);
         blk0 = (seg * KT) >> bsh;
         const int nblk = (((min(seg_end * KT, kv_len) - 1) >> bsh) - blk0) + 1;
-        __syncthreads();  // previous segment done with bt_lds and the stages
+        __syncthreads();  // previous segment done with bt_lds and the ring
         for (int i = tid; i < nblk; i += THREADS) bt_lds[i] = bt[blk0 + i];
         __syncthreads();
         fetch(seg);
         stage(0);
+        fetch(min(seg + 1, seg_end - 1));
+        stage(1);
+        fetch(min(seg + 2, seg_end - 1));
         __syncthreads();
+        score(0, sacc);
+        int buf = 0;
         for (int tile = seg; tile < seg_end; tile++) {
-            const int s = (tile - seg) & 1;
-            // the last tile re-fetches itself: keeps the loads unconditional
-            fetch(tile + 1 < seg_end ? tile + 1 : tile);
-            if (tile >= full_lo && tile < full_hi)
-                body(tile, s, std::false_type{});
-            else
-                body(tile, s, std::true_type{});
-            stage(s ^ 1);
+            const int b1 = buf == kPrefillBufs - 1 ? 0 : buf + 1;
+            const int b2 = b1 == kPrefillBufs - 1 ? 0 : b1 + 1;
+            // masks of edge tiles (window start, causal diagonal, end of keys)
+            if (!(tile >= full_lo && tile < full_hi)) {
+#pragma unroll
+                for (int b = 0; b < NB; b++)
+#pragma unroll
+                    for (int q4 = 0; q4 < SQ; q4++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const int j = tile * KT + 8 * grp + 4 * q4 + r;
+                            const bool ok = j >= ws && j < kv_len && (!p.causal || j <= qpos[b]);
+                            sacc[b][q4][r] = ok ? sacc[b][q4][r] : -INFINITY;
+                        }
+            }
+            // raise the reference max only when a score passes it by 2^8 (or
+            // there is none yet); the row max is formed only then
+            float lmax[NB];
+            bool need = false;
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                float mx = fmaxf(fmaxf(sacc[b][0][0], sacc[b][0][1]), fmaxf(sacc[b][0][2], sacc[b][0][3]));
+#pragma unroll
+                for (int q4 = 1; q4 < SQ; q4++)
+                    mx = fmaxf(mx, fmaxf(fmaxf(sacc[b][q4][0], sacc[b][q4][1]), fmaxf(sacc[b][q4][2], sacc[b][q4][3])));
+                lmax[b] = mx * sl2;
+                need |= lmax[b] > m_use[b] + kRescaleLog2;
+            }
+            if (__any(need)) {
+#pragma unroll
+                for (int b = 0; b < NB; b++) {
+                    float mt = lmax[b];
+                    mt = fmaxf(mt, shfl_xor(mt, 16));
+                    mt = fmaxf(mt, shfl_xor(mt, 32));
+                    const float m_new = fmaxf(m_use[b], mt);
+                    const float corr = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use[b] - m_new);
+                    l_run[b] *= corr;
+#pragma unroll
+                    for (int i = 0; i < NO; i++) o[b][i] *= corr;
+                    m_use[b] = m_new;
+                }
+            }
+            // scores of the next tile (overlaps the exponentials below)
+            score(b1, snext);
+            f16x8 pb[NB];
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                const float mref = m_use[b] == -INFINITY ? 0.0f : m_use[b];
+#pragma unroll
+                for (int q4 = 0; q4 < SQ; q4++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        pb[b][4 * q4 + r] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[b][q4][r], sl2, -mref));
+                // row sum of the f16 probabilities the MFMA consumes
+                float ps = l_run[b];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const f16x2 pr = {pb[b][2 * k], pb[b][2 * k + 1]};
+                    ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
+                }
+                l_run[b] = ps;
+            }
+            // O^T += V^T P^T
+            const f16 *vt = v_lds[buf];
+#pragma unroll
+            for (int i = 0; i < NO; i++) {
+                const int vb = (i < 4 ? v_base_lo : v_base_hi) + 16 * i;
+                const f16x4 lo = lds_read_tr16(vt + vb);
+                const f16x4 hi = lds_read_tr16(vt + vb + 4 * kPrefillVL);
+                const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+                for (int b = 0; b < NB; b++) o[b][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[b], o[b][i], 0, 0, 0);
+            }
+            stage(b2);
+            fetch(min(tile + 3, seg_end - 1));
             __syncthreads();
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int q4 = 0; q4 < SQ; q4++) sacc[b][q4] = snext[b][q4];
+            buf = b1;
         }
     }
 
@@ -260,7 +312,6 @@ __global__ __launch_bounds__(64 * kPrefillWaves, NB >= 4 ? 1 : 2) void prefill_m
 }
 
 constexpr int kPrefillNB = 2;
-constexpr int kPrefillKT = 32;
 
 bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size) {
     return dtype == kF16 && head_dim == 128 && group >= 1 && group <= 16 && (16 % group) == 0 && block_size > 0 &&
@@ -273,7 +324,7 @@ hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream) {
     if (!prefill_mfma_supported(kF16, p.head_dim, G, p.block_size)) return hipErrorInvalidValue;
     const int tok_per_wg = 16 * kPrefillNB * kPrefillWaves / G;
     dim3 grid((p.max_chunk_len + tok_per_wg - 1) / tok_per_wg, p.num_kv_heads, p.num_chunks);
-    hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillNB, kPrefillKT>), grid, dim3(64 * kPrefillWaves), 0, stream,
+    hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillNB>), grid, dim3(64 * kPrefillWaves), 0, stream,
                        p);
     return hipGetLastError();
 }
