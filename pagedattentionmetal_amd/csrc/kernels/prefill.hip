@@ -42,20 +42,24 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
     return __builtin_bit_cast(f16x4, v);
 }
 
-// LDS tiles.  K: rows of KL = HD + 8 halves (17 16-byte units), 16-byte piece
-// p of row r stored at p ^ 4*bit4(r): the 16 rows one S operand load touches
-// (rows 4h + n%4 + 8*(n/4)) then fall on 16 distinct bank groups.  V: rows of
-// VL = HD + 16 halves (18 units), piece p of row r at p ^ 8*bit3(r): the 8 rows
-// x 2 pieces each half-wave of a transposed load touches (rows 8g + 4r' + i/4)
-// fall on 16 distinct bank groups.  Both permutations flip a single address
-// bit, so every read is one of two per-lane bases plus an immediate offset.
-constexpr int kPrefillKL = 128 + 8;
+// LDS tiles (layouts chosen by measuring SQ_LDS_BANK_CONFLICT on gfx950).
+// K: unpadded rows of 128 halves, 16-byte piece p of row r stored at
+// p ^ (r%4 + 4*((r/8)%4)); the S operand loads (rows 4h + n%4 + 8*(n/4)) are
+// then conflict free, and each lane reads chunk c at one of four bases.
+// V: rows of VL = HD + 16 halves, piece p of row r at p ^ 8*bit3(r), which
+// keeps the transposed loads (rows 8g + 4r' + i/4) conflict free with two bases.
+constexpr int kPrefillKL = 128;
 constexpr int kPrefillVL = 128 + 16;
 __device__ __forceinline__ int k_lds_at(int key, int piece) {
-    return key * kPrefillKL + ((piece ^ (((key >> 4) & 1) << 2)) << 3);
+    return key * kPrefillKL + ((piece ^ ((key & 3) + 4 * ((key >> 3) & 3))) << 3);
 }
 __device__ __forceinline__ int v_lds_at(int key, int piece) {
     return key * kPrefillVL + ((piece ^ (((key >> 3) & 1) << 3)) << 3);
+}
+
+// three-way maximum (v_maximum3_f32); scores are never NaN
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
 template <int HD, int NB>
@@ -67,7 +71,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_mfma_kernel(Att
     constexpr int SQ = KT / 16;       // 16-key quarters per tile (S)
     constexpr int PIECES = HD / 8;    // 16-byte pieces per token row
     constexpr int THREADS = 64 * kPrefillWaves;
-    constexpr int PER_THREAD = KT * PIECES / THREADS;
+    constexpr int PER_THREAD = KT * PIECES / THREADS;  // 16-byte pieces per thread per pool
     constexpr int ROWS = 16 * NB * kPrefillWaves;
     static_assert(KT == 32 && THREADS % PIECES == 0 && KT * PIECES % THREADS == 0, "tile shape");
     __shared__ __attribute__((aligned(16))) f16 k_lds[kPrefillBufs][KT * kPrefillKL];
@@ -109,44 +113,46 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_mfma_kernel(Att
         for (int c = 0; c < NC; c++) qv[b][c] = *reinterpret_cast<const f16x8 *>(qp + 32 * c);
     }
 
-    // staging map: element e = tid + i*THREADS -> key e / PIECES, piece e % PIECES
-    // (16 lanes read one key's 256 contiguous bytes)
-    const int64_t row_stride = (int64_t)p.num_kv_heads * HD;
-    const f16 *kpool = static_cast<const f16 *>(p.k_pool) + (int64_t)kvh * HD;
-    const f16 *vpool = static_cast<const f16 *>(p.v_pool) + (int64_t)kvh * HD;
-    const int my_piece = tid % PIECES;
-    f16x8 kreg[PER_THREAD], vreg[PER_THREAD];
+    // staging map: 8 threads per key, thread piece p and p + 8 of it; the two
+    // keys of every 16-lane group are 8 apart, which keeps the LDS writes of a
+    // group on distinct bank groups
+    static_assert(PER_THREAD == 2 && THREADS / 8 == KT, "8 threads per key, two pieces each");
+    const int kk = tid >> 3, my_piece = tid & 7;
+    const int my_key = (kk & 16) | ((kk & 1) << 3) | ((kk >> 1) & 7);
+    const uint32_t row_stride = (uint32_t)(p.num_kv_heads * HD);  // halves per pool row (< 2^32)
+    const f16 *kpool = static_cast<const f16 *>(p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
+    const f16 *vpool = static_cast<const f16 *>(p.v_pool) + (int64_t)kvh * HD + my_piece * 8;
+    f16x8 kreg[2], vreg[2];
     int blk0 = 0;  // first block of the block-table segment held in bt_lds
     auto fetch = [&](int tile) {
-#pragma unroll
-        for (int i = 0; i < PER_THREAD; i++) {
-            int j = tile * KT + tid / PIECES + i * (THREADS / PIECES);
-            // keys outside [ws, kv_len) read the nearest key inside instead: finite
-            // data whose probability is zero after masking (and a block-table entry
-            // of the current segment)
-            j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
-            const uint32_t slot = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
-            const int64_t off = (int64_t)slot * row_stride + my_piece * 8;
-            kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off);
-            vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off);
-        }
+        int j = tile * KT + my_key;
+        // keys outside [ws, kv_len) read the nearest key inside instead: finite
+        // data whose probability is zero after masking (and a block-table entry
+        // of the current segment)
+        j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
+        const uint32_t slot = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
+        const uint64_t off = (uint64_t)slot * row_stride;
+        kreg[0] = *reinterpret_cast<const f16x8 *>(kpool + off);
+        kreg[1] = *reinterpret_cast<const f16x8 *>(kpool + off + 64);
+        vreg[0] = *reinterpret_cast<const f16x8 *>(vpool + off);
+        vreg[1] = *reinterpret_cast<const f16x8 *>(vpool + off + 64);
     };
+    const int k_st0 = k_lds_at(my_key, my_piece), k_st1 = k_lds_at(my_key, my_piece + 8);
+    const int v_st0 = v_lds_at(my_key, my_piece), v_st1 = v_lds_at(my_key, my_piece + 8);
     auto stage = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < PER_THREAD; i++) {
-            const int key = tid / PIECES + i * (THREADS / PIECES);
-            *reinterpret_cast<f16x8 *>(&k_lds[buf][k_lds_at(key, my_piece)]) = kreg[i];
-            *reinterpret_cast<f16x8 *>(&v_lds[buf][v_lds_at(key, my_piece)]) = vreg[i];
-        }
+        *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st0]) = kreg[0];
+        *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st1]) = kreg[1];
+        *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st0]) = vreg[0];
+        *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st1]) = vreg[1];
     };
 
     // S^T for one tile: A-operand row n of quarter h holds key 8*(n/4) + 4h + n%4,
     // so lane group g of that accumulator holds keys 8g + 4h + r: P slot 4h + r
     const int krow0 = 8 * (n >> 2) + (n & 3);
-    // piece 4c + g of row krow0 + 4h: c even at base_e + 32c, c odd at base_o + 32c
-    const int kb4 = (krow0 >> 4) & 1;
-    const int k_base_e = krow0 * kPrefillKL + 8 * grp + 32 * kb4;
-    const int k_base_o = krow0 * kPrefillKL + 8 * grp - 32 * kb4;
+    // piece 4c + g of row krow0 + 4h sits at k_base[c] + 4h rows
+    int k_base[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) k_base[c] = k_lds_at(krow0, 4 * c + grp);
     auto score = [&](int buf, f32x4 (&sacc)[NB][SQ]) {
         const f16 *kt = k_lds[buf];
 #pragma unroll
@@ -157,7 +163,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_mfma_kernel(Att
         for (int q4 = 0; q4 < SQ; q4++) {
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                const int at = ((c & 1) ? k_base_o : k_base_e) + 4 * q4 * kPrefillKL + 32 * c;
+                const int at = k_base[c] + 4 * q4 * kPrefillKL;
                 const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[at]);
 #pragma unroll
                 for (int b = 0; b < NB; b++)
@@ -226,10 +232,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_mfma_kernel(Att
             bool need = false;
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                float mx = fmaxf(fmaxf(sacc[b][0][0], sacc[b][0][1]), fmaxf(sacc[b][0][2], sacc[b][0][3]));
-#pragma unroll
-                for (int q4 = 1; q4 < SQ; q4++)
-                    mx = fmaxf(mx, fmaxf(fmaxf(sacc[b][q4][0], sacc[b][q4][1]), fmaxf(sacc[b][q4][2], sacc[b][q4][3])));
+                static_assert(SQ == 2, "eight scores per lane");
+                const float mx = vmax3(vmax3(sacc[b][0][0], sacc[b][0][1], sacc[b][0][2]),
+                                       vmax3(sacc[b][0][3], sacc[b][1][0], sacc[b][1][1]),
+                                       __builtin_elementwise_maximum(sacc[b][1][2], sacc[b][1][3]));
                 lmax[b] = mx * sl2;
                 need |= lmax[b] > m_use[b] + kRescaleLog2;
             }
