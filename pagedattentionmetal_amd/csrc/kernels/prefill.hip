@@ -5,32 +5,37 @@
 // pool (kernels.metal:693-917 semantics: scale 1/sqrt(d), GQA head h reads kv
 // head h / G, a fixed window start max(0, kv_len - W) for every row).
 //
-// A workgroup (4 waves) owns 64*NB query rows of one kv head: the (token, head)
-// pairs of 64*NB / G consecutive tokens, so the G query heads sharing a kv head
-// share every K/V tile.  Each wave owns NB blocks of 16 rows.  Per KT-key tile:
-//   * all 256 threads stage K (row-major, 16-byte pieces XOR-swizzled) and V
-//     (transposed, [dim][key]) into LDS; the next tile is fetched into
-//     registers while this one is computed;
-//   * S^T = K Q^T per 16-row block and 16-key quarter with
-//     v_mfma_f32_16x16x32_f16: K from LDS is the A operand, Q^T stays in
-//     registers as B.  The A rows are ordered so that, within every 32 keys, lane
-//     group g ends up holding keys 8g .. 8g+7, which is exactly the B-operand
-//     layout of O^T += V^T P^T (16x16x32 again, V^T read from the transposed LDS
-//     tile with one 16-byte load per lane);
+// Matrix work runs on v_mfma_f32_32x32x16_f16, which on gfx950 retires twice
+// the flops per cycle of the 16x16 shapes.  A workgroup (8 waves, one per CU)
+// owns 256 query rows of one kv head: the (token, head) pairs of 256 / G
+// consecutive tokens, so the G query heads sharing a kv head share every K/V
+// tile (the tile bytes per flop set the cache traffic); each wave owns 32 rows.  Per 32-key tile:
+//   * all 512 threads stage K and V rows into a 3-deep LDS ring (the next tiles
+//     are fetched into registers while earlier ones are computed);
+//   * S^T = K Q^T (32 keys x 32 rows, 8 MFMAs over d): K from LDS is the A
+//     operand, Q^T stays in registers as B.  The accumulator leaves lane (n, h)
+//     holding keys 8q + 4h + r (q, r < 4) of row n, and the 8 of them with q in
+//     {2c, 2c+1} are exactly the B operand of O^T += V^T P^T over key chunk c
+//     (16 keys), so P never leaves registers; V^T is read from LDS with the
+//     transposing ds_read_b64_tr_b16;
+//   * the scores of tile t+1 are formed while the probabilities of tile t are
+//     exponentiated, and O += V(t) P(t) runs while tile t+1 is masked and reduced;
 //   * softmax keeps a per-row reference max that is only raised (and O rescaled)
 //     when some score exceeds it by more than 2^8, so P is bounded by 2^8 and
-//     goes to the MFMA in f16; the common case needs no cross-lane reduction;
-//   * tiles wholly inside [window start, causal limit) run a mask-free body.
+//     goes to the MFMA in f16; the common case needs no cross-lane reduction.
 #include "kernels.h"
 #include "pam_device.h"
 
 namespace pam {
 
-constexpr int kPrefillWaves = 4;
-constexpr int kPrefillKT = 32;        // keys per tile
-constexpr int kPrefillBufs = 3;       // LDS ring: tile t computed, t+1 scored, t+2 being written
-constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
-constexpr int kBtCache = 2048;        // block-table entries a workgroup keeps in LDS
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kPrefillWaves = 8;
+constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows per workgroup
+constexpr int kPrefillKT = 32;                     // keys per tile
+constexpr int kPrefillBufs = 3;                    // LDS ring: t computed, t+1 scored, t+2 written
+constexpr float kRescaleLog2 = 8.0f;               // lazy-rescale threshold (log2 units)
+constexpr int kBtCache = 2048;                     // block-table entries a workgroup keeps in LDS
 
 typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
@@ -42,19 +47,16 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
     return __builtin_bit_cast(f16x4, v);
 }
 
-// LDS tiles (layouts chosen by measuring SQ_LDS_BANK_CONFLICT on gfx950).
-// K: unpadded rows of 128 halves, 16-byte piece p of row r stored at
-// p ^ (r%4 + 4*((r/8)%4)); the S operand loads (rows 4h + n%4 + 8*(n/4)) are
-// then conflict free, and each lane reads chunk c at one of four bases.
-// V: rows of VL = HD + 16 halves, piece p of row r at p ^ 8*bit3(r), which
-// keeps the transposed loads (rows 8g + 4r' + i/4) conflict free with two bases.
-constexpr int kPrefillKL = 128;
-constexpr int kPrefillVL = 128 + 16;
-__device__ __forceinline__ int k_lds_at(int key, int piece) {
-    return key * kPrefillKL + ((piece ^ ((key & 3) + 4 * ((key >> 3) & 3))) << 3);
-}
+// LDS tiles (layouts checked against SQ_LDS_BANK_CONFLICT on gfx950).
+// K: rows of 128 + 8 halves, so the 16 consecutive rows one 16-lane pass of an
+// operand load touches fall on 16 distinct 16-byte bank groups.
+// V: rows of 128 halves, 16-byte piece p of row r stored at p ^ 4*(r%4): the 4
+// rows x 64 bytes of each 32-lane pass of a transposed load cover all banks once.
+constexpr int kPrefillKL = 128 + 8;
+constexpr int kPrefillVL = 128;
+__device__ __forceinline__ int k_lds_at(int key, int piece) { return key * kPrefillKL + (piece << 3); }
 __device__ __forceinline__ int v_lds_at(int key, int piece) {
-    return key * kPrefillVL + ((piece ^ (((key >> 3) & 1) << 3)) << 3);
+    return key * kPrefillVL + ((piece ^ ((key & 3) << 2)) << 3);
 }
 
 // three-way maximum (v_maximum3_f32); scores are never NaN
@@ -62,26 +64,25 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
     return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
-template <int HD, int NB>
-__global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_mfma_kernel(AttnParams p) {
-    static_assert(HD == 128, "the LDS swizzle assumes 16 pieces per row");
+template <int HD>
+__global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(AttnParams p) {
+    static_assert(HD == 128, "layouts assume d = 128");
     constexpr int KT = kPrefillKT;
-    constexpr int NC = HD / 32;       // 16x16x32 chunks over d (S)
-    constexpr int NO = HD / 16;       // 16-dim output chunks (PV)
-    constexpr int SQ = KT / 16;       // 16-key quarters per tile (S)
+    constexpr int DC = HD / 16;       // 16-wide d chunks (S operands)
+    constexpr int DT = HD / 32;       // 32-wide output dim tiles
     constexpr int PIECES = HD / 8;    // 16-byte pieces per token row
     constexpr int THREADS = 64 * kPrefillWaves;
-    constexpr int PER_THREAD = KT * PIECES / THREADS;  // 16-byte pieces per thread per pool
-    constexpr int ROWS = 16 * NB * kPrefillWaves;
-    static_assert(KT == 32 && THREADS % PIECES == 0 && KT * PIECES % THREADS == 0, "tile shape");
+    constexpr int KEYS_PER_PASS = THREADS / PIECES;  // 16 lanes per key row
+    constexpr int KPT = KT / KEYS_PER_PASS;          // keys per thread per tile
+    static_assert(KT % KEYS_PER_PASS == 0 && KPT <= 2, "whole keys per thread");
     __shared__ __attribute__((aligned(16))) f16 k_lds[kPrefillBufs][KT * kPrefillKL];
     __shared__ __attribute__((aligned(16))) f16 v_lds[kPrefillBufs][KT * kPrefillVL];
     __shared__ int32_t bt_lds[kBtCache];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, grp = lane >> 4;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
     const int4 ch = p.chunks[blockIdx.z];  // {bt_row, q_offset, len, row_base}
     const int G = p.num_heads / p.num_kv_heads, H = p.num_heads, kvh = blockIdx.y;
-    const int tok_per_wg = ROWS / G;
+    const int tok_per_wg = kPrefillRows / G;
     // heaviest (latest) token blocks first
     const int tok0 = (gridDim.x - 1 - blockIdx.x) * tok_per_wg;
     if (tok0 >= ch.z) return;
@@ -97,241 +98,219 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_mfma_kernel(Att
     int full_hi = kv_len / KT;
     if (p.causal) full_hi = min(full_hi, (ch.y + tok0 + 1) / KT);
 
-    // row of lane column n in block b: wave*16*NB + b*16 + n
-    int qpos[NB];
-    bool row_ok[NB];
-    f16x8 qv[NB][NC];
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        const int rr = wave * 16 * NB + b * 16 + n;
-        const int tok = tok0 + rr / G, head = rr % G;
-        row_ok[b] = tok < tok_end;
-        qpos[b] = ch.y + tok;
+    // this lane's query row (column n of the wave's 32)
+    const int rr = wave * 32 + n;
+    const int my_tok = tok0 + rr / G, my_head = rr % G;
+    const bool row_ok = my_tok < tok_end;
+    const int qpos = ch.y + my_tok;
+    f16x8 qv[DC];
+    {
         const f16 *qp = static_cast<const f16 *>(p.q) +
-                        ((int64_t)(ch.w + (row_ok[b] ? tok : tok0)) * H + kvh * G + head) * HD + grp * 8;
+                        ((int64_t)(ch.w + (row_ok ? my_tok : tok0)) * H + kvh * G + my_head) * HD + 8 * h;
 #pragma unroll
-        for (int c = 0; c < NC; c++) qv[b][c] = *reinterpret_cast<const f16x8 *>(qp + 32 * c);
+        for (int c = 0; c < DC; c++) qv[c] = *reinterpret_cast<const f16x8 *>(qp + 16 * c);
     }
 
-    // staging map: 8 threads per key, thread piece p and p + 8 of it; the two
-    // keys of every 16-lane group are 8 apart, which keeps the LDS writes of a
-    // group on distinct bank groups
-    static_assert(PER_THREAD == 2 && THREADS / 8 == KT, "8 threads per key, two pieces each");
-    const int kk = tid >> 3, my_piece = tid & 7;
-    const int my_key = (kk & 16) | ((kk & 1) << 3) | ((kk >> 1) & 7);
+    // staging map: thread -> piece tid % 16 of keys tid / 16 (+ THREADS / 16)
+    // (16 lanes read one key row's 256 contiguous bytes)
+    const int my_piece = tid % PIECES, my_key = tid / PIECES;
     const uint32_t row_stride = (uint32_t)(p.num_kv_heads * HD);  // halves per pool row (< 2^32)
     const f16 *kpool = static_cast<const f16 *>(p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
     const f16 *vpool = static_cast<const f16 *>(p.v_pool) + (int64_t)kvh * HD + my_piece * 8;
-    f16x8 kreg[2], vreg[2];
+    // two register sets in flight: a tile's rows are loaded two iterations
+    // before they are written to LDS
+    f16x8 kra[KPT], vra[KPT], krb[KPT], vrb[KPT];
     int blk0 = 0;  // first block of the block-table segment held in bt_lds
-    auto fetch = [&](int tile) {
-        int j = tile * KT + my_key;
-        // keys outside [ws, kv_len) read the nearest key inside instead: finite
-        // data whose probability is zero after masking (and a block-table entry
-        // of the current segment)
-        j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
-        const uint32_t slot = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
-        const uint64_t off = (uint64_t)slot * row_stride;
-        kreg[0] = *reinterpret_cast<const f16x8 *>(kpool + off);
-        kreg[1] = *reinterpret_cast<const f16x8 *>(kpool + off + 64);
-        vreg[0] = *reinterpret_cast<const f16x8 *>(vpool + off);
-        vreg[1] = *reinterpret_cast<const f16x8 *>(vpool + off + 64);
+    auto fetch = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+#pragma unroll
+        for (int i = 0; i < KPT; i++) {
+            int j = tile * KT + my_key + i * KEYS_PER_PASS;
+            // keys outside [ws, kv_len) read the nearest key inside instead: finite
+            // data whose probability is zero after masking (and a block-table entry
+            // of the current segment)
+            j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
+            const uint32_t slot = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
+            const uint64_t off = (uint64_t)slot * row_stride;
+            kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off);
+            vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off);
+        }
     };
-    const int k_st0 = k_lds_at(my_key, my_piece), k_st1 = k_lds_at(my_key, my_piece + 8);
-    const int v_st0 = v_lds_at(my_key, my_piece), v_st1 = v_lds_at(my_key, my_piece + 8);
-    auto stage = [&](int buf) {
-        *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st0]) = kreg[0];
-        *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st1]) = kreg[1];
-        *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st0]) = vreg[0];
-        *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st1]) = vreg[1];
-    };
-
-    // S^T for one tile: A-operand row n of quarter h holds key 8*(n/4) + 4h + n%4,
-    // so lane group g of that accumulator holds keys 8g + 4h + r: P slot 4h + r
-    const int krow0 = 8 * (n >> 2) + (n & 3);
-    // piece 4c + g of row krow0 + 4h sits at k_base[c] + 4h rows
-    int k_base[NC];
+    int k_st[KPT], v_st[KPT];
 #pragma unroll
-    for (int c = 0; c < NC; c++) k_base[c] = k_lds_at(krow0, 4 * c + grp);
-    auto score = [&](int buf, f32x4 (&sacc)[NB][SQ]) {
-        const f16 *kt = k_lds[buf];
+    for (int i = 0; i < KPT; i++) {
+        k_st[i] = k_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
+        v_st[i] = v_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
+    }
+    auto stage = [&](int buf, const f16x8(&kreg)[KPT], const f16x8(&vreg)[KPT]) {
 #pragma unroll
-        for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int q4 = 0; q4 < SQ; q4++) sacc[b][q4] = (f32x4)0.0f;
-#pragma unroll
-        for (int q4 = 0; q4 < SQ; q4++) {
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                const int at = k_base[c] + 4 * q4 * kPrefillKL;
-                const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[at]);
-#pragma unroll
-                for (int b = 0; b < NB; b++)
-                    sacc[b][q4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qv[b][c], sacc[b][q4], 0, 0, 0);
-            }
+        for (int i = 0; i < KPT; i++) {
+            *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st[i]]) = kreg[i];
+            *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st[i]]) = vreg[i];
         }
     };
 
-    float m_use[NB], l_run[NB];
-    f32x4 o[NB][NO];
+    // S^T: A operand of chunk c = K[key n][16c + 8h .. +7]
+    const int k_rd = k_lds_at(n, h);
+    auto score = [&](int buf, f32x16 &sc) {
+        const f16 *kt = k_lds[buf];
+        sc = (f32x16)0.0f;
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        m_use[b] = -INFINITY;
-        l_run[b] = 0.0f;
+        for (int c = 0; c < DC; c++) {
+            const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 16 * c]);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[c], sc, 0, 0, 0);
+        }
+    };
+    // V^T operand of dim tile dt, key chunk c: lane (o = lane % 16 of its 16-lane
+    // group, half hh = (lane / 16) % 2, h) reads row 16c + 4h + 8jj + o/4
+    // (jj = 0, 1) at dims 32dt + 16hh + 4(o%4): two transposed loads give keys
+    // 16c + 4h + {0..3, 8..11} of dim 32dt + 16hh + o, the P slot order
+    int v_rd[DT];
+    {
+        const int o = lane & 15, hh = (lane >> 4) & 1;
+        const int row = 4 * h + (o >> 2);
 #pragma unroll
-        for (int i = 0; i < NO; i++) o[b][i] = (f32x4)0.0f;
+        for (int dt = 0; dt < DT; dt++)
+            v_rd[dt] = v_lds_at(row, 4 * dt + 2 * hh + ((o & 3) >> 1)) + 4 * (o & 1);
     }
+
+    float m_use = -INFINITY, l_run = 0.0f;
+    f32x16 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = (f32x16)0.0f;
     const float sl2 = p.scale_log2;
-    // transposed V loads: lane (n, g) addresses row 8g + 4r + n/4, dims
-    // 16i + 4*(n%4), i.e. piece 2i + (n%4)/2 at half offset 4*(n%2); pieces of
-    // i < 4 sit at v_base_lo + 16i, the others at v_base_hi + 16i (+ 4r rows)
-    const int vb3 = grp & 1;
-    const int v_row0 = (8 * grp + (n >> 2)) * kPrefillVL + 8 * ((n & 3) >> 1) + 4 * (n & 1);
-    const int v_base_lo = v_row0 + 64 * vb3;
-    const int v_base_hi = v_row0 - 64 * vb3;
     const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 
-    f32x4 sacc[NB][SQ], snext[NB][SQ];
+    // accumulator register r holds key 8(r/4) + 4h + r%4 of the tile
+    float lmax = -INFINITY;
+    auto prepare = [&](int tile, f32x16 &sc) -> bool {
+        if (!(tile >= full_lo && tile < full_hi)) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int j = tile * KT + 8 * (r >> 2) + 4 * h + (r & 3);
+                const bool ok = j >= ws && j < kv_len && (!p.causal || j <= qpos);
+                sc[r] = ok ? sc[r] : -INFINITY;
+            }
+        }
+        float mx = vmax3(sc[0], sc[1], sc[2]);
+        mx = vmax3(mx, sc[3], sc[4]);
+        mx = vmax3(mx, sc[5], sc[6]);
+        mx = vmax3(mx, sc[7], sc[8]);
+        mx = vmax3(mx, sc[9], sc[10]);
+        mx = vmax3(mx, sc[11], sc[12]);
+        mx = vmax3(mx, sc[13], sc[14]);
+        lmax = __builtin_elementwise_maximum(mx, sc[15]) * sl2;
+        return lmax > m_use + kRescaleLog2;
+    };
+    // raise the reference max to the row max (rare: wave-uniform branch)
+    auto rescale = [&]() {
+        const float mt = fmaxf(lmax, shfl_xor(lmax, 32));
+        const float m_new = fmaxf(m_use, mt);
+        const float corr = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use - m_new);
+        l_run *= corr;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[dt] *= corr;
+        m_use = m_new;
+    };
+
+    f32x16 sacc, snext;
     // tiles run in segments whose block-table entries fit in bt_lds (one segment
     // covers kBtCache * block_size keys, so long contexts only)
-    const int seg_tiles = ((kBtCache - 1) << bsh) / KT;
+    // (an even number of tiles: the loop below runs tiles in pairs, and a segment
+    // of odd length gets one extra tile past the keys, fully masked)
+    const int seg_tiles = (((kBtCache - 1) << bsh) / KT) & ~1;
     for (int seg = t_lo; seg < t_hi; seg += seg_tiles) {
         const int seg_end = min(t_hi, seg + seg_tiles);
+        const int seg_pad = seg + ((seg_end - seg + 1) & ~1);
         blk0 = (seg * KT) >> bsh;
         const int nblk = (((min(seg_end * KT, kv_len) - 1) >> bsh) - blk0) + 1;
         __syncthreads();  // previous segment done with bt_lds and the ring
         for (int i = tid; i < nblk; i += THREADS) bt_lds[i] = bt[blk0 + i];
         __syncthreads();
-        fetch(seg);
-        stage(0);
-        fetch(min(seg + 1, seg_end - 1));
-        stage(1);
-        fetch(min(seg + 2, seg_end - 1));
+        fetch(seg, kra, vra);
+        stage(0, kra, vra);
+        fetch(min(seg + 1, seg_end - 1), kra, vra);
+        stage(1, kra, vra);
+        fetch(min(seg + 2, seg_end - 1), kra, vra);
+        fetch(min(seg + 3, seg_end - 1), krb, vrb);
         __syncthreads();
         score(0, sacc);
+        if (__any(prepare(seg, sacc))) rescale();
         int buf = 0;
-        for (int tile = seg; tile < seg_end; tile++) {
+        // iteration t: S(t+1) on MFMA while P(t) is exponentiated, then
+        // O += V(t) P(t) on MFMA while S(t+1) is masked and reduced
+        auto step = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
             const int b1 = buf == kPrefillBufs - 1 ? 0 : buf + 1;
             const int b2 = b1 == kPrefillBufs - 1 ? 0 : b1 + 1;
-            // masks of edge tiles (window start, causal diagonal, end of keys)
-            if (!(tile >= full_lo && tile < full_hi)) {
-#pragma unroll
-                for (int b = 0; b < NB; b++)
-#pragma unroll
-                    for (int q4 = 0; q4 < SQ; q4++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const int j = tile * KT + 8 * grp + 4 * q4 + r;
-                            const bool ok = j >= ws && j < kv_len && (!p.causal || j <= qpos[b]);
-                            sacc[b][q4][r] = ok ? sacc[b][q4][r] : -INFINITY;
-                        }
-            }
-            // raise the reference max only when a score passes it by 2^8 (or
-            // there is none yet); the row max is formed only then
-            float lmax[NB];
-            bool need = false;
-#pragma unroll
-            for (int b = 0; b < NB; b++) {
-                static_assert(SQ == 2, "eight scores per lane");
-                const float mx = vmax3(vmax3(sacc[b][0][0], sacc[b][0][1], sacc[b][0][2]),
-                                       vmax3(sacc[b][0][3], sacc[b][1][0], sacc[b][1][1]),
-                                       __builtin_elementwise_maximum(sacc[b][1][2], sacc[b][1][3]));
-                lmax[b] = mx * sl2;
-                need |= lmax[b] > m_use[b] + kRescaleLog2;
-            }
-            if (__any(need)) {
-#pragma unroll
-                for (int b = 0; b < NB; b++) {
-                    float mt = lmax[b];
-                    mt = fmaxf(mt, shfl_xor(mt, 16));
-                    mt = fmaxf(mt, shfl_xor(mt, 32));
-                    const float m_new = fmaxf(m_use[b], mt);
-                    const float corr = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use[b] - m_new);
-                    l_run[b] *= corr;
-#pragma unroll
-                    for (int i = 0; i < NO; i++) o[b][i] *= corr;
-                    m_use[b] = m_new;
-                }
-            }
-            // scores of the next tile (overlaps the exponentials below)
             score(b1, snext);
-            f16x8 pb[NB];
+            f16x8 pb[2];
+            {
+                const float mref = m_use == -INFINITY ? 0.0f : m_use;
 #pragma unroll
-            for (int b = 0; b < NB; b++) {
-                const float mref = m_use[b] == -INFINITY ? 0.0f : m_use[b];
-#pragma unroll
-                for (int q4 = 0; q4 < SQ; q4++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        pb[b][4 * q4 + r] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[b][q4][r], sl2, -mref));
+                for (int r = 0; r < 16; r++) pb[r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[r], sl2, -mref));
                 // row sum of the f16 probabilities the MFMA consumes
-                float ps = l_run[b];
+                float ps = l_run;
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const f16x2 pr = {pb[b][2 * k], pb[b][2 * k + 1]};
+                for (int k = 0; k < 8; k++) {
+                    const f16x2 pr = {pb[k >> 2][2 * (k & 3)], pb[k >> 2][2 * (k & 3) + 1]};
                     ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
                 }
-                l_run[b] = ps;
+                l_run = ps;
             }
             // O^T += V^T P^T
             const f16 *vt = v_lds[buf];
 #pragma unroll
-            for (int i = 0; i < NO; i++) {
-                const int vb = (i < 4 ? v_base_lo : v_base_hi) + 16 * i;
-                const f16x4 lo = lds_read_tr16(vt + vb);
-                const f16x4 hi = lds_read_tr16(vt + vb + 4 * kPrefillVL);
-                const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            for (int c = 0; c < 2; c++)
 #pragma unroll
-                for (int b = 0; b < NB; b++) o[b][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[b], o[b][i], 0, 0, 0);
-            }
-            stage(b2);
-            fetch(min(tile + 3, seg_end - 1));
+                for (int dt = 0; dt < DT; dt++) {
+                    const f16x4 lo = lds_read_tr16(vt + v_rd[dt] + 16 * c * kPrefillVL);
+                    const f16x4 hi = lds_read_tr16(vt + v_rd[dt] + (16 * c + 8) * kPrefillVL);
+                    const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], o[dt], 0, 0, 0);
+                }
+            // the last tile's successor is not scored: never let it move the reference
+            const bool need = prepare(tile + 1, snext) && tile + 1 < seg_pad;
+            stage(b2, kreg, vreg);
+            fetch(min(tile + 4, seg_end - 1), kreg, vreg);
             __syncthreads();
-#pragma unroll
-            for (int b = 0; b < NB; b++)
-#pragma unroll
-                for (int q4 = 0; q4 < SQ; q4++) sacc[b][q4] = snext[b][q4];
+            if (__any(need)) rescale();
+            sacc = snext;
             buf = b1;
+        };
+        for (int tile = seg; tile < seg_pad; tile += 2) {
+            step(tile, kra, vra);
+            step(tile + 1, krb, vrb);
         }
     }
 
-    // finish: l summed over the lane groups, O / l, rows in range only
-    f16 *out = static_cast<f16 *>(p.out);
+    // finish: l summed over the two lane halves, O / l, rows in range only
+    const float l = l_run + shfl_xor(l_run, 32);
+    if (!row_ok) return;
+    // no key in range (window past the row): 0/0, as the reference's m/l bookkeeping gives
+    const float inv = 1.0f / l;
+    f16 *op = static_cast<f16 *>(p.out) + ((int64_t)(ch.w + my_tok) * H + kvh * G + my_head) * HD + 4 * h;
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        float l = l_run[b] + shfl_xor(l_run[b], 16);
-        l += shfl_xor(l, 32);
-        if (!row_ok[b]) continue;
-        const int rr = wave * 16 * NB + b * 16 + n;
-        const int tok = tok0 + rr / G, head = rr % G;
-        // no key in range (window past the row): 0/0, as the reference's m/l bookkeeping gives
-        const float inv = 1.0f / l;
-        f16 *op = out + ((int64_t)(ch.w + tok) * H + kvh * G + head) * HD + 4 * grp;
+    for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-        for (int i = 0; i < NO; i++) {
+        for (int q = 0; q < 4; q++) {
             f16x4 v;
 #pragma unroll
-            for (int q = 0; q < 4; q++) v[q] = (f16)(o[b][i][q] * inv);
-            *reinterpret_cast<f16x4 *>(op + 16 * i) = v;
+            for (int r = 0; r < 4; r++) v[r] = (f16)(o[dt][4 * q + r] * inv);
+            *reinterpret_cast<f16x4 *>(op + 32 * dt + 8 * q) = v;
         }
-    }
 }
 
-constexpr int kPrefillNB = 2;
-
 bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size) {
-    return dtype == kF16 && head_dim == 128 && group >= 1 && group <= 16 && (16 % group) == 0 && block_size > 0 &&
-           (block_size & (block_size - 1)) == 0;
+    return dtype == kF16 && head_dim == 128 && group >= 1 && group <= 32 && (kPrefillRows % group) == 0 &&
+           block_size > 0 && (block_size & (block_size - 1)) == 0;
 }
 
 hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream) {
     if (p.chunks == nullptr || p.num_chunks <= 0 || p.max_chunk_len <= 0) return hipErrorInvalidValue;
     const int G = p.num_heads / p.num_kv_heads;
     if (!prefill_mfma_supported(kF16, p.head_dim, G, p.block_size)) return hipErrorInvalidValue;
-    const int tok_per_wg = 16 * kPrefillNB * kPrefillWaves / G;
+    const int tok_per_wg = kPrefillRows / G;
     dim3 grid((p.max_chunk_len + tok_per_wg - 1) / tok_per_wg, p.num_kv_heads, p.num_chunks);
-    hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillNB>), grid, dim3(64 * kPrefillWaves), 0, stream,
-                       p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<128>), grid, dim3(64 * kPrefillWaves), 0, stream, p);
     return hipGetLastError();
 }
 
