@@ -32,7 +32,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPrefillWaves = 8;
 constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows per workgroup
-constexpr int kPrefillKT = 32;                     // keys per tile
+constexpr int kPrefillKT = 64;                     // keys per tile
 constexpr int kPrefillBufs = 3;                    // LDS ring: t computed, t+1 scored, t+2 written
 constexpr float kRescaleLog2 = 8.0f;               // lazy-rescale threshold (log2 units)
 constexpr int kBtCache = 2048;                     // block-table entries a workgroup keeps in LDS
@@ -68,6 +68,7 @@ template <int HD>
 __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(AttnParams p) {
     static_assert(HD == 128, "layouts assume d = 128");
     constexpr int KT = kPrefillKT;
+    constexpr int KH = KT / 32;       // 32-key score blocks per tile
     constexpr int DC = HD / 16;       // 16-wide d chunks (S operands)
     constexpr int DT = HD / 32;       // 32-wide output dim tiles
     constexpr int PIECES = HD / 8;    // 16-byte pieces per token row
@@ -151,13 +152,16 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
 
     // S^T: A operand of chunk c = K[key n][16c + 8h .. +7]
     const int k_rd = k_lds_at(n, h);
-    auto score = [&](int buf, f32x16 &sc) {
+    auto score = [&](int buf, f32x16(&sc)[KH]) {
         const f16 *kt = k_lds[buf];
-        sc = (f32x16)0.0f;
 #pragma unroll
-        for (int c = 0; c < DC; c++) {
-            const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 16 * c]);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[c], sc, 0, 0, 0);
+        for (int e = 0; e < KH; e++) {
+            sc[e] = (f32x16)0.0f;
+#pragma unroll
+            for (int c = 0; c < DC; c++) {
+                const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * kPrefillKL + 16 * c]);
+                sc[e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[c], sc[e], 0, 0, 0);
+            }
         }
     };
     // V^T operand of dim tile dt, key chunk c: lane (o = lane % 16 of its 16-lane
@@ -180,25 +184,27 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
     const float sl2 = p.scale_log2;
     const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 
-    // accumulator register r holds key 8(r/4) + 4h + r%4 of the tile
+    // accumulator register r of block e holds key 32e + 8(r/4) + 4h + r%4 of the tile
     float lmax = -INFINITY;
-    auto prepare = [&](int tile, f32x16 &sc) -> bool {
+    auto prepare = [&](int tile, f32x16(&sc)[KH]) -> bool {
         if (!(tile >= full_lo && tile < full_hi)) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int j = tile * KT + 8 * (r >> 2) + 4 * h + (r & 3);
-                const bool ok = j >= ws && j < kv_len && (!p.causal || j <= qpos);
-                sc[r] = ok ? sc[r] : -INFINITY;
-            }
+            for (int e = 0; e < KH; e++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int j = tile * KT + 32 * e + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const bool ok = j >= ws && j < kv_len && (!p.causal || j <= qpos);
+                    sc[e][r] = ok ? sc[e][r] : -INFINITY;
+                }
         }
-        float mx = vmax3(sc[0], sc[1], sc[2]);
-        mx = vmax3(mx, sc[3], sc[4]);
-        mx = vmax3(mx, sc[5], sc[6]);
-        mx = vmax3(mx, sc[7], sc[8]);
-        mx = vmax3(mx, sc[9], sc[10]);
-        mx = vmax3(mx, sc[11], sc[12]);
-        mx = vmax3(mx, sc[13], sc[14]);
-        lmax = __builtin_elementwise_maximum(mx, sc[15]) * sl2;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < KH; e++) {
+            mx = vmax3(mx, sc[e][0], sc[e][1]);
+#pragma unroll
+            for (int r = 2; r < 16; r += 2) mx = vmax3(mx, sc[e][r], sc[e][r + 1]);
+        }
+        lmax = mx * sl2;
         return lmax > m_use + kRescaleLog2;
     };
     // raise the reference max to the row max (rare: wave-uniform branch)
@@ -212,7 +218,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
         m_use = m_new;
     };
 
-    f32x16 sacc, snext;
+    f32x16 sacc[KH], snext[KH];
     // tiles run in segments whose block-table entries fit in bt_lds (one segment
     // covers kBtCache * block_size keys, so long contexts only)
     // (an even number of tiles: the loop below runs tiles in pairs, and a segment
@@ -242,15 +248,18 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             const int b1 = buf == kPrefillBufs - 1 ? 0 : buf + 1;
             const int b2 = b1 == kPrefillBufs - 1 ? 0 : b1 + 1;
             score(b1, snext);
-            f16x8 pb[2];
+            f16x8 pb[2 * KH];
             {
                 const float mref = m_use == -INFINITY ? 0.0f : m_use;
 #pragma unroll
-                for (int r = 0; r < 16; r++) pb[r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[r], sl2, -mref));
+                for (int e = 0; e < KH; e++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        pb[2 * e + (r >> 3)][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[e][r], sl2, -mref));
                 // row sum of the f16 probabilities the MFMA consumes
                 float ps = l_run;
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
+                for (int k = 0; k < 8 * KH; k++) {
                     const f16x2 pr = {pb[k >> 2][2 * (k & 3)], pb[k >> 2][2 * (k & 3) + 1]};
                     ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
                 }
@@ -259,7 +268,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             // O^T += V^T P^T
             const f16 *vt = v_lds[buf];
 #pragma unroll
-            for (int c = 0; c < 2; c++)
+            for (int c = 0; c < 2 * KH; c++)
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) {
                     const f16x4 lo = lds_read_tr16(vt + v_rd[dt] + 16 * c * kPrefillVL);
@@ -273,7 +282,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             fetch(min(tile + 4, seg_end - 1), kreg, vreg);
             __syncthreads();
             if (__any(need)) rescale();
-            sacc = snext;
+#pragma unroll
+            for (int e = 0; e < KH; e++) sacc[e] = snext[e];
             buf = b1;
         };
         for (int tile = seg; tile < seg_pad; tile += 2) {
