@@ -154,23 +154,35 @@ def time_mixed(torch, eng, w, t, steps, warmup):
     return ms, sum(kern) / len(kern)
 
 
-def cpu_baseline_decode(torch, w, t, threads):
-    """The oracle (C restatement of the reference's paged attention) on host cores."""
+def cpu_baseline_decode(torch, w, t, threads, batch=None, min_seconds=2.0, max_reps=5):
+    """The oracle (C restatement of the reference's paged attention) on host cores:
+    the first `batch` sequences of the step (all by default), repeated until
+    `min_seconds` of wall time (at most `max_reps` passes); returns GB/s and seconds."""
     import numpy as np
 
     import oracle
     q, kp, vp, bt, lens, out, layer, ks, vs = t
-    qh = q.cpu().numpy()
+    B = w.batch if batch is None else batch
+    qh = q[:B].cpu().numpy()
     if w.data_type == 2:
         kh, vh = kp.cpu().numpy(), vp.cpu().numpy()
         ksh, vsh = ks.cpu().numpy().view(np.uint16), vs.cpu().numpy().view(np.uint16)
     else:
         kh, vh, ksh, vsh = kp.cpu().numpy(), vp.cpu().numpy(), None, None
-    t0 = time.perf_counter()
-    oracle.decode(w.data_type, qh, kh, vh, w.block_tables, w.seq_lens, w.num_heads, window=w.window,
-                  k_scale=ksh, v_scale=vsh, n_threads=threads)
-    dt = time.perf_counter() - t0
-    return w.kv_bytes() / dt / 1e9, dt
+    L = w.seq_lens[:B].astype(np.int64)
+    if w.window > 0:
+        L = np.minimum(L, w.window)
+    elem = {0: 4, 1: 2, 2: 1}[w.data_type]
+    nbytes = int(L.sum()) * w.num_kv_heads * w.head_dim * 2 * elem
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.decode(w.data_type, qh, kh, vh, w.block_tables[:B], w.seq_lens[:B], w.num_heads, window=w.window,
+                      k_scale=ksh, v_scale=vsh, n_threads=threads)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds or reps >= max_reps:
+            break
+    return nbytes * reps / dt / 1e9, dt, reps
 
 
 def main():
@@ -180,6 +192,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--all", action="store_true", help="also measure c1, c4, c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run the 1 GiB read and copy calibration streams (achievable HBM rate; "
+                         "the byte counters of a profiling run are scaled by what they read on these)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the paged-attention path runs on a single GPU "
@@ -218,10 +233,14 @@ def main():
     if not args.no_cpu:
         threads = max(1, min(16, os.cpu_count() or 1))
         log(f"bench: CPU baseline (oracle, {threads} threads) on the full c2 batch")
-        cgbs, cdt = cpu_baseline_decode(torch, w, t, threads)
+        cgbs, cdt, creps = cpu_baseline_decode(torch, w, t, threads)
+        log(f"bench: CPU baseline single-threaded on the first 8 sequences")
+        sgbs, sdt, sreps = cpu_baseline_decode(torch, w, t, 1, batch=8)
         cpu = {"value": round(cgbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"one full c2 decode step (B=64, {kv / 1e9:.3f} GB of KV) through the C oracle, "
-                         f"OpenMP over (sequence, head), {cdt:.2f} s"}
+               "sample": f"{creps} x one full c2 decode step (B=64, {kv / 1e9:.3f} GB of KV) through the C "
+                         f"oracle, OpenMP over (sequence, head) on {threads} host threads, {cdt:.2f} s",
+               "single_thread": {"value": round(sgbs, 4), "unit": "GB/s", "cores": 1,
+                                 "sample": f"{sreps} x the first 8 sequences of the c2 step, {sdt:.2f} s"}}
     del t, eng
 
     result = {
@@ -244,7 +263,8 @@ def main():
                    "tokens_per_s": round(w.batch / (ms * 1e-3), 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "attn_mfma_kernel<f16,128,bs16>", "kernel_ms": round(kern_ms, 5),
+                     "kernel": "attn_mfma_persistent<f16,128,bs16> (split-context partials) + attn_reduce_kernel",
+                     "kernel_ms": round(kern_ms, 5),
                      "reduce_ms": round(red_ms, 5)},
         "cpu_baseline": cpu,
         "prefill": {"workload": "c3: mixed continuous-batching step, 8 chunks x 512 new tokens (context "
@@ -256,6 +276,19 @@ def main():
                     "flops_per_launch": pflops, "tflops": round(tflops, 2), "peak_tflops": FP16_PEAK_TFLOPS,
                     "frac": round(tflops / FP16_PEAK_TFLOPS, 4)},
     }
+
+    if args.calibrate:
+        import torch as _t
+        gib = 1 << 30
+        src = _t.empty(gib, dtype=_t.uint8, device="cuda").fill_(1)
+        dst = _t.empty_like(src)
+        ec = api.PagedAttentionEngine()
+        rd = min(ec.calib_stream_read(src) for _ in range(5))
+        cp = min(ec.calib_stream_copy(src, dst) for _ in range(5))
+        result["calibration"] = {"stream_read_GBps": round(gib / (rd * 1e-3) / 1e9, 1),
+                                 "stream_copy_GBps": round(2 * gib / (cp * 1e-3) / 1e9, 1),
+                                 "bytes": gib}
+        del src, dst
 
     if args.all:
         cfgs = {}

@@ -36,6 +36,7 @@ constexpr int kPrefillKT = 64;                     // keys per tile
 constexpr int kPrefillBufs = 3;                    // LDS ring: t computed, t+1 scored, t+2 written
 constexpr float kRescaleLog2 = 8.0f;               // lazy-rescale threshold (log2 units)
 constexpr int kBtCache = 2048;                     // block-table entries a workgroup keeps in LDS
+constexpr int kXcds = 8;                           // accelerator dies (each with its own L2)
 
 typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
@@ -81,11 +82,20 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
     __shared__ int32_t bt_lds[kBtCache];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
-    const int4 ch = p.chunks[blockIdx.z];  // {bt_row, q_offset, len, row_base}
-    const int G = p.num_heads / p.num_kv_heads, H = p.num_heads, kvh = blockIdx.y;
+    const int G = p.num_heads / p.num_kv_heads, H = p.num_heads;
     const int tok_per_wg = kPrefillRows / G;
-    // heaviest (latest) token blocks first
-    const int tok0 = (gridDim.x - 1 - blockIdx.x) * tok_per_wg;
+    // Workgroup -> (chunk, kv head, token block).  Workgroups are dispatched to
+    // the 8 XCDs round-robin by id, and each XCD has its own L2: all token
+    // blocks of one (chunk, kv head) get ids of one residue mod 8, so the K/V
+    // rows they share are fetched from HBM into one L2 only.  Chunks arrive
+    // longest first; within a group the latest (heaviest) token blocks go first.
+    const int nx = (p.max_chunk_len + tok_per_wg - 1) / tok_per_wg;
+    const int xcd = blockIdx.x & (kXcds - 1), r = blockIdx.x / kXcds;
+    const int grp = xcd + kXcds * (r / nx);
+    if (grp >= p.num_chunks * p.num_kv_heads) return;
+    const int4 ch = p.chunks[grp / p.num_kv_heads];  // {bt_row, q_offset, len, row_base}
+    const int kvh = grp % p.num_kv_heads;
+    const int tok0 = (nx - 1 - r % nx) * tok_per_wg;
     if (tok0 >= ch.z) return;
     const int32_t *bt = p.block_tables + (int64_t)ch.x * p.bt_stride;
     const int bsh = __builtin_ctz(p.block_size), bsm = p.block_size - 1;  // block_size is a power of two
@@ -319,7 +329,9 @@ hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream) {
     const int G = p.num_heads / p.num_kv_heads;
     if (!prefill_mfma_supported(kF16, p.head_dim, G, p.block_size)) return hipErrorInvalidValue;
     const int tok_per_wg = kPrefillRows / G;
-    dim3 grid((p.max_chunk_len + tok_per_wg - 1) / tok_per_wg, p.num_kv_heads, p.num_chunks);
+    const int nx = (p.max_chunk_len + tok_per_wg - 1) / tok_per_wg;
+    const int groups = p.num_chunks * p.num_kv_heads;
+    dim3 grid(kXcds * nx * ((groups + kXcds - 1) / kXcds));
     hipLaunchKernelGGL((prefill_mfma_kernel<128>), grid, dim3(64 * kPrefillWaves), 0, stream, p);
     return hipGetLastError();
 }
