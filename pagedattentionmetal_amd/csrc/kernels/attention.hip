@@ -110,58 +110,63 @@ __device__ __forceinline__ f16x8 e4m3x8_to_f16x8(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(f16x8, h);
 }
 
-// Chunk c (8 elements) of a lane's raw K/V slice as the MFMA operand / LDS row.
-//  f16: the bytes themselves.
-//  e4m3, per-tile scale (block size 16): exact value * 2^-8; the scale and 2^8
-//        are applied to S (keys) and folded into P (values) per tile.
-//  e4m3, per-token scale: the reference's half dequantisation per element.
-template <typename KV, bool kTileScale>
-__device__ __forceinline__ f16x8 operand_chunk(const uint4 *raw, int c, f16 scale) {
-    if constexpr (sizeof(KV) == 2) {
-        return __builtin_bit_cast(f16x8, raw[c]);
-    } else {
-        const uint32_t *w = reinterpret_cast<const uint32_t *>(raw) + c * 2;
-        if constexpr (kTileScale) {
-            return e4m3x8_to_f16x8(w[0], w[1]);
-        } else {
-            f16x8 o;
-#pragma unroll
-            for (int i = 0; i < 8; i++) o[i] = fp8_dequant((w[i >> 2] >> (8 * (i & 3))) & 0xFFu, scale);
-            return o;
-        }
-    }
-}
-
 // Waves per workgroup of the MFMA kernel: they split one partition's tiles and
 // merge their softmax states in LDS.
 constexpr int kMfmaWaves = 4;
 // Rows the persistent form can index from LDS (its item table).
 constexpr int kPersistentMaxRows = 2048;
 
+// How a 16-token tile finds its physical blocks.
+enum BlockMode : int {
+    kBlkTile = 0,   // block_size a power of two >= 16: the whole tile lies in one block
+    kBlkSmall = 1,  // block_size 8: two blocks per tile
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
+// ds_read_b64_tr_b16: the 16 lanes of a group each address 4 consecutive halves
+// a[i][0..3]; lane o receives a[4j + o/4][o%4] for j = 0..3.
+__device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
+    const fp16x4_raw v =
+        __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) fp16x4_raw *)(p));
+    return __builtin_bit_cast(f16x4, v);
+}
+
 template <typename KV, int HD>
 struct MfmaShape {
-    static constexpr int NC = HD / 32;                 // 16x16x32 chunks per S tile
-    static constexpr int NO = HD / 16;                 // 16-dim output chunks
-    static constexpr int EPL = 16 / KvTraits<KV>::kBytes;  // elements per 16-byte load
-    static constexpr int RAW = HD / (4 * EPL);         // 16-byte loads per lane per token row
-    static constexpr int CPL = EPL / 8;                // 8-element operand chunks per load
-    static constexpr int LDS = HD + 8;                 // padded V row (halves)
+    static constexpr int NC = HD / 32;                        // 16x16x32 chunks per S tile
+    static constexpr int NO = HD / 16;                        // 16-dim output chunks
+    static constexpr int EPL = 16 / KvTraits<KV>::kBytes;     // elements per 16-byte load
+    static constexpr int LPR = HD / EPL;                      // lanes per token row (one 16-byte load each)
+    static constexpr int RPI = 64 / LPR;                      // token rows per load instruction
+    static constexpr int NI = 16 / RPI;                       // load instructions per 16-token tile
+    static constexpr int KL = HD + 8;                         // K row in LDS (halves): odd 16-byte units
+    static constexpr int VL = HD + 16;                        // V row in LDS (halves)
     static constexpr int NW = kMfmaWaves;
-    static constexpr int VT = 16 * LDS;                // halves of one wave's V tile
-    // per-wave V tiles during the tile loop, per-wave partial outputs in the merge
-    static constexpr int kSmemBytes = NW * VT * 2 > NW * 16 * HD * 4 ? NW * VT * 2 : NW * 16 * HD * 4;
+    static constexpr int WT = 16 * (KL + VL);                 // halves of one wave's K and V tiles
+    static constexpr int kSmemBytes = NW * WT * 2 > NW * 16 * HD * 4 ? NW * WT * 2 : NW * 16 * HD * 4;
+    static_assert(64 % LPR == 0 && 16 % RPI == 0, "token rows must tile the wave");
 };
 
 // One work item: (row r, split-context partition `part`, kv head kvh) on the
 // whole workgroup.  Returns uniformly across the workgroup.
-template <typename KV, int HD, bool BS16>
+//
+// Loads: 16 lanes (8 for e4m3) cover one token row's HD elements with 16-byte
+// loads, so each load instruction reads whole 256-byte rows (measured on
+// gfx950: ~6.4 TB/s for this pattern against ~4.8 TB/s when one instruction
+// gathers 64-byte slices of 16 rows).  The rows then pass through LDS: K is read
+// back as the A operand of S^T = K Q^T (v_mfma_f32_16x16x32_f16, query heads on
+// the N side) and V with the transposing ds_read_b64_tr_b16 as the A operand of
+// O^T = V^T P^T (v_mfma_f32_16x16x16_f16), whose B operand is the S^T
+// accumulator layout itself (lane%16 = head, lane/16 = token quad).
+template <typename KV, int HD, int BLK>
 __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, int kvh, char *smem,
                                           float (*sm_ml)[16][2]) {
     using S = MfmaShape<KV, HD>;
-    constexpr int NC = S::NC, NO = S::NO, EPL = S::EPL, RAW = S::RAW, CPL = S::CPL, LDS = S::LDS, NW = S::NW,
-                  VT = S::VT;
+    constexpr int NC = S::NC, NO = S::NO, EPL = S::EPL, LPR = S::LPR, RPI = S::RPI, NI = S::NI, KL = S::KL,
+                  VL = S::VL, NW = S::NW, WT = S::WT;
     constexpr bool kFp8 = sizeof(KV) == 1;
-    constexpr bool kTileScale = kFp8 && BS16;   // one block per tile: scale folded out of the products
+    constexpr bool kTileScale = kFp8 && BLK == kBlkTile;  // one block per tile: scale folded out of the products
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
     const int H = p.num_heads;
@@ -186,20 +191,16 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
         pr.t_begin = wg.t_begin + wave * per;
         pr.t_end = pr.t_begin + per < wg.t_end ? pr.t_begin + per : wg.t_end;
     }
-    f16 *vt = reinterpret_cast<f16 *>(smem) + wave * VT;
+    f16 *kt = reinterpret_cast<f16 *>(smem) + wave * WT;
+    f16 *vt = kt + 16 * KL;
 
-    // Contraction order: load u of lane group g covers row bytes [64u + 16g, +16),
-    // so one load instruction reads 64 contiguous bytes of each of the 16 token
-    // rows; operand chunk c holds dims dim_of(c) .. +8 of that slice.
-    auto dim_of = [&](int cidx) { return (cidx / CPL) * 4 * EPL + grp * EPL + (cidx % CPL) * 8; };
-
-    // Q^T B operand: lane holds Q[h][dim_of(c) .. +8] for chunk c
+    // Q^T B operand: lane holds Q[h][32c + 8g .. +8] for chunk c
     f16x8 qv[NC];
     {
-        const f16 *qp = static_cast<const f16 *>(p.q) + ((int64_t)c.out_row * H + (head_ok ? h : 0)) * HD;
+        const f16 *qp = static_cast<const f16 *>(p.q) + ((int64_t)c.out_row * H + (head_ok ? h : 0)) * HD + 8 * grp;
 #pragma unroll
         for (int i = 0; i < NC; i++) {
-            f16x8 v = *reinterpret_cast<const f16x8 *>(qp + dim_of(i));
+            f16x8 v = *reinterpret_cast<const f16x8 *>(qp + 32 * i);
             qv[i] = head_ok ? v : (f16x8)(f16)0.0f;
         }
     }
@@ -208,65 +209,111 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
     const char *kbase = static_cast<const char *>(p.k_pool);
     const char *vbase = static_cast<const char *>(p.v_pool);
     const int bs = p.block_size;
+    const int bsh = __builtin_ctz(bs);  // block_size is a power of two
+    const int lrow = lane / LPR, piece = lane % LPR;  // row within an instruction, 16-byte piece of the row
 
     // Raw loads stay untouched until they are consumed: any arithmetic on them
     // right after the load would make the wave wait for it there.  Lanes whose
     // token lies outside the key range read a zero page instead of the pool, so
     // no masking of loaded data is needed (their S entries become -inf anyway).
     struct Tile {
-        uint4 k[RAW], v[RAW];
-        uint16_t ksb, vsb;
+        u32x4 k[NI], v[NI];
+        uint16_t ksb[kTileScale ? 1 : NI], vsb[kTileScale ? 1 : NI];
     };
 
-    // Block size 16: one physical block per tile.  Table entries for 64 tiles
-    // from window_base sit in one VGPR (lane i = tile window_base + i), refreshed
-    // once per 16-tile chunk, so a tile's address never waits on a table load.
-    int window_base = pr.t_begin;
+    // Block-table entries of 64 consecutive blocks from window_blk sit in one
+    // VGPR (lane i = block window_blk + i), refreshed once per 16-tile chunk, so
+    // a tile's address never waits on a table load.  The window covers the
+    // chunk's tiles and the two tiles loaded ahead of its end.
+    const int nlb = (c.k_hi + bs - 1) >> bsh;  // blocks holding keys of this row
+    int window_blk = 0;
     int32_t bt_window = 0;
-    auto refresh_window = [&](int base) {
-        window_base = base;
-        if (BS16) {
-            const int idx = base + lane < pr.t_end ? base + lane : pr.t_end - 1;
-            bt_window = c.bt[idx];
-        }
+    auto refresh_window = [&](int tile) {
+        window_blk = (tile * 16) >> bsh;
+        const int idx = window_blk + lane < nlb ? window_blk + lane : nlb - 1;
+        bt_window = c.bt[idx];
     };
     if (pr.t_begin < pr.t_end) refresh_window(pr.t_begin);
-    auto tile_block = [&](int tile) -> int {
-        return __builtin_amdgcn_readlane(bt_window, tile - window_base);
-    };
 
     // Tokens this wave may use: [k_lo, k_hi) cut to the partition.  Tiles past the
     // partition end are still "loaded" (from its last tile, a cache hit) so that
     // every step issues the same loads: with no load under a branch the compiler
     // can wait for exactly the tile it needs instead of draining all of them.
     const int j_hi = c.k_hi < pr.t_end * 16 ? c.k_hi : pr.t_end * 16;
+    const uint32_t row_bytes = (uint32_t)(row_stride * KvTraits<KV>::kBytes);  // bytes per token row (< 2^32)
+    const uint32_t lane_const = (uint32_t)(kvh * HD * KvTraits<KV>::kBytes + piece * 16);
     auto load_tile = [&](int tile, Tile &t) {
         const int lt = tile < pr.t_end ? tile : pr.t_end - 1;
-        const int j = tile * 16 + row;
-        const bool valid = j >= c.k_lo && j < j_hi;
-        int phys, slot;
-        if (BS16) {
-            phys = tile_block(lt);
-            slot = row;
-        } else {
-            const int jj = valid ? j : c.k_lo;
-            phys = c.bt[jj / bs];
-            slot = jj % bs;
-        }
-        const int64_t off = (((int64_t)phys * bs + slot) * row_stride + (int64_t)kvh * HD) * KvTraits<KV>::kBytes + grp * 16;
-        // Every lane loads unconditionally (loads under a branch would make the
-        // compiler drain every outstanding load before each use).
-        const char *zp = static_cast<const char *>(p.zero_page) + grp * 16;
-        const uint4 *kp = reinterpret_cast<const uint4 *>(valid ? kbase + off : zp);
-        const uint4 *vp = reinterpret_cast<const uint4 *>(valid ? vbase + off : zp);
+        if constexpr (BLK == kBlkTile) {
+            // One block holds the tile: a uniform base plus a per-lane 32-bit
+            // offset.  Rows outside [k_lo, j_hi) read the nearest row inside
+            // instead (finite data; their scores are masked to -inf, so their
+            // probabilities are 0).
+            const int phys = __builtin_amdgcn_readlane(bt_window, ((lt * 16) >> bsh) - window_blk);
+            const uint64_t tile_off =
+                (uint64_t)(((uint32_t)phys << bsh) + (uint32_t)((lt * 16) & (bs - 1))) * row_bytes;
+            const int r_lo = c.k_lo - lt * 16 > 0 ? c.k_lo - lt * 16 : 0;
+            const int r_hi = j_hi - lt * 16 < 16 ? j_hi - lt * 16 : 16;
+            const char *kb = kbase + tile_off, *vb = vbase + tile_off;
 #pragma unroll
-        for (int i = 0; i < RAW; i++) {
-            t.k[i] = kp[4 * i];
-            t.v[i] = vp[4 * i];
+            for (int u = 0; u < NI; u++) {
+                int trow = u * RPI + lrow;
+                trow = trow < r_lo ? r_lo : (trow >= r_hi ? r_hi - 1 : trow);
+                const uint32_t off = (uint32_t)trow * row_bytes + lane_const;
+                t.k[u] = *reinterpret_cast<const u32x4 *>(kb + off);
+                t.v[u] = *reinterpret_cast<const u32x4 *>(vb + off);
+            }
+            if constexpr (kTileScale) {
+                t.ksb[0] = p.k_scale[phys];
+                t.vsb[0] = p.v_scale[phys];
+            }
+        } else {
+            const char *zp = static_cast<const char *>(p.zero_page) + piece * 16;
+#pragma unroll
+            for (int u = 0; u < NI; u++) {
+                const int trow = u * RPI + lrow;
+                const int j = tile * 16 + trow;
+                const bool valid = j >= c.k_lo && j < j_hi;
+                const int jt = lt * 16 + trow;  // inside the window
+                const int phys = __shfl(bt_window, (jt >> bsh) - window_blk, 64);
+                const uint64_t off =
+                    (uint64_t)(((uint32_t)phys << bsh) + (uint32_t)(jt & (bs - 1))) * row_bytes + lane_const;
+                // Every lane loads unconditionally (loads under a branch would make
+                // the compiler drain every outstanding load before each use):
+                // masked lanes select the zero page.
+                const uint64_t ka = valid ? (uint64_t)kbase + off : (uint64_t)zp;
+                const uint64_t va = valid ? (uint64_t)vbase + off : (uint64_t)zp;
+                t.k[u] = *reinterpret_cast<const u32x4 *>(ka);
+                t.v[u] = *reinterpret_cast<const u32x4 *>(va);
+                if constexpr (kFp8) {
+                    t.ksb[u] = p.k_scale[phys];
+                    t.vsb[u] = p.v_scale[phys];
+                }
+            }
         }
-        if constexpr (kFp8) {  // phys is in bounds for every lane
-            t.ksb = p.k_scale[phys];
-            t.vsb = p.v_scale[phys];
+    };
+    // raw 16-byte pieces -> LDS rows (e4m3: widened to halves)
+    auto stage_rows = [&](const u32x4 *raw, const uint16_t *sb, f16 *dst, int ld) {
+#pragma unroll
+        for (int u = 0; u < NI; u++) {
+            f16 *d = dst + (u * RPI + lrow) * ld + piece * EPL;
+            if constexpr (!kFp8) {
+                *reinterpret_cast<u32x4 *>(d) = raw[u];
+            } else if constexpr (kTileScale) {
+                *reinterpret_cast<f16x8 *>(d) = e4m3x8_to_f16x8(raw[u][0], raw[u][1]);
+                *reinterpret_cast<f16x8 *>(d + 8) = e4m3x8_to_f16x8(raw[u][2], raw[u][3]);
+            } else {
+                const f16 sc = bits_to_f16(sb[u]);
+                const uint32_t w[4] = {raw[u][0], raw[u][1], raw[u][2], raw[u][3]};
+                f16x8 lo, hi;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    lo[i] = fp8_dequant((w[i >> 2] >> (8 * (i & 3))) & 0xFFu, sc);
+                    hi[i] = fp8_dequant((w[2 + (i >> 2)] >> (8 * (i & 3))) & 0xFFu, sc);
+                }
+                *reinterpret_cast<f16x8 *>(d) = lo;
+                *reinterpret_cast<f16x8 *>(d + 8) = hi;
+            }
         }
     };
 
@@ -275,39 +322,34 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
 #pragma unroll
     for (int i = 0; i < NO; i++) o[i] = (f32x4)0.0f;
 
-    // Two register tiles in flight per wave.  As soon as a tile's K has fed the S
-    // MFMAs and its V rows sit in LDS, its registers are refilled with the tile two
-    // ahead, so the next tile is always loading while this one's softmax and PV
-    // run, and the refill overlaps the following tile's work.
+    // Two register tiles in flight per wave.  As soon as a tile's rows sit in
+    // LDS, its registers are refilled with the tile two ahead, so the next tile
+    // is always loading while this one's scores, softmax and PV run.
     auto step = [&](int tile, Tile &t) {
-        // keep the scheduler from hoisting the next tile's MFMAs (and with them
-        // the wait for its loads) into this one
+        // keep the scheduler from hoisting the next tile's work (and with it the
+        // wait for its loads) into this one
         __builtin_amdgcn_sched_barrier(0);
-        // per-tile scales: block size 16 puts the whole tile in one block and 2^8
-        // undoes the operand shift; otherwise each lane's token has its own scale
-        f16 ks = (f16)0.0f, vs = (f16)0.0f;
+        // per-tile scales: a tile inside one block has one scale, and 2^8 undoes
+        // the widening shift; otherwise each row was dequantised on staging
+        f16 ks = (f16)1.0f, vs = (f16)1.0f;
         if constexpr (kTileScale) {
-            ks = (f16)((float)bits_to_f16(t.ksb) * 256.0f);
-            vs = (f16)((float)bits_to_f16(t.vsb) * 256.0f);
-        } else if constexpr (kFp8) {
-            ks = bits_to_f16(t.ksb);
-            vs = bits_to_f16(t.vsb);
+            ks = (f16)((float)bits_to_f16(t.ksb[0]) * 256.0f);
+            vs = (f16)((float)bits_to_f16(t.vsb[0]) * 256.0f);
         }
-        // S^T[token][head] over HD dims
+        stage_rows(t.k, t.ksb, kt, KL);
+        stage_rows(t.v, t.vsb, vt, VL);
+        // LDS ops of one wave execute in order; the wave barrier pins the compiler's
+        __builtin_amdgcn_wave_barrier();
+        load_tile(tile + 2, t);
+
+        // S^T[token][head] over HD dims: K row `row`, dims 32i + 8g .. +8
         f32x4 s = (f32x4)0.0f;
 #pragma unroll
         for (int i = 0; i < NC; i++)
-            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(operand_chunk<KV, kTileScale>(t.k, i, ks), qv[i], s, 0, 0, 0);
-
-        // stage V rows (token = row) for the transposed read; LDS ops of one wave
-        // execute in order, the wave barriers only pin the compiler's order
-#pragma unroll
-        for (int i = 0; i < NC; i++)
-            *reinterpret_cast<f16x8 *>(&vt[row * LDS + dim_of(i)]) = operand_chunk<KV, kTileScale>(t.v, i, vs);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8 *>(&kt[row * KL + 32 * i + 8 * grp]),
+                                                       qv[i], s, 0, 0, 0);
         const float sc = kTileScale ? p.scale_log2 * (float)ks : p.scale_log2;
         const float pv_scale = kTileScale ? (float)vs : 1.0f;
-        __builtin_amdgcn_wave_barrier();
-        load_tile(tile + 2, t);
 
         // online softmax on this lane's 4 tokens of head `row`
         float sv[4];
@@ -336,13 +378,12 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
 #pragma unroll
         for (int i = 0; i < NO; i++) o[i] *= corr;
 
+        // V^T operand of dims 16i..: lane (o, g) addresses row 4g + o/4, dims
+        // 16i + 4(o%4); the transposed load hands it tokens 4g..4g+3 of dim 16i + o
+        const f16 *vrow = vt + (4 * grp + (row >> 2)) * VL + 4 * (row & 3);
 #pragma unroll
-        for (int i = 0; i < NO; i++) {
-            f16x4 a;
-#pragma unroll
-            for (int q = 0; q < 4; q++) a[q] = vt[(4 * grp + q) * LDS + 16 * i + row];
-            o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[i], 0, 0, 0);
-        }
+        for (int i = 0; i < NO; i++)
+            o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(lds_read_tr16(vrow + 16 * i), pb, o[i], 0, 0, 0);
         __builtin_amdgcn_wave_barrier();
     };
 
@@ -368,7 +409,7 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
     float l_tot = l_run + shfl_xor(l_run, 16);
     l_tot += shfl_xor(l_tot, 32);
 
-    // Merge the waves' states.  The merge area overlays the V tiles, so every
+    // Merge the waves' states.  The merge area overlays the K/V tiles, so every
     // wave must be done with its tiles first.
     __syncthreads();
     float *mo = reinterpret_cast<float *>(smem);  // [NW][16][HD]
@@ -415,18 +456,18 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
     }
 }
 
-template <typename KV, int HD, bool BS16>
+template <typename KV, int HD, int BLK>
 __global__ __launch_bounds__(64 * kMfmaWaves, HD >= 256 ? 1 : 3) void attn_mfma_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[MfmaShape<KV, HD>::kSmemBytes];
     __shared__ float sm_ml[kMfmaWaves][16][2];
-    mfma_item<KV, HD, BS16>(p, blockIdx.z, blockIdx.x, blockIdx.y, smem, sm_ml);
+    mfma_item<KV, HD, BLK>(p, blockIdx.z, blockIdx.x, blockIdx.y, smem, sm_ml);
 }
 
 // Persistent form: a grid sized to the resident capacity walks a compacted list
 // of items, (row, partition) major and kv head minor, so no workgroup is spent
 // on empty partitions of short rows and the wave slots stay full to the end.
 // Every workgroup builds the list's row prefix sums in LDS from the row ranges.
-template <typename KV, int HD, bool BS16>
+template <typename KV, int HD, int BLK>
 __global__ __launch_bounds__(64 * kMfmaWaves, HD >= 256 ? 1 : 3) void attn_mfma_persistent(AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[MfmaShape<KV, HD>::kSmemBytes];
     __shared__ float sm_ml[kMfmaWaves][16][2];
@@ -469,7 +510,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves, HD >= 256 ? 1 : 3) void attn_mfma_
             else hi = mid;
         }
         __syncthreads();  // the previous item's LDS use is over
-        mfma_item<KV, HD, BS16>(p, lo, q - prefix[lo], kvh, smem, sm_ml);
+        mfma_item<KV, HD, BLK>(p, lo, q - prefix[lo], kvh, smem, sm_ml);
     }
 }
 
@@ -659,13 +700,13 @@ __global__ __launch_bounds__(64) void attn_reduce_kernel(AttnParams p) {
 
 // ------------------------------------------------------------------ launchers
 
-bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group) {
+bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size) {
     return (dtype == kF16 || dtype == kFP8) && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
-           group >= 1 && group <= 16;
+           group >= 1 && group <= 16 && block_size >= 8 && (block_size & (block_size - 1)) == 0;
 }
 
-template <typename KV, int HD>
-static hipError_t launch_mfma_hd(const AttnParams &p, hipStream_t stream) {
+template <typename KV, int HD, int BLK>
+static hipError_t launch_mfma_blk(const AttnParams &p, hipStream_t stream) {
     const dim3 block(64 * kMfmaWaves);
     if (p.rows <= kPersistentMaxRows) {
         // resident capacity of the persistent kernel, queried once per instantiation
@@ -675,27 +716,25 @@ static hipError_t launch_mfma_hd(const AttnParams &p, hipStream_t stream) {
             hipError_t e = hipGetDevice(&dev);
             if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
             if (e == hipSuccess)
-                e = p.block_size == 16 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                             &per_cu, attn_mfma_persistent<KV, HD, true>, block.x, 0)
-                                       : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                             &per_cu, attn_mfma_persistent<KV, HD, false>, block.x, 0);
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_persistent<KV, HD, BLK>, block.x, 0);
             if (e != hipSuccess) return e;
             resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
         }
         const int64_t upper = (int64_t)p.rows * p.max_parts * p.num_kv_heads;
         const dim3 grid((unsigned)(upper < resident ? upper : resident));
-        if (p.block_size == 16)
-            hipLaunchKernelGGL((attn_mfma_persistent<KV, HD, true>), grid, block, 0, stream, p);
-        else
-            hipLaunchKernelGGL((attn_mfma_persistent<KV, HD, false>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((attn_mfma_persistent<KV, HD, BLK>), grid, block, 0, stream, p);
         return hipGetLastError();
     }
     const dim3 grid(p.max_parts, p.num_kv_heads, p.rows);
-    if (p.block_size == 16)
-        hipLaunchKernelGGL((attn_mfma_kernel<KV, HD, true>), grid, block, 0, stream, p);
-    else
-        hipLaunchKernelGGL((attn_mfma_kernel<KV, HD, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((attn_mfma_kernel<KV, HD, BLK>), grid, block, 0, stream, p);
     return hipGetLastError();
+}
+
+template <typename KV, int HD>
+static hipError_t launch_mfma_hd(const AttnParams &p, hipStream_t stream) {
+    if (p.block_size % 16 == 0) return launch_mfma_blk<KV, HD, kBlkTile>(p, stream);
+    if (p.block_size == 8) return launch_mfma_blk<KV, HD, kBlkSmall>(p, stream);
+    return hipErrorInvalidValue;
 }
 
 template <typename KV>

@@ -54,7 +54,7 @@ struct AttnParams {
 // otherwise the VALU kernel.  Launches the split-context reduce when max_parts > 1.
 hipError_t launch_attention(const AttnParams &p, int32_t dtype, bool use_mfma, hipStream_t stream,
                             hipEvent_t after_main = nullptr);
-bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group);
+bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size);
 
 // KV append into the paged pools.
 struct AppendParams {

@@ -77,6 +77,7 @@ void Context::ensure_device() {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) throw PamError("GPU device or stream could not be initialized.");
     hip_check(hipGetDevice(&device_), "hipGetDevice");
+    hip_check(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, device_), "hipDeviceGetAttribute");
     hip_check(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking), "hipStreamCreate");
     hip_check(hipEventCreate(&ev0_), "hipEventCreate");
     hip_check(hipEventCreate(&ev1_), "hipEventCreate");
@@ -223,12 +224,29 @@ pam_stats Context::stats() {
 // Tokens per split-context partition.  Partitions are 16-token tiles; the grid
 // should hold a few thousand waves so all 256 CUs stay busy and ragged rows do
 // not leave a long tail.
-int32_t Context::choose_part_tokens(int64_t waves_per_part, int64_t max_tiles) {
+// Split-context partition length (tokens, a multiple of 16).
+//  MFMA kernel: one workgroup per (row, kv head, partition) item, about three
+//  resident per CU.  Items should number about twice the resident workgroups
+//  (so the persistent grid balances), but each should stream as many tiles as
+//  possible: longer partitions keep every wave's load pipeline full for longer
+//  between the per-item start-up and merge.
+//  VALU kernel: one wave per (row, head group, partition).
+int32_t Context::choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma) {
     if (max_tiles <= 0) return 16;
     if (part_tokens_override > 0) return std::max<int32_t>(16, part_tokens_override / 16 * 16);
-    if (waves_per_part >= 8192) return (int32_t)(max_tiles * 16);  // enough rows: one partition per row
+    if (mfma) {
+        const int64_t target = 6 * (int64_t)cus_;
+        if (items_per_part >= target) return (int32_t)(max_tiles * 16);
+        const int64_t parts = ceil_div(target, items_per_part);
+        const int64_t want = ceil_div(max_tiles, parts);
+        int64_t tpp = 16;
+        while (tpp < want) tpp <<= 1;
+        if (tpp >= max_tiles) tpp = max_tiles;
+        return (int32_t)(tpp * 16);
+    }
+    if (items_per_part >= 8192) return (int32_t)(max_tiles * 16);  // enough rows: one partition per row
     int64_t tpp = 16;
-    while (tpp > 4 && waves_per_part * ceil_div(max_tiles, tpp) < 4096) tpp /= 2;
+    while (tpp > 4 && items_per_part * ceil_div(max_tiles, tpp) < 4096) tpp /= 2;
     if (tpp >= max_tiles) tpp = max_tiles;
     return (int32_t)(tpp * 16);
 }
@@ -276,9 +294,9 @@ void Context::decode(const pam_decode_request &r) {
 void Context::decode_gpu(const pam_decode_request &r) {
     const pam_layer_spec &l = r.layer;
     const int32_t G = l.num_heads / l.num_kv_heads;
-    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && G >= 4;
+    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size) && G >= 4;
     if (decode_kernel_choice == 1) use_mfma = false;
-    if (decode_kernel_choice == 2) use_mfma = mfma_supported(l.data_type, l.head_dim, G);
+    if (decode_kernel_choice == 2) use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size);
     const int32_t nh = heads_per_wave(G);
 
     AttnParams p{};
@@ -307,7 +325,7 @@ void Context::decode_gpu(const pam_decode_request &r) {
     int64_t max_tiles = ceil_div(cap_tokens, 16);
     if (l.window_size > 0) max_tiles = std::min<int64_t>(max_tiles, l.window_size / 16 + 2);
     const int64_t waves = (int64_t)r.batch_size * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-    p.part_tokens = choose_part_tokens(waves, max_tiles);
+    p.part_tokens = choose_part_tokens(waves, max_tiles, use_mfma);
     p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles, p.part_tokens / 16));
     int64_t tmp = 0;
     if (p.max_parts > 1) {
@@ -382,7 +400,7 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
     p.zero_page = zero_page_;
 
     const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G, l.block_size) && decode_kernel_choice != 1;
-    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && decode_kernel_choice != 1;
+    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size) && decode_kernel_choice != 1;
     const int32_t nh = heads_per_wave(G);
     p.heads_per_wave = nh;
     const int64_t kv_len = (int64_t)r.q_offset + r.seq_len;
@@ -397,7 +415,7 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
         p.max_parts = 1;
     } else {
         const int64_t waves = (int64_t)r.seq_len * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-        p.part_tokens = choose_part_tokens(waves, max_tiles);
+        p.part_tokens = choose_part_tokens(waves, max_tiles, use_mfma);
         p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles, p.part_tokens / 16));
         if (p.max_parts > 1) {
             const int64_t slots = (int64_t)r.seq_len * l.num_heads * p.max_parts;
@@ -528,7 +546,7 @@ void Context::mixed_step(const pam_mixed_request &r) {
     std::stable_sort(chunks.begin(), chunks.end(),
                      [](const int4 &a, const int4 &b) { return a.y + a.z > b.y + b.z; });
     const int32_t ragged_rows = (int32_t)rows.size();
-    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G) && G >= 4;
+    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size) && G >= 4;
     if (decode_kernel_choice == 1) use_mfma = false;
     const int32_t nh = heads_per_wave(G);
 
@@ -598,7 +616,7 @@ void Context::mixed_step(const pam_mixed_request &r) {
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
     p.zero_page = zero_page_;
     const int64_t waves = (int64_t)ragged_rows * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-    p.part_tokens = choose_part_tokens(waves, max_tiles + 1);
+    p.part_tokens = choose_part_tokens(waves, max_tiles + 1, use_mfma);
     p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles + 1, p.part_tokens / 16));
     int64_t tmp = 0;
     if (ragged_rows > 0 && p.max_parts > 1) {

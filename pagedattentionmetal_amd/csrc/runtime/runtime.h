@@ -115,12 +115,13 @@ class Context {
     void decode_gpu(const pam_decode_request &r);
     void prefill_gpu(const pam_prefill_request &r);
     void append_gpu(const pam_append_request &r);
-    int32_t choose_part_tokens(int64_t waves_per_part, int64_t max_tiles);
+    int32_t choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma);
     void record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t blocks, int64_t tmp, bool split,
                       bool has_mid);
 
     bool device_ready_ = false;
     int device_ = 0;
+    int cus_ = 256;  // compute units of the device (set in ensure_device)
     hipStream_t own_stream_ = nullptr, ext_stream_ = nullptr;
     bool use_ext_stream_ = false;
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr, evmid_ = nullptr, staged_ = nullptr;
