@@ -500,7 +500,15 @@ __global__ __launch_bounds__(64 * kMfmaWaves, HD >= 256 ? 1 : 3) void attn_mfma_
     if (tid == NT - 1) prefix[rows] = chunk_sum[NT - 1];
     __syncthreads();
     const int32_t total = prefix[rows] * p.num_kv_heads;
-    for (int32_t item = blockIdx.x; item < total; item += gridDim.x) {
+    // Items are dealt in rounds of gridDim.x, alternating direction (a snake), so
+    // a workgroup that drew an early, long partition draws a late, short one next.
+    for (int32_t k = 0;; k++) {
+        const int32_t item = k * (int32_t)gridDim.x + ((k & 1) ? (int32_t)gridDim.x - 1 - (int32_t)blockIdx.x
+                                                                 : (int32_t)blockIdx.x);
+        if (item >= total) {
+            if (k * (int32_t)gridDim.x >= total) break;
+            continue;  // a short last round: this workgroup's slot is empty
+        }
         const int32_t q = item / p.num_kv_heads;
         const int kvh = item - q * p.num_kv_heads;
         int lo = 0, hi = rows;  // last row with prefix[row] <= q

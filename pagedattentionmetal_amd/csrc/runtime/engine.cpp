@@ -226,21 +226,17 @@ pam_stats Context::stats() {
 // not leave a long tail.
 // Split-context partition length (tokens, a multiple of 16).
 //  MFMA kernel: one workgroup per (row, kv head, partition) item, about three
-//  resident per CU.  Items should number about twice the resident workgroups
-//  (so the persistent grid balances), but each should stream as many tiles as
-//  possible: longer partitions keep every wave's load pipeline full for longer
-//  between the per-item start-up and merge.
+//  resident per CU, items dealt to the persistent grid in snake order.  Long
+//  partitions (1024 tokens) keep every wave's load pipeline full between the
+//  per-item start-up and merge, and bound the imbalance of ragged rows; they
+//  shrink only when there would be too few items to fill the grid.
 //  VALU kernel: one wave per (row, head group, partition).
 int32_t Context::choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma) {
     if (max_tiles <= 0) return 16;
     if (part_tokens_override > 0) return std::max<int32_t>(16, part_tokens_override / 16 * 16);
     if (mfma) {
-        const int64_t target = 6 * (int64_t)cus_;
-        if (items_per_part >= target) return (int32_t)(max_tiles * 16);
-        const int64_t parts = ceil_div(target, items_per_part);
-        const int64_t want = ceil_div(max_tiles, parts);
-        int64_t tpp = 16;
-        while (tpp < want) tpp <<= 1;
+        int64_t tpp = 64;
+        while (tpp > 16 && items_per_part * ceil_div(max_tiles, tpp) < 3 * (int64_t)cus_) tpp /= 2;
         if (tpp >= max_tiles) tpp = max_tiles;
         return (int32_t)(tpp * 16);
     }
