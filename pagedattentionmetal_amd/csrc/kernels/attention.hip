@@ -677,32 +677,48 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnParams p, int lanes_p
 
 // ------------------------------------------------------------------ split-context reduce
 // O = sum_p 2^{m_p - M} O_p / sum_p 2^{m_p - M} l_p over the row's partitions.
+// Split-context reduce: one wave per (row, head), four per workgroup.  The
+// partials' maxima and sums are reduced across lanes (one partition per lane),
+// then lane groups of HD/4 lanes each accumulate a share of the partitions'
+// weighted outputs and the groups are summed with shuffles.
 template <typename QT>
-__global__ __launch_bounds__(64) void attn_reduce_kernel(AttnParams p) {
-    const int r = blockIdx.y, h = blockIdx.x;
+__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnParams p) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = blockIdx.y, h = blockIdx.x * 4 + wave;
+    if (h >= p.num_heads) return;
     const RowCtx c = row_ctx(p, r);
     const PartRange pr = part_range(c, 0, p.part_tokens);
-    if (pr.nparts <= 1) return;
+    const int np = pr.nparts;
+    if (np <= 1) return;
     const int HD = p.head_dim, H = p.num_heads;
     const int64_t base = ((int64_t)r * H + h) * p.max_parts;
     float M = -INFINITY;
-    for (int i = 0; i < pr.nparts; i++) M = fmaxf(M, p.part_ml[(base + i) * 2]);
+    for (int i = lane; i < np; i += 64) M = fmaxf(M, p.part_ml[(base + i) * 2]);
+    M = wave_max_xor(M, 1, 64);
     float den = 0.0f;
-    for (int i = 0; i < pr.nparts; i++) den += exp2f(p.part_ml[(base + i) * 2] - M) * p.part_ml[(base + i) * 2 + 1];
-    const float inv = 1.0f / den;
-    QT *out = static_cast<QT *>(p.out);
-    for (int d0 = threadIdx.x * 4; d0 < HD; d0 += 256) {
-        float a[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int i = 0; i < pr.nparts; i++) {
+    for (int i = lane; i < np; i += 64) den += exp2f(p.part_ml[(base + i) * 2] - M) * p.part_ml[(base + i) * 2 + 1];
+    den = wave_sum_xor(den, 1, 64);
+    // lanes per group: HD/4 rounded up to a power of two (<= 64)
+    int lpg = 1;
+    while (lpg * 4 < HD) lpg <<= 1;
+    const int ng = 64 / lpg, g = lane / lpg, d0 = (lane % lpg) * 4;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    if (d0 < HD) {
+        for (int i = g; i < np; i += ng) {
             const float w = exp2f(p.part_ml[(base + i) * 2] - M);
             float v[4];
             load4<float>(p.part_o + (base + i) * HD + d0, v);
 #pragma unroll
             for (int e = 0; e < 4; e++) a[e] += w * v[e];
         }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) a[e] = wave_sum_xor(a[e], lpg, 64);
+    if (g == 0 && d0 < HD) {
+        const float inv = 1.0f / den;
 #pragma unroll
         for (int e = 0; e < 4; e++) a[e] *= inv;
-        store4<QT>(out + (c.out_row * H + h) * (int64_t)HD + d0, a);
+        store4<QT>(static_cast<QT *>(p.out) + (c.out_row * H + h) * (int64_t)HD + d0, a);
     }
 }
 
@@ -792,11 +808,11 @@ hipError_t launch_attention(const AttnParams &p, int32_t dtype, bool use_mfma, h
     if (e != hipSuccess) return e;
     if (after_main) (void)hipEventRecord(after_main, stream);
     if (p.max_parts <= 1) return e;
-    dim3 grid(p.num_heads, p.rows);
+    dim3 grid((p.num_heads + 3) / 4, p.rows);
     if (dtype == kF32)
-        hipLaunchKernelGGL((attn_reduce_kernel<float>), grid, dim3(64), 0, stream, p);
+        hipLaunchKernelGGL((attn_reduce_kernel<float>), grid, dim3(256), 0, stream, p);
     else
-        hipLaunchKernelGGL((attn_reduce_kernel<f16>), grid, dim3(64), 0, stream, p);
+        hipLaunchKernelGGL((attn_reduce_kernel<f16>), grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
