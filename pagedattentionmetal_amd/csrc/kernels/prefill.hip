@@ -6,17 +6,19 @@
 // head h / G, a fixed window start max(0, kv_len - W) for every row).
 //
 // Matrix work runs on v_mfma_f32_32x32x16_f16, which on gfx950 retires twice
-// the flops per cycle of the 16x16 shapes.  A workgroup (8 waves, one per CU)
+// the flops per cycle of the 16x16 shapes.  A workgroup (8 waves, two per SIMD)
 // owns 256 query rows of one kv head: the (token, head) pairs of 256 / G
 // consecutive tokens, so the G query heads sharing a kv head share every K/V
-// tile (the tile bytes per flop set the cache traffic); each wave owns 32 rows.  Per 32-key tile:
-//   * all 512 threads stage K and V rows into a 3-deep LDS ring (the next tiles
-//     are fetched into registers while earlier ones are computed);
-//   * S^T = K Q^T (32 keys x 32 rows, 8 MFMAs over d): K from LDS is the A
-//     operand, Q^T stays in registers as B.  The accumulator leaves lane (n, h)
-//     holding keys 8q + 4h + r (q, r < 4) of row n, and the 8 of them with q in
-//     {2c, 2c+1} are exactly the B operand of O^T += V^T P^T over key chunk c
-//     (16 keys), so P never leaves registers; V^T is read from LDS with the
+// tile.  Each wave owns RB blocks of 32 rows; every K or V operand it reads from
+// LDS feeds RB MFMAs (RB = 2 halves the LDS traffic but needs AGPR
+// accumulators and one wave per SIMD, which measured slower).  Per 32-key tile:
+//   * all 256 threads stage K and V rows into a 3-deep LDS ring (the next tiles
+//     are fetched into registers two iterations ahead);
+//   * S^T = K Q^T (32 keys x 32 rows per block, 8 MFMAs over d): K from LDS is
+//     the A operand, Q^T stays in registers as B.  The accumulator leaves lane
+//     (n, h) holding keys 8q + 4h + r (q, r < 4) of row n, and the 8 of them with
+//     q in {2c, 2c+1} are exactly the B operand of O^T += V^T P^T over key chunk
+//     c (16 keys), so P never leaves registers; V^T is read from LDS with the
 //     transposing ds_read_b64_tr_b16;
 //   * the scores of tile t+1 are formed while the probabilities of tile t are
 //     exponentiated, and O += V(t) P(t) runs while tile t+1 is masked and reduced;
@@ -30,13 +32,14 @@ namespace pam {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kPrefillWaves = 8;
-constexpr int kPrefillRows = 32 * kPrefillWaves;  // query rows per workgroup
-constexpr int kPrefillKT = 64;                     // keys per tile
-constexpr int kPrefillBufs = 3;                    // LDS ring: t computed, t+1 scored, t+2 written
-constexpr float kRescaleLog2 = 8.0f;               // lazy-rescale threshold (log2 units)
-constexpr int kBtCache = 2048;                     // block-table entries a workgroup keeps in LDS
-constexpr int kXcds = 8;                           // accelerator dies (each with its own L2)
+constexpr int kPrefillWaves = 8;                               // one workgroup per CU
+constexpr int kPrefillRB = 1;                                  // 32-row blocks per wave
+constexpr int kPrefillRows = 32 * kPrefillRB * kPrefillWaves;  // query rows per workgroup
+constexpr int kPrefillKT = 32;                                 // keys per tile
+constexpr int kPrefillBufs = 3;                // LDS ring: t computed, t+1 scored, t+2 written
+constexpr float kRescaleLog2 = 8.0f;           // lazy-rescale threshold (log2 units)
+constexpr int kBtCache = 2048;                 // block-table entries a workgroup keeps in LDS
+constexpr int kXcds = 8;                       // accelerator dies (each with its own L2)
 
 typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
@@ -65,7 +68,7 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
     return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
-template <int HD>
+template <int HD, int RB>
 __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(AttnParams p) {
     static_assert(HD == 128, "layouts assume d = 128");
     constexpr int KT = kPrefillKT;
@@ -76,6 +79,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
     constexpr int THREADS = 64 * kPrefillWaves;
     constexpr int KEYS_PER_PASS = THREADS / PIECES;  // 16 lanes per key row
     constexpr int KPT = KT / KEYS_PER_PASS;          // keys per thread per tile
+    constexpr int ROWS = 32 * RB * kPrefillWaves;
     static_assert(KT % KEYS_PER_PASS == 0 && KPT <= 2, "whole keys per thread");
     __shared__ __attribute__((aligned(16))) f16 k_lds[kPrefillBufs][KT * kPrefillKL];
     __shared__ __attribute__((aligned(16))) f16 v_lds[kPrefillBufs][KT * kPrefillVL];
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
     const int G = p.num_heads / p.num_kv_heads, H = p.num_heads;
-    const int tok_per_wg = kPrefillRows / G;
+    const int tok_per_wg = ROWS / G;
     // Workgroup -> (chunk, kv head, token block).  Workgroups are dispatched to
     // the 8 XCDs round-robin by id, and each XCD has its own L2: all token
     // blocks of one (chunk, kv head) get ids of one residue mod 8, so the K/V
@@ -109,17 +113,21 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
     int full_hi = kv_len / KT;
     if (p.causal) full_hi = min(full_hi, (ch.y + tok0 + 1) / KT);
 
-    // this lane's query row (column n of the wave's 32)
-    const int rr = wave * 32 + n;
-    const int my_tok = tok0 + rr / G, my_head = rr % G;
-    const bool row_ok = my_tok < tok_end;
-    const int qpos = ch.y + my_tok;
-    f16x8 qv[DC];
-    {
-        const f16 *qp = static_cast<const f16 *>(p.q) +
-                        ((int64_t)(ch.w + (row_ok ? my_tok : tok0)) * H + kvh * G + my_head) * HD + 8 * h;
+    // this lane's query rows: column n of each of the wave's 32-row blocks
+    int my_tok[RB], my_head[RB], qpos[RB];
+    bool row_ok[RB];
+    f16x8 qv[RB][DC];
 #pragma unroll
-        for (int c = 0; c < DC; c++) qv[c] = *reinterpret_cast<const f16x8 *>(qp + 16 * c);
+    for (int b = 0; b < RB; b++) {
+        const int rr = (wave * RB + b) * 32 + n;
+        my_tok[b] = tok0 + rr / G;
+        my_head[b] = rr % G;
+        row_ok[b] = my_tok[b] < tok_end;
+        qpos[b] = ch.y + my_tok[b];
+        const f16 *qp = static_cast<const f16 *>(p.q) +
+                        ((int64_t)(ch.w + (row_ok[b] ? my_tok[b] : tok0)) * H + kvh * G + my_head[b]) * HD + 8 * h;
+#pragma unroll
+        for (int c = 0; c < DC; c++) qv[b][c] = *reinterpret_cast<const f16x8 *>(qp + 16 * c);
     }
 
     // staging map: thread -> piece tid % 16 of keys tid / 16 (+ THREADS / 16)
@@ -160,17 +168,20 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
         }
     };
 
-    // S^T: A operand of chunk c = K[key n][16c + 8h .. +7]
+    // S^T: A operand of chunk c = K[key n][16c + 8h .. +7], shared by the row blocks
     const int k_rd = k_lds_at(n, h);
-    auto score = [&](int buf, f32x16(&sc)[KH]) {
+    auto score = [&](int buf, f32x16(&sc)[RB][KH]) {
         const f16 *kt = k_lds[buf];
 #pragma unroll
         for (int e = 0; e < KH; e++) {
-            sc[e] = (f32x16)0.0f;
+#pragma unroll
+            for (int b = 0; b < RB; b++) sc[b][e] = (f32x16)0.0f;
 #pragma unroll
             for (int c = 0; c < DC; c++) {
                 const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * kPrefillKL + 16 * c]);
-                sc[e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[c], sc[e], 0, 0, 0);
+#pragma unroll
+                for (int b = 0; b < RB; b++)
+                    sc[b][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[b][c], sc[b][e], 0, 0, 0);
             }
         }
     };
@@ -187,48 +198,61 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             v_rd[dt] = v_lds_at(row, 4 * dt + 2 * hh + ((o & 3) >> 1)) + 4 * (o & 1);
     }
 
-    float m_use = -INFINITY, l_run = 0.0f;
-    f32x16 o[DT];
+    float m_use[RB], l_run[RB], lmax[RB];
+    f32x16 o[RB][DT];
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++) o[dt] = (f32x16)0.0f;
+    for (int b = 0; b < RB; b++) {
+        m_use[b] = -INFINITY;
+        l_run[b] = 0.0f;
+        lmax[b] = -INFINITY;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[b][dt] = (f32x16)0.0f;
+    }
     const float sl2 = p.scale_log2;
     const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 
     // accumulator register r of block e holds key 32e + 8(r/4) + 4h + r%4 of the tile
-    float lmax = -INFINITY;
-    auto prepare = [&](int tile, f32x16(&sc)[KH]) -> bool {
-        if (!(tile >= full_lo && tile < full_hi)) {
+    auto prepare = [&](int tile, f32x16(&sc)[RB][KH]) -> bool {
+        bool need = false;
 #pragma unroll
-            for (int e = 0; e < KH; e++)
+        for (int b = 0; b < RB; b++) {
+            if (!(tile >= full_lo && tile < full_hi)) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int j = tile * KT + 32 * e + 8 * (r >> 2) + 4 * h + (r & 3);
-                    const bool ok = j >= ws && j < kv_len && (!p.causal || j <= qpos);
-                    sc[e][r] = ok ? sc[e][r] : -INFINITY;
-                }
+                for (int e = 0; e < KH; e++)
+#pragma unroll
+                    for (int r2 = 0; r2 < 16; r2++) {
+                        const int j = tile * KT + 32 * e + 8 * (r2 >> 2) + 4 * h + (r2 & 3);
+                        const bool ok = j >= ws && j < kv_len && (!p.causal || j <= qpos[b]);
+                        sc[b][e][r2] = ok ? sc[b][e][r2] : -INFINITY;
+                    }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < KH; e++) {
+                mx = vmax3(mx, sc[b][e][0], sc[b][e][1]);
+#pragma unroll
+                for (int r2 = 2; r2 < 16; r2 += 2) mx = vmax3(mx, sc[b][e][r2], sc[b][e][r2 + 1]);
+            }
+            lmax[b] = mx * sl2;
+            need |= lmax[b] > m_use[b] + kRescaleLog2;
         }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int e = 0; e < KH; e++) {
-            mx = vmax3(mx, sc[e][0], sc[e][1]);
-#pragma unroll
-            for (int r = 2; r < 16; r += 2) mx = vmax3(mx, sc[e][r], sc[e][r + 1]);
-        }
-        lmax = mx * sl2;
-        return lmax > m_use + kRescaleLog2;
+        return need;
     };
     // raise the reference max to the row max (rare: wave-uniform branch)
     auto rescale = [&]() {
-        const float mt = fmaxf(lmax, shfl_xor(lmax, 32));
-        const float m_new = fmaxf(m_use, mt);
-        const float corr = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use - m_new);
-        l_run *= corr;
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[dt] *= corr;
-        m_use = m_new;
+        for (int b = 0; b < RB; b++) {
+            const float mt = fmaxf(lmax[b], shfl_xor(lmax[b], 32));
+            const float m_new = fmaxf(m_use[b], mt);
+            const float corr = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use[b] - m_new);
+            l_run[b] *= corr;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) o[b][dt] *= corr;
+            m_use[b] = m_new;
+        }
     };
 
-    f32x16 sacc[KH], snext[KH];
+    f32x16 sacc[RB][KH], snext[RB][KH];
     // tiles run in segments whose block-table entries fit in bt_lds (one segment
     // covers kBtCache * block_size keys, so long contexts only)
     // (an even number of tiles: the loop below runs tiles in pairs, and a segment
@@ -258,24 +282,26 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             const int b1 = buf == kPrefillBufs - 1 ? 0 : buf + 1;
             const int b2 = b1 == kPrefillBufs - 1 ? 0 : b1 + 1;
             score(b1, snext);
-            f16x8 pb[2 * KH];
-            {
-                const float mref = m_use == -INFINITY ? 0.0f : m_use;
+            f16x8 pb[RB][2 * KH];
+#pragma unroll
+            for (int b = 0; b < RB; b++) {
+                const float mref = m_use[b] == -INFINITY ? 0.0f : m_use[b];
 #pragma unroll
                 for (int e = 0; e < KH; e++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        pb[2 * e + (r >> 3)][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[e][r], sl2, -mref));
+                    for (int r2 = 0; r2 < 16; r2++)
+                        pb[b][2 * e + (r2 >> 3)][r2 & 7] =
+                            (f16)__builtin_amdgcn_exp2f(fmaf(sacc[b][e][r2], sl2, -mref));
                 // row sum of the f16 probabilities the MFMA consumes
-                float ps = l_run;
+                float ps = l_run[b];
 #pragma unroll
                 for (int k = 0; k < 8 * KH; k++) {
-                    const f16x2 pr = {pb[k >> 2][2 * (k & 3)], pb[k >> 2][2 * (k & 3) + 1]};
+                    const f16x2 pr = {pb[b][k >> 2][2 * (k & 3)], pb[b][k >> 2][2 * (k & 3) + 1]};
                     ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
                 }
-                l_run = ps;
+                l_run[b] = ps;
             }
-            // O^T += V^T P^T
+            // O^T += V^T P^T, each V^T operand shared by the row blocks
             const f16 *vt = v_lds[buf];
 #pragma unroll
             for (int c = 0; c < 2 * KH; c++)
@@ -284,7 +310,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
                     const f16x4 lo = lds_read_tr16(vt + v_rd[dt] + 16 * c * kPrefillVL);
                     const f16x4 hi = lds_read_tr16(vt + v_rd[dt] + (16 * c + 8) * kPrefillVL);
                     const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], o[dt], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < RB; b++)
+                        o[b][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[b][c], o[b][dt], 0, 0, 0);
                 }
             // the last tile's successor is not scored: never let it move the reference
             const bool need = prepare(tile + 1, snext) && tile + 1 < seg_pad;
@@ -293,7 +321,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             __syncthreads();
             if (__any(need)) rescale();
 #pragma unroll
-            for (int e = 0; e < KH; e++) sacc[e] = snext[e];
+            for (int b = 0; b < RB; b++)
+#pragma unroll
+                for (int e = 0; e < KH; e++) sacc[b][e] = snext[b][e];
             buf = b1;
         };
         for (int tile = seg; tile < seg_pad; tile += 2) {
@@ -303,20 +333,23 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
     }
 
     // finish: l summed over the two lane halves, O / l, rows in range only
-    const float l = l_run + shfl_xor(l_run, 32);
-    if (!row_ok) return;
-    // no key in range (window past the row): 0/0, as the reference's m/l bookkeeping gives
-    const float inv = 1.0f / l;
-    f16 *op = static_cast<f16 *>(p.out) + ((int64_t)(ch.w + my_tok) * H + kvh * G + my_head) * HD + 4 * h;
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++)
+    for (int b = 0; b < RB; b++) {
+        const float l = l_run[b] + shfl_xor(l_run[b], 32);
+        if (!row_ok[b]) continue;
+        // no key in range (window past the row): 0/0, as the reference's m/l bookkeeping gives
+        const float inv = 1.0f / l;
+        f16 *op = static_cast<f16 *>(p.out) + ((int64_t)(ch.w + my_tok[b]) * H + kvh * G + my_head[b]) * HD + 4 * h;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            f16x4 v;
+        for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) v[r] = (f16)(o[dt][4 * q + r] * inv);
-            *reinterpret_cast<f16x4 *>(op + 32 * dt + 8 * q) = v;
-        }
+            for (int q = 0; q < 4; q++) {
+                f16x4 v;
+#pragma unroll
+                for (int r2 = 0; r2 < 4; r2++) v[r2] = (f16)(o[b][dt][4 * q + r2] * inv);
+                *reinterpret_cast<f16x4 *>(op + 32 * dt + 8 * q) = v;
+            }
+    }
 }
 
 bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size) {
@@ -332,7 +365,7 @@ hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream) {
     const int nx = (p.max_chunk_len + tok_per_wg - 1) / tok_per_wg;
     const int groups = p.num_chunks * p.num_kv_heads;
     dim3 grid(kXcds * nx * ((groups + kXcds - 1) / kXcds));
-    hipLaunchKernelGGL((prefill_mfma_kernel<128>), grid, dim3(64 * kPrefillWaves), 0, stream, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB>), grid, dim3(64 * kPrefillWaves), 0, stream, p);
     return hipGetLastError();
 }
 
