@@ -253,7 +253,8 @@ int32_t pam_buffer_download(void *context, void *host_dst, const void *device_sr
 int32_t pam_buffer_zero(void *context, void *device_ptr, size_t bytes);
 /* Launch on an external hipStream_t (NULL = the device's default stream). */
 int32_t pam_set_stream(void *context, void *hip_stream);
-/* Go back to launching on the context's own (non-blocking) stream. */
+/* Go back to launching on the context's own stream (a blocking stream: ordered
+ * against work on the legacy default stream). */
 int32_t pam_use_own_stream(void *context);
 /* true (default): calls wait for their GPU work; false: calls return once enqueued. */
 int32_t pam_set_synchronous(void *context, bool synchronous);

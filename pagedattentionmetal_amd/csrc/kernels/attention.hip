@@ -166,7 +166,7 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
     constexpr int NC = S::NC, NO = S::NO, EPL = S::EPL, LPR = S::LPR, RPI = S::RPI, NI = S::NI, KL = S::KL,
                   VL = S::VL, NW = S::NW, WT = S::WT;
     constexpr bool kFp8 = sizeof(KV) == 1;
-    constexpr bool kTileScale = kFp8 && BLK == kBlkTile;  // one block per tile: scale folded out of the products
+    constexpr bool kTileScale = kFp8 && BLK == kBlkTile;  // one block (one scale pair) per tile
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
     const int H = p.num_heads;
@@ -293,15 +293,19 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
         }
     };
     // raw 16-byte pieces -> LDS rows (e4m3: widened to halves)
-    auto stage_rows = [&](const u32x4 *raw, const uint16_t *sb, f16 *dst, int ld) {
+    auto stage_rows = [&](const u32x4 *raw, const uint16_t *sb, f16 tile_scale, f16 *dst, int ld) {
 #pragma unroll
         for (int u = 0; u < NI; u++) {
             f16 *d = dst + (u * RPI + lrow) * ld + piece * EPL;
             if constexpr (!kFp8) {
                 *reinterpret_cast<u32x4 *>(d) = raw[u];
             } else if constexpr (kTileScale) {
-                *reinterpret_cast<f16x8 *>(d) = e4m3x8_to_f16x8(raw[u][0], raw[u][1]);
-                *reinterpret_cast<f16x8 *>(d + 8) = e4m3x8_to_f16x8(raw[u][2], raw[u][3]);
+                // exact code value * 2^-8, times scale * 2^8 in one binary16
+                // multiply: the reference's half dequantisation (two half products,
+                // the second a power of two) up to results below the normal range
+                const f16x8 s8 = (f16x8)tile_scale;
+                *reinterpret_cast<f16x8 *>(d) = e4m3x8_to_f16x8(raw[u][0], raw[u][1]) * s8;
+                *reinterpret_cast<f16x8 *>(d + 8) = e4m3x8_to_f16x8(raw[u][2], raw[u][3]) * s8;
             } else {
                 const f16 sc = bits_to_f16(sb[u]);
                 const uint32_t w[4] = {raw[u][0], raw[u][1], raw[u][2], raw[u][3]};
@@ -329,15 +333,15 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
         // keep the scheduler from hoisting the next tile's work (and with it the
         // wait for its loads) into this one
         __builtin_amdgcn_sched_barrier(0);
-        // per-tile scales: a tile inside one block has one scale, and 2^8 undoes
-        // the widening shift; otherwise each row was dequantised on staging
+        // per-tile scales (a tile inside one block has one scale pair); 2^8 undoes
+        // the widening shift.  Otherwise each row is dequantised on staging.
         f16 ks = (f16)1.0f, vs = (f16)1.0f;
         if constexpr (kTileScale) {
             ks = (f16)((float)bits_to_f16(t.ksb[0]) * 256.0f);
             vs = (f16)((float)bits_to_f16(t.vsb[0]) * 256.0f);
         }
-        stage_rows(t.k, t.ksb, kt, KL);
-        stage_rows(t.v, t.vsb, vt, VL);
+        stage_rows(t.k, t.ksb, ks, kt, KL);
+        stage_rows(t.v, t.vsb, vs, vt, VL);
         // LDS ops of one wave execute in order; the wave barrier pins the compiler's
         __builtin_amdgcn_wave_barrier();
         load_tile(tile + 2, t);
@@ -348,8 +352,7 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
         for (int i = 0; i < NC; i++)
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8 *>(&kt[row * KL + 32 * i + 8 * grp]),
                                                        qv[i], s, 0, 0, 0);
-        const float sc = kTileScale ? p.scale_log2 * (float)ks : p.scale_log2;
-        const float pv_scale = kTileScale ? (float)vs : 1.0f;
+        const float sc = p.scale_log2;
 
         // online softmax on this lane's 4 tokens of head `row`
         float sv[4];
@@ -371,7 +374,7 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
         for (int q = 0; q < 4; q++) {
             const float pq = exp2f(sv[q] - m_use);
             psum += pq;
-            pb[q] = (f16)(pq * pv_scale);
+            pb[q] = (f16)pq;
         }
         l_run = l_run * corr + psum;
         m_run = m_new;

@@ -78,7 +78,10 @@ void Context::ensure_device() {
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) throw PamError("GPU device or stream could not be initialized.");
     hip_check(hipGetDevice(&device_), "hipGetDevice");
     hip_check(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, device_), "hipDeviceGetAttribute");
-    hip_check(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking), "hipStreamCreate");
+    // A blocking stream: work the caller queued on the legacy default stream (the
+    // usual producer of the buffers passed in) completes before ours starts, and
+    // the other way round, as for the reference's synchronous command buffers.
+    hip_check(hipStreamCreateWithFlags(&own_stream_, hipStreamDefault), "hipStreamCreate");
     hip_check(hipEventCreate(&ev0_), "hipEventCreate");
     hip_check(hipEventCreate(&ev1_), "hipEventCreate");
     hip_check(hipEventCreate(&evmid_), "hipEventCreate");

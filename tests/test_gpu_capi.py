@@ -1,0 +1,155 @@
+"""GPU tests of the reference's flat C ABI end to end (PagedAttentionCABI.swift:71-372)
+and of the engine behaviour around it.
+
+They run on a device cache: pam_reserve_sequence, pam_append_tokens, pam_append_kv,
+pam_prefill and pam_decode, all called through ctypes with device pointers, and
+checked against the oracle on the cache's own pools.  They also cover
+copy-on-write of a shared prefix block in HBM (KVCacheManager.swift:176-214,
+FP8 scales included), and graceful degradation and retries
+(PagedAttentionEngine.swift:375-418).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import TOL, row_rel_err, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    return torch
+
+
+def _p(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def _lib():
+    from pagedattentionmetal_amd import _lib
+    return _lib.load()
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+def test_cabi_append_prefill_decode_on_device(torch, dtype):
+    from pagedattentionmetal_amd import KVCacheManager, PagedAttentionEngine
+    lib = _lib()
+    eng = PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    hkv, H, d, bs = 4, 16, 128, 16
+    cache = KVCacheManager(eng, 64, bs, d, hkv, dtype)
+    rng = np.random.default_rng(40 + dtype)
+    io = np.float32 if dtype == 0 else np.float16
+    tdt = torch.float32 if dtype == 0 else torch.float16
+    lens = {7: 100, 9: 37}
+    for sid, L in lens.items():
+        cache.allocate_sequence(sid)
+        cache.append_tokens(sid, L)
+        keys = to_dev(rng.standard_normal((L, hkv, d)).astype(io))
+        vals = to_dev(rng.standard_normal((L, hkv, d)).astype(io))
+        assert lib.pam_append_kv(eng.handle, cache.handle, sid, _p(keys), _p(vals), 0, L, hkv) == 0, \
+            lib.pam_last_error(eng.handle)
+    torch.cuda.synchronize()
+    kh, vh = to_host(cache.k_pool()), to_host(cache.v_pool())
+    ks = vs = None
+    if dtype == 2:
+        ks, vs = to_host(cache.k_scale()).view(np.uint16), to_host(cache.v_scale()).view(np.uint16)
+
+    # pam_prefill: causal attention over the whole sequence 7
+    L = lens[7]
+    q = rng.standard_normal((L, H, d)).astype(io)
+    out = torch.zeros((L, H, d), dtype=tdt, device="cuda")
+    assert lib.pam_prefill(eng.handle, cache.handle, 7, _p(to_dev(q)), _p(out), L, H, True) == 0, \
+        lib.pam_last_error(eng.handle)
+    bt7 = np.array(cache.get_block_table(7), np.int32)
+    ref = oracle.prefill(dtype, q, kh, vh, bt7, 0, causal=True, k_scale=ks, v_scale=vs)
+    err = row_rel_err(to_host(out), ref)
+    assert err <= TOL[dtype], f"pam_prefill rel err {err:.3e}"
+
+    # pam_decode over both sequences (zero-padded batch slab built by the library)
+    ids = (C.c_int64 * 2)(9, 7)
+    qd = rng.standard_normal((2, H, d)).astype(io)
+    outd = torch.zeros((2, H, d), dtype=tdt, device="cuda")
+    assert lib.pam_decode(eng.handle, cache.handle, ids, 2, _p(to_dev(qd)), _p(outd), H) == 0, \
+        lib.pam_last_error(eng.handle)
+    t9, t7 = cache.get_block_table(9), cache.get_block_table(7)
+    slab = np.zeros((2, max(len(t9), len(t7))), np.int32)
+    slab[0, :len(t9)], slab[1, :len(t7)] = t9, t7
+    ref = oracle.decode(dtype, qd, kh, vh, slab, np.array([lens[9], lens[7]], np.uint32), H,
+                        k_scale=ks, v_scale=vs)
+    err = row_rel_err(to_host(outd), ref)
+    assert err <= TOL[dtype], f"pam_decode rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [1, 2])
+def test_copy_on_write_copies_block_and_scales_in_hbm(torch, dtype):
+    """Two sequences share a prefix block via block hashes; making one exclusive
+    gives it a new physical block holding the same bytes (and FP8 scales)."""
+    from pagedattentionmetal_amd import KVCacheManager, PagedAttentionEngine
+    lib = _lib()
+    eng = PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    hkv, d, bs = 2, 64, 16
+    cache = KVCacheManager(eng, 16, bs, d, hkv, dtype)
+    rng = np.random.default_rng(77)
+    cache.allocate_sequence(1)
+    cache.append_tokens(1, 20, block_hashes=[0xABC, 0xDEF])
+    keys = to_dev(rng.standard_normal((20, hkv, d)).astype(np.float16))
+    vals = to_dev(rng.standard_normal((20, hkv, d)).astype(np.float16))
+    assert lib.pam_append_kv(eng.handle, cache.handle, 1, _p(keys), _p(vals), 0, 20, hkv) == 0
+    cache.allocate_sequence(2)
+    cache.append_tokens(2, 16, block_hashes=[0xABC])  # prefix hit on the first block
+    t1, t2 = cache.get_block_table(1), cache.get_block_table(2)
+    assert t2[0] == t1[0], "prefix block is shared"
+    cache.ensure_exclusive_access(2, 0)
+    torch.cuda.synchronize()
+    t2b = cache.get_block_table(2)
+    assert t2b[0] != t1[0], "copy-on-write moved the writer to a new block"
+    kh, vh = to_host(cache.k_pool()), to_host(cache.v_pool())
+    assert np.array_equal(kh[t2b[0]].view(np.uint8), kh[t1[0]].view(np.uint8))
+    assert np.array_equal(vh[t2b[0]].view(np.uint8), vh[t1[0]].view(np.uint8))
+    if dtype == 2:
+        ks, vs = to_host(cache.k_scale()).view(np.uint16), to_host(cache.v_scale()).view(np.uint16)
+        assert ks[t2b[0]] == ks[t1[0]] and vs[t2b[0]] == vs[t1[0]] and ks[t1[0]] != 0
+
+
+def test_graceful_degradation_and_retries(torch):
+    """A failed launch: with graceful degradation on, the call succeeds with a
+    zero-filled output; off, it returns the error; a transient failure within the
+    retry budget is retried and the result is correct."""
+    from pagedattentionmetal_amd import PagedAttentionEngine, PagedAttentionError, PagedLayerSpec
+    eng = PagedAttentionEngine()
+    rng = np.random.default_rng(3)
+    H, hkv, d, bs = 8, 8, 64, 16
+    lens = np.array([40, 17], np.uint32)
+    nb = 8
+    k = rng.standard_normal((nb, bs, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((nb, bs, hkv, d)).astype(np.float16)
+    q = rng.standard_normal((2, H, d)).astype(np.float16)
+    bt = np.array([[0, 1, 2], [3, 4, 0]], np.int32)
+    args = (to_dev(q), to_dev(k), to_dev(v), to_dev(bt), to_dev(lens))
+    layer = PagedLayerSpec(d, H, hkv, bs, 1)
+    ref = oracle.decode(1, q, k, v, bt, lens, H)
+
+    out = torch.full((2, H, d), 7.0, dtype=torch.float16, device="cuda")
+    eng.set_graceful_degradation(True)
+    eng.set_max_retries(1)
+    eng.debug_fail_next_launches(5)
+    eng.decode(*args, out, 2, 3, layer)
+    assert np.all(to_host(out) == 0), "degraded call zero-fills its output"
+
+    eng.set_graceful_degradation(False)
+    eng.debug_fail_next_launches(5)
+    with pytest.raises(PagedAttentionError):
+        eng.decode(*args, out, 2, 3, layer)
+
+    eng.debug_fail_next_launches(0)
+    eng.set_max_retries(3)
+    eng.debug_fail_next_launches(2)  # fails twice, the third attempt runs
+    eng.decode(*args, out, 2, 3, layer)
+    err = row_rel_err(to_host(out), ref)
+    assert err <= TOL[1], f"rel err after retries {err:.3e}"

@@ -1,0 +1,141 @@
+"""GPU parity at the benchmark configurations' full sizes (c1, c2, c4, c5 decode and
+the c3 mixed continuous-batching step), on the same seeded inputs bench.py uses.
+
+The oracle checks every decode row.  Only the pool blocks the block tables
+reference are copied to the host: they are gathered on the device into a compact
+pool and the tables are renumbered.  A windowed row keeps just the blocks of
+its last W tokens; its other entries point at block 0 and are never read.
+For the c3 prefill chunks the oracle checks three 16-row slices per chunk: the
+first, middle and last rows.  The appended K/V bytes are compared in full.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from helpers import TOL, row_rel_err, to_dev, to_host, worst_rows
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    return torch
+
+
+def compact_pools(torch, bt, lens, window, bs, pools, scales=()):
+    """Gather the blocks each row reads into a dense pool; returns host arrays
+    (pools..., scales...) and the renumbered table."""
+    bt = np.asarray(bt)
+    need = {}
+    new_bt = np.zeros_like(bt)
+    for b, L in enumerate(np.asarray(lens, np.int64)):
+        first = max(0, L - window) // bs if window > 0 else 0
+        for i in range(first, (L + bs - 1) // bs):
+            new_bt[b, i] = need.setdefault(int(bt[b, i]), len(need))
+    order = torch.tensor(sorted(need, key=need.get), dtype=torch.long, device=pools[0].device)
+    out = [to_host(p.index_select(0, order)) for p in pools]
+    out += [to_host(s.index_select(0, order)) for s in scales]
+    return out, new_bt
+
+
+def decode_inputs(torch, k):
+    """Device tensors of decode workload k, as bench.decode_setup builds them."""
+    from pagedattentionmetal_amd import api, workloads
+    w = workloads.config(k)
+    q, kp, vp = workloads.device_pools(w)
+    eng = api.PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    bt = torch.from_numpy(w.block_tables).cuda()
+    ks = vs = None
+    if w.data_type == 2:
+        src_k, src_v = kp, vp
+        kp = torch.zeros(src_k.shape, dtype=torch.uint8, device="cuda")
+        vp = torch.zeros_like(kp)
+        ks = torch.zeros(w.pool_blocks, dtype=torch.float16, device="cuda")
+        vs = torch.zeros_like(ks)
+        lay = api.PagedLayerSpec(w.head_dim, w.num_kv_heads, w.num_kv_heads, w.block_size, 2)
+        for b in range(w.batch):
+            L = int(w.seq_lens[b])
+            tok = torch.arange(L, device="cuda")
+            phys = bt[b][tok // w.block_size].long()
+            eng.append_to_cache(src_k[phys, tok % w.block_size].contiguous(),
+                                src_v[phys, tok % w.block_size].contiguous(), kp, vp, bt[b].contiguous(), 0, L, lay,
+                                k_scale=ks, v_scale=vs)
+        del src_k, src_v
+    return w, eng, q, kp, vp, bt, ks, vs
+
+
+@pytest.mark.parametrize("k", [1, 2, 4, 5])
+def test_decode_config_full_size(torch, k):
+    from pagedattentionmetal_amd import api
+    w, eng, q, kp, vp, bt, ks, vs = decode_inputs(torch, k)
+    lens = torch.from_numpy(w.seq_lens.view(np.int32)).cuda()
+    out = torch.empty_like(q)
+    layer = api.PagedLayerSpec(w.head_dim, w.num_heads, w.num_kv_heads, w.block_size, w.data_type, w.window)
+    eng.decode(q, kp, vp, bt, lens, out, w.batch, w.max_num_blocks, layer, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    scales = () if ks is None else (ks, vs)
+    host, cbt = compact_pools(torch, w.block_tables, w.seq_lens, w.window, w.block_size, (kp, vp), scales)
+    kh, vh = host[0], host[1]
+    ksh = vsh = None
+    if ks is not None:
+        ksh, vsh = host[2].view(np.uint16), host[3].view(np.uint16)
+    ref = oracle.decode(w.data_type, to_host(q), kh, vh, cbt, w.seq_lens, w.num_heads, window=w.window,
+                        k_scale=ksh, v_scale=vsh, n_threads=16)
+    got = to_host(out)
+    err = row_rel_err(got, ref)
+    assert err <= TOL[w.data_type], f"c{k}: rel err {err:.3e}; worst (row, head, err): {worst_rows(got, ref)}"
+
+
+def test_mixed_step_c3_full_size(torch):
+    from pagedattentionmetal_amd import api, workloads
+    w = workloads.mixed_config()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(w.seed)
+    shape = (w.pool_blocks, w.block_size, w.num_kv_heads, w.head_dim)
+    kp = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
+    vp = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
+    rows = w.total_rows
+    q = torch.randn((rows, w.num_heads, w.head_dim), generator=g, device="cuda", dtype=torch.float32).half()
+    nk = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
+    nv = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
+    bt = torch.from_numpy(w.block_tables).cuda()
+    out = torch.empty_like(q)
+    eng = api.PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    layer = api.PagedLayerSpec(w.head_dim, w.num_heads, w.num_kv_heads, w.block_size, 1)
+    eng.mixed_step(q, out, kp, vp, bt, w.context_lens, w.query_lens, layer, new_keys=nk, new_values=nv)
+    torch.cuda.synchronize()
+
+    ctx, ql, bs = w.context_lens.astype(np.int64), w.query_lens.astype(np.int64), w.block_size
+    total = ctx + ql
+    host, cbt = compact_pools(torch, w.block_tables, total, 0, bs, (kp, vp))
+    kh, vh = host
+    # appended rows landed at their slots, bit for bit
+    nkh, nvh = to_host(nk), to_host(nv)
+    r0 = 0
+    for s in range(len(ctx)):
+        pos = ctx[s] + np.arange(ql[s])
+        blk, slot = cbt[s][pos // bs], pos % bs
+        assert np.array_equal(kh[blk, slot].view(np.uint16), nkh[r0:r0 + ql[s]].view(np.uint16)), f"K append seq {s}"
+        assert np.array_equal(vh[blk, slot].view(np.uint16), nvh[r0:r0 + ql[s]].view(np.uint16)), f"V append seq {s}"
+        r0 += int(ql[s])
+
+    qh, got = to_host(q), to_host(out)
+    cu = np.concatenate([[0], np.cumsum(ql)])
+    # decode rows: every one
+    dec = np.nonzero(ql == 1)[0]
+    ref_dec = oracle.decode(1, qh[cu[dec]], kh, vh, cbt[dec], total[dec].astype(np.uint32), w.num_heads,
+                            n_threads=16)
+    err = row_rel_err(got[cu[dec]], ref_dec)
+    assert err <= TOL[1], f"decode rows: rel err {err:.3e}"
+    # prefill chunks: first, middle and last 16 rows of each
+    for s in np.nonzero(ql > 1)[0]:
+        T = int(ql[s])
+        for i0 in (0, T // 2 - 8, T - 16):
+            rows_ = slice(cu[s] + i0, cu[s] + i0 + 16)
+            ref = oracle.prefill(1, qh[rows_], kh, vh, cbt[s], int(ctx[s]) + i0, causal=True, n_threads=16)
+            # prefill restates a chunk at [q_offset, q_offset + 16): its keys end at q_offset + 16 <= total
+            e = row_rel_err(got[rows_], ref)
+            assert e <= TOL[1], f"chunk {s} rows {i0}..{i0 + 16}: rel err {e:.3e}"
