@@ -143,6 +143,10 @@ struct MfmaShape {
     static constexpr int KL = HD + 8;                         // K row in LDS (halves): odd 16-byte units
     static constexpr int VL = HD + 16;                        // V row in LDS (halves)
     static constexpr int NW = kMfmaWaves;
+    // register tiles in flight per wave, and resident workgroups per CU the
+    // registers allow (f16 rows need twice the registers of e4m3 rows)
+    static constexpr int DEPTH = (sizeof(KV) == 2 && HD <= 128) ? 3 : 2;
+    static constexpr int OCC = HD >= 256 ? 1 : ((sizeof(KV) == 2 && HD == 128) ? 2 : 3);
     static constexpr int WT = 16 * (KL + VL);                 // halves of one wave's K and V tiles
     static constexpr int kSmemBytes = NW * WT * 2 > NW * 16 * HD * 4 ? NW * WT * 2 : NW * 16 * HD * 4;
     static_assert(64 % LPR == 0 && 16 % RPI == 0, "token rows must tile the wave");
@@ -224,7 +228,7 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
     // Block-table entries of 64 consecutive blocks from window_blk sit in one
     // VGPR (lane i = block window_blk + i), refreshed once per 16-tile chunk, so
     // a tile's address never waits on a table load.  The window covers the
-    // chunk's tiles and the two tiles loaded ahead of its end.
+    // chunk's tiles and the tiles loaded ahead of its end.
     const int nlb = (c.k_hi + bs - 1) >> bsh;  // blocks holding keys of this row
     int window_blk = 0;
     int32_t bt_window = 0;
@@ -326,9 +330,9 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
 #pragma unroll
     for (int i = 0; i < NO; i++) o[i] = (f32x4)0.0f;
 
-    // Two register tiles in flight per wave.  As soon as a tile's rows sit in
-    // LDS, its registers are refilled with the tile two ahead, so the next tile
-    // is always loading while this one's scores, softmax and PV run.
+    // DEPTH register tiles in flight per wave.  As soon as a tile's rows sit in
+    // LDS, its registers are refilled with the tile DEPTH ahead, so the next
+    // tiles are always loading while this one's scores, softmax and PV run.
     auto step = [&](int tile, Tile &t) {
         // keep the scheduler from hoisting the next tile's work (and with it the
         // wait for its loads) into this one
@@ -344,7 +348,7 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
         stage_rows(t.v, t.vsb, vs, vt, VL);
         // LDS ops of one wave execute in order; the wave barrier pins the compiler's
         __builtin_amdgcn_wave_barrier();
-        load_tile(tile + 2, t);
+        load_tile(tile + S::DEPTH, t);
 
         // S^T[token][head] over HD dims: K row `row`, dims 32i + 8g .. +8
         f32x4 s = (f32x4)0.0f;
@@ -390,21 +394,24 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
         __builtin_amdgcn_wave_barrier();
     };
 
-    // 16-tile chunks run as straight-line code: inside a chunk the compiler can
+    // 15- or 16-tile chunks run as straight-line code: inside a chunk the compiler can
     // count outstanding loads exactly and waits only for the tile it consumes (a
     // loop back edge makes it drain everything).  Exits are uniform branches.
     if (pr.t_begin < pr.t_end) {
-    Tile ta, tb;
+    constexpr int CH = S::DEPTH * (16 / S::DEPTH);  // tiles per straight-line chunk
+    Tile ta, tb, tc;
     load_tile(pr.t_begin, ta);
     load_tile(pr.t_begin + 1, tb);
-    for (int chunk = pr.t_begin; chunk < pr.t_end; chunk += 16) {
+    if constexpr (S::DEPTH == 3) load_tile(pr.t_begin + 2, tc);
+    for (int chunk = pr.t_begin; chunk < pr.t_end; chunk += CH) {
         if (chunk != pr.t_begin) refresh_window(chunk);
 #pragma unroll
-        for (int k2 = 0; k2 < 16; k2 += 2) {
-            const int tile = chunk + k2;
-            if (k2 > 0 && tile >= pr.t_end) break;
+        for (int k = 0; k < CH; k += S::DEPTH) {
+            const int tile = chunk + k;
+            if (k > 0 && tile >= pr.t_end) break;
             step(tile, ta);
-            step(tile + 1, tb);  // a tile past the partition end is fully masked
+            step(tile + 1, tb);  // tiles past the partition end are fully masked
+            if constexpr (S::DEPTH == 3) step(tile + 2, tc);
         }
     }
     }
@@ -460,7 +467,7 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
 }
 
 template <typename KV, int HD, int BLK>
-__global__ __launch_bounds__(64 * kMfmaWaves, HD >= 256 ? 1 : 3) void attn_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void attn_mfma_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[MfmaShape<KV, HD>::kSmemBytes];
     __shared__ float sm_ml[kMfmaWaves][16][2];
     mfma_item<KV, HD, BLK>(p, blockIdx.z, blockIdx.x, blockIdx.y, smem, sm_ml);
@@ -471,7 +478,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves, HD >= 256 ? 1 : 3) void attn_mfma_
 // on empty partitions of short rows and the wave slots stay full to the end.
 // Every workgroup builds the list's row prefix sums in LDS from the row ranges.
 template <typename KV, int HD, int BLK>
-__global__ __launch_bounds__(64 * kMfmaWaves, HD >= 256 ? 1 : 3) void attn_mfma_persistent(AttnParams p) {
+__global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void attn_mfma_persistent(AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[MfmaShape<KV, HD>::kSmemBytes];
     __shared__ float sm_ml[kMfmaWaves][16][2];
     __shared__ int32_t prefix[kPersistentMaxRows + 1];
