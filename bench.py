@@ -73,6 +73,8 @@ def time_decode(torch, eng, w, t, steps, warmup):
     def step():
         eng.decode(q, kp, vp, bt, lens, out, w.batch, w.max_num_blocks, layer, k_scale=ks, v_scale=vs)
 
+    # the timed steps run as a serving loop would: no per-call timing events
+    eng.set_gpu_timing(False)
     for _ in range(max(warmup, 1)):
         step()
     torch.cuda.synchronize()
@@ -83,6 +85,7 @@ def time_decode(torch, eng, w, t, steps, warmup):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    eng.set_gpu_timing(True)
     # per-kernel durations: HIP events recorded by the engine around each launch
     kern, red = [], []
     for _ in range(steps):
@@ -134,6 +137,8 @@ def time_mixed(torch, eng, w, t, steps, warmup):
         eng.mixed_step(q[:rows_ch], out[:rows_ch], kp, vp, bt[:nch], ctx[:nch], ql[:nch], layer)
 
     assert (ql[:nch] > 1).all() and (ql[nch:] == 1).all()
+    # the timed steps run as a serving loop would: no per-call timing events
+    eng.set_gpu_timing(False)
     for _ in range(max(warmup, 1)):
         step()
     torch.cuda.synchronize()
@@ -144,6 +149,7 @@ def time_mixed(torch, eng, w, t, steps, warmup):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    eng.set_gpu_timing(True)
     for _ in range(max(warmup, 1)):
         prefill_only()
     kern = []

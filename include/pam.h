@@ -265,6 +265,10 @@ int32_t pam_reserve_workspace(void *context, size_t bytes);
 int32_t pam_set_partition_tokens(void *context, int32_t tokens);
 /* Kernel choice for decode: 0 automatic, 1 force VALU, 2 force MFMA (when supported). */
 int32_t pam_set_decode_kernel(void *context, int32_t choice);
+/* true (default): time every call's kernels with HIP events (the elapsed, kernel
+ * and reduce times of pam_engine_last_stats); false: no events are recorded and
+ * those times read -1. */
+int32_t pam_set_gpu_timing(void *context, bool enabled);
 
 /* Mixed continuous-batching step: every sequence s appends query_lens[s] new
  * tokens after context_lens[s] cached ones (query_lens = 1 is a decode), the new

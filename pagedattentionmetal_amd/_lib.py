@@ -122,6 +122,7 @@ SIGNATURES = {
     "pam_reserve_workspace": (I32, [P, SZ]),
     "pam_set_partition_tokens": (I32, [P, I32]),
     "pam_set_decode_kernel": (I32, [P, I32]),
+    "pam_set_gpu_timing": (I32, [P, C.c_bool]),
     "pam_engine_mixed_step": (I32, [P, C.POINTER(MixedRequest)]),
     "pam_fp8_quantize": (I32, [P, P, P, P, I64]),
     "pam_fp8_dequant": (I32, [P, P, P, P, I64]),

@@ -174,6 +174,10 @@ class PagedAttentionEngine:
     def set_decode_kernel(self, choice: int):
         self._check(lib().pam_set_decode_kernel(self._ctx, int(choice)))
 
+    def set_gpu_timing(self, enabled: bool):
+        """HIP-event timing of every call (last_stats times); off: no events, times -1."""
+        self._check(lib().pam_set_gpu_timing(self._ctx, bool(enabled)))
+
     def reserve_workspace(self, nbytes: int):
         self._check(lib().pam_reserve_workspace(self._ctx, int(nbytes)))
 

@@ -113,8 +113,10 @@ __device__ __forceinline__ f16x8 e4m3x8_to_f16x8(uint32_t w0, uint32_t w1) {
 // Waves per workgroup of the MFMA kernel: they split one partition's tiles and
 // merge their softmax states in LDS.
 constexpr int kMfmaWaves = 4;
-// Rows the persistent form can index from LDS (its item table).
+// Rows the stream-K form can index from LDS (its row prefix table).
 constexpr int kPersistentMaxRows = 2048;
+// Fewest tiles per stream-K unit: shorter units would only add partials.
+constexpr int kStreamKMinTiles = 8;
 
 // How a 16-token tile finds its physical blocks.
 enum BlockMode : int {
@@ -152,8 +154,11 @@ struct MfmaShape {
     static_assert(64 % LPR == 0 && 16 % RPI == 0, "token rows must tile the wave");
 };
 
-// One work item: (row r, split-context partition `part`, kv head kvh) on the
-// whole workgroup.  Returns uniformly across the workgroup.
+// The tile loop shared by both work forms: tiles [t_begin, t_end) of row
+// context c for kv head kvh, on the calling wave alone, using its LDS tiles kt
+// (K) and kt + 16 * KL (V).  Leaves the wave's online-softmax state: m_run (log2
+// units, per head), l_run (this lane's share of the row sum) and o[i], lane
+// (head `lane % 16`, quad `lane / 16`) holding dims 16i + 4 quad .. +4.
 //
 // Loads: 16 lanes (8 for e4m3) cover one token row's HD elements with 16-byte
 // loads, so each load instruction reads whole 256-byte rows (measured on
@@ -164,38 +169,18 @@ struct MfmaShape {
 // O^T = V^T P^T (v_mfma_f32_16x16x16_f16), whose B operand is the S^T
 // accumulator layout itself (lane%16 = head, lane/16 = token quad).
 template <typename KV, int HD, int BLK>
-__device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, int kvh, char *smem,
-                                          float (*sm_ml)[16][2]) {
+__device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, int kvh, const PartRange pr, f16 *kt,
+                                          float &m_run, float &l_run, f32x4 (&o)[MfmaShape<KV, HD>::NO]) {
     using S = MfmaShape<KV, HD>;
     constexpr int NC = S::NC, NO = S::NO, EPL = S::EPL, LPR = S::LPR, RPI = S::RPI, NI = S::NI, KL = S::KL,
-                  VL = S::VL, NW = S::NW, WT = S::WT;
+                  VL = S::VL;
     constexpr bool kFp8 = sizeof(KV) == 1;
     constexpr bool kTileScale = kFp8 && BLK == kBlkTile;  // one block (one scale pair) per tile
-    const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
     const int H = p.num_heads;
     const int G = H / p.num_kv_heads;
-    const RowCtx c = row_ctx(p, r);
-    const PartRange wg = part_range(c, part, p.part_tokens);
-    if (part >= (wg.nparts > 1 ? wg.nparts : 1)) return;
-
     const int h = kvh * G + row;  // this lane's query head (N column)
     const bool head_ok = row < G;
-    f16 *out = static_cast<f16 *>(p.out);
-    if (wg.nparts == 0) {
-        // no keys: 0/0 as in the reference's m/l bookkeeping
-        for (int idx = threadIdx.x; idx < G * HD; idx += 64 * NW)
-            out[(c.out_row * H + kvh * G) * (int64_t)HD + idx] = (f16)__builtin_nanf("");
-        return;
-    }
-    // this wave's contiguous share of the workgroup's tiles (possibly empty)
-    PartRange pr = wg;
-    {
-        const int per = (wg.t_end - wg.t_begin + NW - 1) / NW;
-        pr.t_begin = wg.t_begin + wave * per;
-        pr.t_end = pr.t_begin + per < wg.t_end ? pr.t_begin + per : wg.t_end;
-    }
-    f16 *kt = reinterpret_cast<f16 *>(smem) + wave * WT;
     f16 *vt = kt + 16 * KL;
 
     // Q^T B operand: lane holds Q[h][32c + 8g .. +8] for chunk c
@@ -325,8 +310,8 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
         }
     };
 
-    float m_run = -INFINITY, l_run = 0.0f;
-    f32x4 o[NO];
+    m_run = -INFINITY;
+    l_run = 0.0f;
 #pragma unroll
     for (int i = 0; i < NO; i++) o[i] = (f32x4)0.0f;
 
@@ -415,9 +400,46 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
         }
     }
     }
+}
 
+// One work item of the workgroup form: (row r, split-context partition `part`,
+// kv head kvh) shared by the whole workgroup.  Each wave takes a contiguous
+// share of the partition's tiles; the waves merge their softmax states in LDS
+// and write the output (one partition) or the partial for the reduce kernel.
+// Returns uniformly across the workgroup.
+template <typename KV, int HD, int BLK>
+__device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, int kvh, char *smem,
+                                          float (*sm_ml)[16][2]) {
+    using S = MfmaShape<KV, HD>;
+    constexpr int NO = S::NO, NW = S::NW, WT = S::WT;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
+    const int H = p.num_heads;
+    const int G = H / p.num_kv_heads;
+    const RowCtx c = row_ctx(p, r);
+    const PartRange wg = part_range(c, part, p.part_tokens);
+    if (part >= (wg.nparts > 1 ? wg.nparts : 1)) return;
+    const bool head_ok = row < G;
+    f16 *out = static_cast<f16 *>(p.out);
+    if (wg.nparts == 0) {
+        // no keys: 0/0 as in the reference's m/l bookkeeping
+        for (int idx = threadIdx.x; idx < G * HD; idx += 64 * NW)
+            out[(c.out_row * H + kvh * G) * (int64_t)HD + idx] = (f16)__builtin_nanf("");
+        return;
+    }
+    // this wave's contiguous share of the workgroup's tiles (possibly empty)
+    PartRange pr = wg;
+    {
+        const int per = (wg.t_end - wg.t_begin + NW - 1) / NW;
+        pr.t_begin = wg.t_begin + wave * per;
+        pr.t_end = pr.t_begin + per < wg.t_end ? pr.t_begin + per : wg.t_end;
+    }
+    float m_run, l_run;
+    f32x4 o[NO];
+    mfma_core<KV, HD, BLK>(p, c, kvh, pr, reinterpret_cast<f16 *>(smem) + wave * WT, m_run, l_run, o);
     float l_tot = l_run + shfl_xor(l_run, 16);
     l_tot += shfl_xor(l_tot, 32);
+
 
     // Merge the waves' states.  The merge area overlays the K/V tiles, so every
     // wave must be done with its tiles first.
@@ -473,28 +495,49 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
     mfma_item<KV, HD, BLK>(p, blockIdx.z, blockIdx.x, blockIdx.y, smem, sm_ml);
 }
 
-// Persistent form: a grid sized to the resident capacity walks a compacted list
-// of items, (row, partition) major and kv head minor, so no workgroup is spent
-// on empty partitions of short rows and the wave slots stay full to the end.
-// Every workgroup builds the list's row prefix sums in LDS from the row ranges.
+// Agent-scope (sc1) 16- and 8-byte accesses to the stream-K partials: stores
+// write through the XCD's L2 and loads do not hit a stale line there, so a
+// partial written on one XCD can be merged on another without a whole-L2
+// writeback.  Offsets are bytes from the partial area's base (< 2 GiB).
+constexpr int kSc1 = 16;  // cache-policy bits of an agent-scope access on gfx950
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const AttnParams &p) {
+    return __builtin_amdgcn_make_buffer_rsrc(p.part_o, 0, (int)p.part_bytes, 0x00020000);
+}
+
+// Stream-K form (rows <= kPersistentMaxRows).  The key tiles of all rows are laid
+// end to end on one line, row after row.  The workgroups are taken in runs of
+// NHG = Hkv / NH (NH = 4, 2 or 1 kv heads, the largest dividing Hkv, read side by
+// side by the NH waves of a workgroup): the run of unit u covers tiles
+// [u T / U, (u + 1) T / U) of the line, one workgroup per head group, so all
+// heads of a tile are read at about the same time.  Every wave streams the same
+// number of tiles (+-1) whatever the row lengths, and no wave waits on another.
+//
+// A unit that covers part of a row leaves a partial softmax state per head.
+// It is written with write-through stores, then the (row, kv head) counter is
+// incremented; the wave that brings it to the number of units covering the row
+// merges all partials with the whole wave (write-through loads), writes the
+// output and resets the counter to 0.  A row inside one unit is finished in
+// registers.  No reduce kernel runs.  The partials of (unit u, row r) sit in slot
+// block u + r, unique because a row's units start where the previous row's end:
+// floats [((u + r) * Hkv + kvh) * G + g] * d for query head g of kv head kvh.
 template <typename KV, int HD, int BLK>
-__global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void attn_mfma_persistent(AttnParams p) {
-    __shared__ __attribute__((aligned(16))) char smem[MfmaShape<KV, HD>::kSmemBytes];
-    __shared__ float sm_ml[kMfmaWaves][16][2];
+__global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void attn_mfma_streamk(AttnParams p) {
+    using S = MfmaShape<KV, HD>;
+    constexpr int NO = S::NO, WT = S::WT;
+    __shared__ __attribute__((aligned(16))) f16 tiles[kMfmaWaves * WT];
     __shared__ int32_t prefix[kPersistentMaxRows + 1];
     __shared__ int32_t chunk_sum[64 * kMfmaWaves];
     constexpr int NT = 64 * kMfmaWaves;
     const int tid = threadIdx.x;
     const int rows = p.rows;
-    // each thread counts the items of a contiguous run of rows (a row with no
-    // keys still needs one item to write its 0/0 output)
+    // tiles per row (0 for a row without keys), prefix-summed in LDS
     const int per = (rows + NT - 1) / NT;
     const int r0 = tid * per, r1 = r0 + per < rows ? r0 + per : rows;
     int32_t run = 0;
     for (int rr = r0; rr < r1; rr++) {
-        const int np = part_range(row_ctx(p, rr), 0, p.part_tokens).nparts;
+        const PartRange whole = part_range(row_ctx(p, rr), 0, 1 << 30);
         prefix[rr] = run;
-        run += np > 1 ? np : 1;
+        run += whole.nparts > 0 ? whole.t_end - whole.t_begin : 0;
     }
     chunk_sum[tid] = run;
     __syncthreads();
@@ -509,26 +552,140 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
     for (int rr = r0; rr < r1; rr++) prefix[rr] += base;
     if (tid == NT - 1) prefix[rows] = chunk_sum[NT - 1];
     __syncthreads();
-    const int32_t total = prefix[rows] * p.num_kv_heads;
-    // Items are dealt in rounds of gridDim.x, alternating direction (a snake), so
-    // a workgroup that drew an early, long partition draws a late, short one next.
-    for (int32_t k = 0;; k++) {
-        const int32_t item = k * (int32_t)gridDim.x + ((k & 1) ? (int32_t)gridDim.x - 1 - (int32_t)blockIdx.x
-                                                                 : (int32_t)blockIdx.x);
-        if (item >= total) {
-            if (k * (int32_t)gridDim.x >= total) break;
-            continue;  // a short last round: this workgroup's slot is empty
+
+    const int H = p.num_heads, Hkv = p.num_kv_heads, G = H / Hkv;
+    f16 *out = static_cast<f16 *>(p.out);
+    // rows without keys: 0/0 as in the reference's m/l bookkeeping
+    for (int rr = blockIdx.x; rr < rows; rr += gridDim.x)
+        if (prefix[rr + 1] == prefix[rr]) {
+            const int orow = row_ctx(p, rr).out_row;
+            for (int idx = tid; idx < H * HD; idx += NT) out[(int64_t)orow * H * HD + idx] = (f16)__builtin_nanf("");
         }
-        const int32_t q = item / p.num_kv_heads;
-        const int kvh = item - q * p.num_kv_heads;
-        int lo = 0, hi = rows;  // last row with prefix[row] <= q
+
+    const int NH = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
+    const int WPH = kMfmaWaves / NH, NHG = Hkv / NH;
+    // wave-uniform values read from LDS are moved to scalar registers
+    const int64_t T = __builtin_amdgcn_readfirstlane(prefix[rows]);
+    int64_t U = (int64_t)gridDim.x * WPH / NHG;
+    const int64_t u_cap = (T + kStreamKMinTiles - 1) / kStreamKMinTiles;
+    if (U > u_cap) U = u_cap;
+    const int wave = tid >> 6, lane = tid & 63, row = lane & 15, grp = lane >> 4;
+    const int64_t wu = (int64_t)blockIdx.x * WPH + wave / NH;  // workgroup unit
+    const int64_t u = wu / NHG;
+    const int kvh = (int)(wu % NHG) * NH + wave % NH;
+    if (u >= U) return;  // no workgroup barrier follows
+    const bool head_ok = row < G;
+    f16 *kt = tiles + wave * WT;
+    const __amdgpu_buffer_rsrc_t prs = part_rsrc(p);
+    const int ml_off = (int)((const char *)p.part_ml - (const char *)p.part_o);  // bytes
+    using gint = __attribute__((address_space(1))) int32_t;
+
+    const int64_t x1 = (u + 1) * T / U;
+    for (int64_t x = u * T / U; x < x1;) {
+        // the row holding line position x: last r with prefix[r] <= x
+        int lo = 0, hi = rows;
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
-            if (prefix[mid] <= q) lo = mid;
+            if (prefix[mid] <= x) lo = mid;
             else hi = mid;
         }
-        __syncthreads();  // the previous item's LDS use is over
-        mfma_item<KV, HD, BLK>(p, lo, q - prefix[lo], kvh, smem, sm_ml);
+        lo = __builtin_amdgcn_readfirstlane(lo);
+        const int64_t P = __builtin_amdgcn_readfirstlane(prefix[lo]);
+        const int nt = __builtin_amdgcn_readfirstlane(prefix[lo + 1]) - (int)P;  // > 0: x lies inside this row
+        const int64_t e = x1 < P + nt ? x1 : P + nt;
+        const RowCtx c = row_ctx(p, lo);
+        const int tile0 = c.k_lo / 16;
+        PartRange pr;
+        pr.t_begin = tile0 + (int)(x - P);
+        pr.t_end = tile0 + (int)(e - P);
+        pr.nparts = 1;
+        const int64_t first = ((P + 1) * U - 1) / T, last = ((P + nt) * U - 1) / T;
+        const int nseg = (int)(last - first + 1);
+        x = e;
+
+        float m_run, l_run;
+        f32x4 o[NO];
+        mfma_core<KV, HD, BLK>(p, c, kvh, pr, kt, m_run, l_run, o);
+        float l_tot = l_run + shfl_xor(l_run, 16);
+        l_tot += shfl_xor(l_tot, 32);
+        f16 *orow = out + ((int64_t)c.out_row * H + kvh * G) * HD;  // this kv head's G heads
+
+        if (nseg == 1) {
+            if (head_ok) {
+                const float inv = 1.0f / l_tot;
+#pragma unroll
+                for (int i = 0; i < NO; i++) {
+                    f16x4 v;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) v[q] = (f16)(o[i][q] * inv);
+                    *reinterpret_cast<f16x4 *>(orow + row * HD + 16 * i + 4 * grp) = v;
+                }
+            }
+            continue;
+        }
+        // publish this unit's partial and count it
+        auto slot0 = [&](int64_t uu) { return ((uu + lo) * Hkv + kvh) * (int64_t)G; };  // head g: + g
+        if (head_ok) {
+            const int ob = (int)((slot0(u) + row) * HD * 4) + 16 * grp;
+#pragma unroll
+            for (int i = 0; i < NO; i++) __builtin_amdgcn_raw_buffer_store_b128(o[i], prs, ob + 64 * i, 0, kSc1);
+            if (grp == 0) {
+                const f32x2 ml = {m_run, l_tot};
+                __builtin_amdgcn_raw_buffer_store_b64(ml, prs, ml_off + (int)((slot0(u) + row) * 8), 0, kSc1);
+            }
+        }
+        // the stores have completed (written through) before the count
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        gint *cnt = (gint *)(p.seg_count + (int64_t)lo * Hkv + kvh);
+        int32_t old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old != nseg - 1) continue;
+
+        // Last unit of this (row, kv head): merge all partials, the whole wave at
+        // once.  The G * HD floats of one unit are contiguous; the lane owns the
+        // 4-float pieces v = lane + 64 k (head 4v / HD), four units in flight.
+        const int nv = G * HD / 4;
+        for (int k = 0; k * 64 < nv; k++) {
+            const int v = lane + 64 * k < nv ? lane + 64 * k : lane;  // inactive lanes re-read piece `lane`
+            const int g = (4 * v) / HD;
+            float M = -INFINITY, den = 0.0f;
+            f32x4 acc = (f32x4)0.0f;
+            auto fold = [&](const f32x2 ml, const f32x4 ov) {
+                const float Mn = fmaxf(M, ml[0]);
+                const float a = M == -INFINITY ? 0.0f : exp2f(M - Mn);
+                const float b = ml[0] == -INFINITY ? 0.0f : exp2f(ml[0] - Mn);
+                den = den * a + ml[1] * b;
+                acc = acc * a + ov * b;
+                M = Mn;
+            };
+            auto ld_ml = [&](int64_t uu) {
+                return __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)((slot0(uu) + g) * 8), 0, kSc1);
+            };
+            auto ld_o = [&](int64_t uu) {
+                return __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(slot0(uu) * HD * 4) + 16 * v, 0, kSc1);
+            };
+            int64_t uu = first;
+            for (; uu + 3 <= last; uu += 4) {
+                const f32x2 m0 = ld_ml(uu), m1 = ld_ml(uu + 1), m2 = ld_ml(uu + 2), m3 = ld_ml(uu + 3);
+                const f32x4 o0 = ld_o(uu), o1 = ld_o(uu + 1), o2 = ld_o(uu + 2), o3 = ld_o(uu + 3);
+                fold(m0, o0);
+                fold(m1, o1);
+                fold(m2, o2);
+                fold(m3, o3);
+            }
+            for (; uu <= last; uu++) fold(ld_ml(uu), ld_o(uu));
+            if (lane + 64 * k < nv) {
+                const float inv = 1.0f / den;
+                f16x4 h;
+#pragma unroll
+                for (int q = 0; q < 4; q++) h[q] = (f16)(acc[q] * inv);
+                *reinterpret_cast<f16x4 *>(orow + 4 * v) = h;
+            }
+        }
+        if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -739,24 +896,33 @@ bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t bloc
            group >= 1 && group <= 16 && block_size >= 8 && (block_size & (block_size - 1)) == 0;
 }
 
+// Resident workgroups of the stream-K kernel on this device (its grid), queried
+// once per instantiation.
+template <typename KV, int HD, int BLK>
+static hipError_t streamk_grid(int *grid) {
+    static int resident = 0;
+    if (resident == 0) {
+        int dev = 0, cus = 0, per_cu = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e == hipSuccess)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_streamk<KV, HD, BLK>, 64 * kMfmaWaves, 0);
+        if (e != hipSuccess) return e;
+        resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    }
+    *grid = resident;
+    return hipSuccess;
+}
+
 template <typename KV, int HD, int BLK>
 static hipError_t launch_mfma_blk(const AttnParams &p, hipStream_t stream) {
     const dim3 block(64 * kMfmaWaves);
-    if (p.rows <= kPersistentMaxRows) {
-        // resident capacity of the persistent kernel, queried once per instantiation
-        static int resident = 0;
-        if (resident == 0) {
-            int dev = 0, cus = 0, per_cu = 0;
-            hipError_t e = hipGetDevice(&dev);
-            if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-            if (e == hipSuccess)
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_persistent<KV, HD, BLK>, block.x, 0);
-            if (e != hipSuccess) return e;
-            resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
-        }
-        const int64_t upper = (int64_t)p.rows * p.max_parts * p.num_kv_heads;
-        const dim3 grid((unsigned)(upper < resident ? upper : resident));
-        hipLaunchKernelGGL((attn_mfma_persistent<KV, HD, BLK>), grid, block, 0, stream, p);
+    if (p.seg_count != nullptr) {
+        if (p.rows > kPersistentMaxRows) return hipErrorInvalidValue;
+        int grid = 0;
+        const hipError_t e = streamk_grid<KV, HD, BLK>(&grid);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((attn_mfma_streamk<KV, HD, BLK>), dim3(grid), block, 0, stream, p);
         return hipGetLastError();
     }
     const dim3 grid(p.max_parts, p.num_kv_heads, p.rows);
@@ -779,6 +945,38 @@ static hipError_t launch_mfma(const AttnParams &p, hipStream_t stream) {
         case 256: return launch_mfma_hd<KV, 256>(p, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+template <typename KV, int HD>
+static hipError_t streamk_grid_hd(int block_size, int *grid) {
+    if (block_size % 16 == 0) return streamk_grid<KV, HD, kBlkTile>(grid);
+    if (block_size == 8) return streamk_grid<KV, HD, kBlkSmall>(grid);
+    return hipErrorInvalidValue;
+}
+
+template <typename KV>
+static hipError_t streamk_grid_kv(int head_dim, int block_size, int *grid) {
+    switch (head_dim) {
+        case 64: return streamk_grid_hd<KV, 64>(block_size, grid);
+        case 128: return streamk_grid_hd<KV, 128>(block_size, grid);
+        case 256: return streamk_grid_hd<KV, 256>(block_size, grid);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool mfma_streamk_plan(const AttnParams &p, int32_t dtype, int64_t *part_slots, int64_t *counters) {
+    if (p.rows <= 0 || p.rows > kPersistentMaxRows) return false;
+    if (!mfma_supported(dtype, p.head_dim, p.num_heads / p.num_kv_heads, p.block_size)) return false;
+    int grid = 0;
+    const hipError_t e = dtype == kF16 ? streamk_grid_kv<f16>(p.head_dim, p.block_size, &grid)
+                                       : streamk_grid_kv<uint8_t>(p.head_dim, p.block_size, &grid);
+    if (e != hipSuccess) return false;
+    const int64_t Hkv = p.num_kv_heads, G = p.num_heads / p.num_kv_heads;
+    const int64_t NH = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
+    const int64_t units = (int64_t)grid * (kMfmaWaves / NH) / (Hkv / NH);
+    *part_slots = (units + (int64_t)p.rows) * Hkv * G;
+    *counters = (int64_t)p.rows * Hkv;
+    return true;
 }
 
 template <typename KV, typename QT>
@@ -817,7 +1015,7 @@ hipError_t launch_attention(const AttnParams &p, int32_t dtype, bool use_mfma, h
     }
     if (e != hipSuccess) return e;
     if (after_main) (void)hipEventRecord(after_main, stream);
-    if (p.max_parts <= 1) return e;
+    if (p.max_parts <= 1 || (use_mfma && p.seg_count != nullptr)) return e;
     dim3 grid((p.num_heads + 3) / 4, p.rows);
     if (dtype == kF32)
         hipLaunchKernelGGL((attn_reduce_kernel<float>), grid, dim3(256), 0, stream, p);

@@ -33,6 +33,9 @@ struct AttnParams {
     const int4 *row_info;          // ragged mode
     float *part_o;             // [rows][H][max_parts][d] split-context partial outputs
     float *part_ml;            // [rows][H][max_parts][2] (max in log2 units, sum)
+                               // (stream-K: [part_slots][d] and [part_slots][2])
+    int32_t *seg_count;        // stream-K MFMA form: [rows][Hkv] counters, all 0 between launches
+    uint32_t part_bytes;       // stream-K: bytes of part_o + part_ml (< 2^31)
     const void *zero_page;     // >= 1 KiB of zeros: the source of masked lanes' loads
     int32_t rows;
     int32_t bt_stride;
@@ -55,6 +58,11 @@ struct AttnParams {
 hipError_t launch_attention(const AttnParams &p, int32_t dtype, bool use_mfma, hipStream_t stream,
                             hipEvent_t after_main = nullptr);
 bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size);
+// Stream-K form of the MFMA kernel (rows <= 2048): one launch, no reduce kernel.
+// Gives the partial slots (floats per slot: d + 2) and the counters it needs; the
+// counters must be zero before the first launch and every launch leaves them
+// zero.  Launches that share counters must not overlap.  False: not applicable.
+bool mfma_streamk_plan(const AttnParams &p, int32_t dtype, int64_t *part_slots, int64_t *counters);
 
 // KV append into the paged pools.
 struct AppendParams {

@@ -548,6 +548,10 @@ PAM_API int32_t pam_set_decode_kernel(void *context, int32_t choice) {
     });
 }
 
+PAM_API int32_t pam_set_gpu_timing(void *context, bool enabled) {
+    return guarded(context, [&](Context *ctx) { ctx->gpu_timing = enabled; });
+}
+
 PAM_API int32_t pam_engine_mixed_step(void *context, const pam_mixed_request *request) {
     if (!request) return -1;
     return guarded(context, [&](Context *ctx) { ctx->mixed_step(*request); });

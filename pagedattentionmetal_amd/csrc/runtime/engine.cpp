@@ -61,6 +61,7 @@ Context::~Context() {
     (void)hipSetDevice(device_);
     if (own_stream_) (void)hipStreamSynchronize(own_stream_);
     if (workspace_.ptr) (void)hipFree(workspace_.ptr);
+    if (seg_count_.ptr) (void)hipFree(seg_count_.ptr);
     for (auto &s : scratch_)
         if (s.ptr) (void)hipFree(s.ptr);
     if (pinned_) (void)hipHostFree(pinned_);
@@ -200,7 +201,7 @@ void Context::record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t b
     last_stats.temporary_bytes = tmp;
     last_stats.used_split_pass = split ? 1 : 0;
     last_stats.elapsed_ms = last_stats.kernel_ms = last_stats.reduce_ms = -1.0;
-    stats_pending_ = true;
+    stats_pending_ = gpu_timing;
     stats_has_mid_ = has_mid;
     if (synchronous) stats();
 }
@@ -228,18 +229,19 @@ pam_stats Context::stats() {
 // should hold a few thousand waves so all 256 CUs stay busy and ragged rows do
 // not leave a long tail.
 // Split-context partition length (tokens, a multiple of 16).
-//  MFMA kernel: one workgroup per (row, kv head, partition) item, about three
-//  resident per CU, items dealt to the persistent grid in snake order.  Long
-//  partitions (1024 tokens) keep every wave's load pipeline full between the
-//  per-item start-up and merge, and bound the imbalance of ragged rows; they
-//  shrink only when there would be too few items to fill the grid.
+//  MFMA kernel: in its persistent form one wave per (row, kv head, partition)
+//  item, eight or twelve waves resident per CU, items dealt in snake order.
+//  Long partitions (up to 1024 tokens) keep a wave's load pipeline full between
+//  per-item start-ups and keep the split-context partials small; they shrink
+//  until there are about three items per resident wave, which bounds the tail
+//  of ragged rows.
 //  VALU kernel: one wave per (row, head group, partition).
 int32_t Context::choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma) {
     if (max_tiles <= 0) return 16;
     if (part_tokens_override > 0) return std::max<int32_t>(16, part_tokens_override / 16 * 16);
     if (mfma) {
         int64_t tpp = 64;
-        while (tpp > 16 && items_per_part * ceil_div(max_tiles, tpp) < 3 * (int64_t)cus_) tpp /= 2;
+        while (tpp > 8 && items_per_part * ceil_div(max_tiles, tpp) < 3 * 8 * (int64_t)cus_) tpp /= 2;
         if (tpp >= max_tiles) tpp = max_tiles;
         return (int32_t)(tpp * 16);
     }
@@ -248,6 +250,49 @@ int32_t Context::choose_part_tokens(int64_t items_per_part, int64_t max_tiles, b
     while (tpp > 4 && items_per_part * ceil_div(max_tiles, tpp) < 4096) tpp /= 2;
     if (tpp >= max_tiles) tpp = max_tiles;
     return (int32_t)(tpp * 16);
+}
+
+// Split-context set-up of a row launch (p.rows and the shape already filled).
+// The MFMA kernel runs in its stream-K form when the rows fit it: partial slots
+// in the workspace plus the counters, no reduce kernel.  Otherwise rows are cut
+// into fixed partitions merged by the reduce kernel.  Returns the workspace
+// bytes used (0: none).
+int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves) {
+    p.seg_count = nullptr;
+    int64_t slots = 0, counters = 0;
+    // a partition length set through pam_set_partition_tokens selects the
+    // partitioned form
+    if (use_mfma && part_tokens_override == 0 && mfma_streamk_plan(p, dtype, &slots, &counters)) {
+        p.part_tokens = (int32_t)(max_tiles * 16);
+        p.max_parts = 1;
+        const int64_t bytes = slots * ((int64_t)p.head_dim + 2) * 4;
+        if (bytes >= ((int64_t)1 << 31)) throw PamError("stream-K workspace exceeds 2 GiB");
+        reserve_workspace((size_t)bytes);
+        p.part_o = static_cast<float *>(workspace_.ptr);
+        p.part_ml = p.part_o + slots * p.head_dim;
+        p.part_bytes = (uint32_t)bytes;
+        if ((size_t)counters * 4 > seg_count_.bytes) {
+            hip_check(hipStreamSynchronize(stream()), "counter resize");
+            if (seg_count_.ptr) hip_check(hipFree(seg_count_.ptr), "hipFree");
+            seg_count_.ptr = nullptr;
+            seg_count_.bytes = 0;
+            hip_check(hipMalloc(&seg_count_.ptr, (size_t)counters * 4), "hipMalloc counters");
+            hip_check(hipMemsetAsync(seg_count_.ptr, 0, (size_t)counters * 4, stream()), "counter clear");
+            hip_check(hipStreamSynchronize(stream()), "counter clear");
+            seg_count_.bytes = (size_t)counters * 4;
+        }
+        p.seg_count = static_cast<int32_t *>(seg_count_.ptr);
+        return bytes;
+    }
+    p.part_tokens = choose_part_tokens(waves, max_tiles, use_mfma);
+    p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles, p.part_tokens / 16));
+    if (p.max_parts <= 1) return 0;
+    const int64_t slots_p = (int64_t)p.rows * p.num_heads * p.max_parts;
+    const int64_t bytes = slots_p * ((int64_t)p.head_dim + 2) * 4;
+    reserve_workspace((size_t)bytes);
+    p.part_o = static_cast<float *>(workspace_.ptr);
+    p.part_ml = p.part_o + slots_p * p.head_dim;
+    return bytes;
 }
 
 static int32_t heads_per_wave(int32_t group) {
@@ -324,23 +369,14 @@ void Context::decode_gpu(const pam_decode_request &r) {
     int64_t max_tiles = ceil_div(cap_tokens, 16);
     if (l.window_size > 0) max_tiles = std::min<int64_t>(max_tiles, l.window_size / 16 + 2);
     const int64_t waves = (int64_t)r.batch_size * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-    p.part_tokens = choose_part_tokens(waves, max_tiles, use_mfma);
-    p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles, p.part_tokens / 16));
-    int64_t tmp = 0;
-    if (p.max_parts > 1) {
-        const int64_t slots = (int64_t)r.batch_size * l.num_heads * p.max_parts;
-        tmp = slots * ((int64_t)l.head_dim + 2) * 4;
-        reserve_workspace((size_t)tmp);
-        p.part_o = static_cast<float *>(workspace_.ptr);
-        p.part_ml = p.part_o + slots * l.head_dim;
-    }
+    const int64_t tmp = plan_split(p, l.data_type, use_mfma, max_tiles, waves);
     with_retry("decodeFlat", [&] {
-        (void)hipEventRecord(ev0_, stream());
-        check_launch(launch_attention(p, l.data_type, use_mfma, stream(), evmid_), "decode");
-        (void)hipEventRecord(ev1_, stream());
+        mark(ev0_);
+        check_launch(launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "decode");
+        mark(ev1_);
         finish("decode");
     });
-    record_stats(PAM_OP_DECODE, r.batch_size, 0, r.max_num_blocks, tmp, p.max_parts > 1, true);
+    record_stats(PAM_OP_DECODE, r.batch_size, 0, r.max_num_blocks, tmp, p.max_parts > 1 || p.seg_count != nullptr, true);
 }
 
 // ------------------------------------------------------------------ prefill
@@ -414,27 +450,19 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
         p.max_parts = 1;
     } else {
         const int64_t waves = (int64_t)r.seq_len * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-        p.part_tokens = choose_part_tokens(waves, max_tiles, use_mfma);
-        p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles, p.part_tokens / 16));
-        if (p.max_parts > 1) {
-            const int64_t slots = (int64_t)r.seq_len * l.num_heads * p.max_parts;
-            tmp = slots * ((int64_t)l.head_dim + 2) * 4;
-            reserve_workspace((size_t)tmp);
-            p.part_o = static_cast<float *>(workspace_.ptr);
-            p.part_ml = p.part_o + slots * l.head_dim;
-        }
+        tmp = plan_split(p, l.data_type, use_mfma, max_tiles, waves);
     }
     with_retry("prefill", [&] {
-        (void)hipEventRecord(ev0_, stream());
+        mark(ev0_);
         if (dense)
             check_launch(launch_prefill_mfma(p, stream()), "prefill");
         else
-            check_launch(launch_attention(p, l.data_type, use_mfma, stream(), evmid_), "prefill");
-        (void)hipEventRecord(ev1_, stream());
+            check_launch(launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "prefill");
+        mark(ev1_);
         finish("prefill");
     });
     const int32_t op = (dense || use_mfma) ? PAM_OP_PREFILL_MMA : PAM_OP_PREFILL_TILED_PASS;
-    record_stats(op, 1, r.seq_len, (int32_t)ceil_div(kv_len, l.block_size), tmp, p.max_parts > 1, !dense);
+    record_stats(op, 1, r.seq_len, (int32_t)ceil_div(kv_len, l.block_size), tmp, p.max_parts > 1 || p.seg_count != nullptr, !dense);
 }
 
 // ------------------------------------------------------------------ append
@@ -488,9 +516,9 @@ void Context::append_gpu(const pam_append_request &r) {
     p.head_dim = l.head_dim;
     p.block_size = l.block_size;
     with_retry(l.data_type == kFP8 ? "appendToCacheCheckedFP8" : "appendToCacheFlat", [&] {
-        (void)hipEventRecord(ev0_, stream());
+        mark(ev0_);
         check_launch(launch_append(p, l.data_type, stream()), "append");
-        (void)hipEventRecord(ev1_, stream());
+        mark(ev1_);
         finish("append");
     });
     record_stats(PAM_OP_APPEND, 1, r.num_new_tokens, 0, 0, false, false);
@@ -615,28 +643,19 @@ void Context::mixed_step(const pam_mixed_request &r) {
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
     p.zero_page = zero_page_;
     const int64_t waves = (int64_t)ragged_rows * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-    p.part_tokens = choose_part_tokens(waves, max_tiles + 1, use_mfma);
-    p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles + 1, p.part_tokens / 16));
-    int64_t tmp = 0;
-    if (ragged_rows > 0 && p.max_parts > 1) {
-        const int64_t slots = (int64_t)ragged_rows * l.num_heads * p.max_parts;
-        tmp = slots * ((int64_t)l.head_dim + 2) * 4;
-        reserve_workspace((size_t)tmp);
-        p.part_o = static_cast<float *>(workspace_.ptr);
-        p.part_ml = p.part_o + slots * l.head_dim;
-    }
+    const int64_t tmp = ragged_rows > 0 ? plan_split(p, l.data_type, use_mfma, max_tiles + 1, waves) : 0;
     with_retry("mixedStep", [&] {
-        (void)hipEventRecord(ev0_, stream());
+        mark(ev0_);
         if (ab.keys) check_launch(launch_append_batch(ab, l.data_type, stream()), "mixed append");
         if (!chunks.empty()) check_launch(launch_prefill_mfma(p, stream()), "mixed prefill");
         if (ragged_rows > 0)
-            check_launch(launch_attention(p, l.data_type, use_mfma, stream(), evmid_), "mixed attention");
+            check_launch(launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "mixed attention");
         else
-            (void)hipEventRecord(evmid_, stream());
-        (void)hipEventRecord(ev1_, stream());
+            mark(evmid_);
+        mark(ev1_);
         finish("mixed step");
     });
-    record_stats(PAM_OP_DECODE, r.num_seqs, total, r.bt_stride, tmp, p.max_parts > 1, true);
+    record_stats(PAM_OP_DECODE, r.num_seqs, total, r.bt_stride, tmp, p.max_parts > 1 || p.seg_count != nullptr, true);
 }
 
 // ------------------------------------------------------------------ codec

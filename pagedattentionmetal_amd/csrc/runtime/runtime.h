@@ -98,6 +98,12 @@ class Context {
     int32_t fail_next_launches = 0;
     int32_t part_tokens_override = 0;
     int32_t decode_kernel_choice = 0;
+    // HIP events around each call's kernels (the timings of last_stats); off
+    // saves their queue packets between back-to-back launches
+    bool gpu_timing = true;
+    void mark(hipEvent_t e) {
+        if (gpu_timing) (void)hipEventRecord(e, stream());
+    }
 
     // --- scratch
     void reserve_workspace(size_t bytes);
@@ -116,6 +122,7 @@ class Context {
     void prefill_gpu(const pam_prefill_request &r);
     void append_gpu(const pam_append_request &r);
     int32_t choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma);
+    int64_t plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves);
     void record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t blocks, int64_t tmp, bool split,
                       bool has_mid);
 
@@ -129,6 +136,7 @@ class Context {
     bool stats_pending_ = false;
     bool stats_has_mid_ = false;
     DeviceBuffer workspace_;
+    DeviceBuffer seg_count_;  // stream-K counters: zero between launches
     DeviceBuffer scratch_[6];
     void *pinned_ = nullptr;
     size_t pinned_bytes_ = 0;

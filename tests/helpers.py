@@ -11,8 +11,12 @@ TOL = {0: 1e-5, 1: 2e-3, 2: 2e-3}
 def row_rel_err(out, ref):
     out = np.asarray(out, np.float64).reshape(-1, ref.shape[-1])
     ref = np.asarray(ref, np.float64).reshape(-1, ref.shape[-1])
-    num = np.abs(out - ref).max(axis=1)
-    den = np.maximum(np.abs(ref).max(axis=1), 1e-6)
+    # a row without keys is 0/0 = NaN in the reference; NaN must meet NaN
+    both = np.isnan(out) & np.isnan(ref)
+    diff = np.where(both, 0.0, np.abs(out - ref))
+    diff = np.where(np.isnan(diff), np.inf, diff)
+    num = diff.max(axis=1)
+    den = np.maximum(np.nan_to_num(np.abs(ref), nan=0.0).max(axis=1), 1e-6)
     return float((num / den).max())
 
 

@@ -135,6 +135,15 @@ DECODE_CASES = [
     (3, 32, 8, 128, 16, 2, [3, 200, 1500], 0, 0, 0),              # fp8 MFMA
     (3, 32, 8, 128, 16, 2, [3, 200, 1500], 0, 1, 0),              # fp8 VALU
     (2, 24, 8, 128, 16, 1, [77, 1025], 0, 0, 0),                  # group 3 -> VALU
+    # stream-K MFMA form: head groups of 2 (Hkv 6, 2), one long row merged from
+    # ~150 units, rows without keys among others; forced partitions take the
+    # workgroup form with the reduce kernel instead
+    (3, 24, 6, 128, 16, 1, [50, 900, 2000], 0, 0, 0),
+    (2, 8, 2, 128, 16, 1, [3000, 64], 0, 0, 0),
+    (1, 32, 8, 128, 16, 1, [20000], 0, 0, 0),
+    (4, 32, 8, 128, 16, 1, [0, 20, 0, 300], 0, 0, 0),
+    (3, 32, 8, 128, 16, 2, [3, 200, 1500], 0, 0, 128),
+    (2, 32, 8, 64, 8, 2, [900, 40], 0, 0, 0),                      # fp8, bs 8
 ]
 
 
@@ -190,6 +199,53 @@ def test_decode_parity(engine, case):
     finally:
         engine.set_decode_kernel(0)
         engine.set_partition_tokens(0)
+
+
+def test_decode_streamk_repeatable(engine):
+    """The stream-K form keeps per-(row, kv head) counters between launches: shapes
+    that split rows differently must each stay correct, and a repeated launch gives
+    the same bits (partials merge in a fixed order)."""
+    import torch
+    rng = np.random.default_rng(91)
+    shapes = [(6, 32, 8, 128, 16, [4000, 17, 2500, 1, 900, 3333]),
+              (2, 8, 2, 128, 16, [7000, 5]),
+              (3, 64, 8, 128, 16, [12000, 300, 8000])]
+    runs = []
+    for B, H, hkv, d, bs, lens in shapes:
+        q, k, v, bt, lens = make_case(rng, B, H, hkv, d, bs, 1, lens)
+        args = (to_dev(q), to_dev(k), to_dev(v), to_dev(bt), to_dev(lens))
+        ref = oracle.decode(1, q, k, v, bt, lens, H, n_threads=8)
+        runs.append((args, B, bt.shape[1], layer(H, hkv, d, bs, 1), ref))
+    first = []
+    for rep in range(2):
+        for i, (args, B, nb, lay, ref) in enumerate(runs):
+            out = torch.zeros((B, lay.num_heads, lay.head_dim), dtype=torch.float16, device="cuda")
+            engine.decode(*args, out, B, nb, lay)
+            got = to_host(out)
+            err = row_rel_err(got, ref)
+            assert err <= TOL[1], f"shape {i} pass {rep}: rel err {err:.3e}"
+            if rep == 0:
+                first.append(got)
+            else:
+                assert np.array_equal(got.view(np.uint16), first[i].view(np.uint16)), f"shape {i} not repeatable"
+
+
+def test_decode_mfma_many_rows_workgroup_form(engine):
+    """More rows than the stream-K form indexes: the workgroup form plus reduce."""
+    import torch
+    rng = np.random.default_rng(92)
+    B = 2100
+    lens = rng.integers(0, 400, B)
+    q, k, v, bt, lens = make_case(rng, B, 32, 8, 64, 16, 1, lens)
+    out = torch.zeros((B, 32, 64), dtype=torch.float16, device="cuda")
+    engine.decode(to_dev(q), to_dev(k), to_dev(v), to_dev(bt), to_dev(lens), out, B, bt.shape[1],
+                  layer(32, 8, 64, 16, 1))
+    ref = oracle.decode(1, q, k, v, bt, lens, 32, n_threads=8)
+    got = to_host(out)
+    empty = lens == 0
+    assert np.isnan(got[empty].astype(np.float64)).all()
+    err = row_rel_err(got[~empty], ref[~empty])
+    assert err <= TOL[1], f"rel err {err:.3e}"
 
 
 def test_decode_empty_sequence_is_nan(engine):
