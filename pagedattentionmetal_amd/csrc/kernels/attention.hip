@@ -389,7 +389,12 @@ __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, 
     load_tile(pr.t_begin + 1, tb);
     if constexpr (S::DEPTH == 3) load_tile(pr.t_begin + 2, tc);
     for (int chunk = pr.t_begin; chunk < pr.t_end; chunk += CH) {
-        if (chunk != pr.t_begin) refresh_window(chunk);
+        // the window holds 64 blocks: refresh it only when this chunk's loads
+        // (tiles up to chunk + CH - 1 + DEPTH) would leave it
+        if (chunk != pr.t_begin) {
+            const int far = chunk + CH - 1 + S::DEPTH < pr.t_end - 1 ? chunk + CH - 1 + S::DEPTH : pr.t_end - 1;
+            if (((far * 16 + 15) >> bsh) - window_blk >= 64) refresh_window(chunk);
+        }
 #pragma unroll
         for (int k = 0; k < CH; k += S::DEPTH) {
             const int tile = chunk + k;
