@@ -9,22 +9,24 @@
 // the flops per cycle of the 16x16 shapes.  A workgroup (8 waves, two per SIMD)
 // owns 256 query rows of one kv head: the (token, head) pairs of 256 / G
 // consecutive tokens, so the G query heads sharing a kv head share every K/V
-// tile.  Each wave owns RB blocks of 32 rows; every K or V operand it reads from
-// LDS feeds RB MFMAs (RB = 2 halves the LDS traffic but needs AGPR
-// accumulators and one wave per SIMD, which measured slower).  Per 32-key tile:
-//   * all 256 threads stage K and V rows into a 3-deep LDS ring (the next tiles
-//     are fetched into registers two iterations ahead);
-//   * S^T = K Q^T (32 keys x 32 rows per block, 8 MFMAs over d): K from LDS is
-//     the A operand, Q^T stays in registers as B.  The accumulator leaves lane
-//     (n, h) holding keys 8q + 4h + r (q, r < 4) of row n, and the 8 of them with
-//     q in {2c, 2c+1} are exactly the B operand of O^T += V^T P^T over key chunk
-//     c (16 keys), so P never leaves registers; V^T is read from LDS with the
-//     transposing ds_read_b64_tr_b16;
-//   * the scores of tile t+1 are formed while the probabilities of tile t are
-//     exponentiated, and O += V(t) P(t) runs while tile t+1 is masked and reduced;
-//   * softmax keeps a per-row reference max that is only raised (and O rescaled)
-//     when some score exceeds it by more than 2^8, so P is bounded by 2^8 and
-//     goes to the MFMA in f16; the common case needs no cross-lane reduction.
+// tile.  Each wave owns RB blocks of 32 rows (RB = 2 would halve the LDS
+// traffic but needs AGPR accumulators and one wave per SIMD, measured slower).
+// Per 32-key tile t a wave runs two phases separated by workgroup barriers:
+//   * matrix phase M_t: S^T(t+1) = K Q^T (32 keys x 32 rows, 8 MFMAs over d; K
+//     from LDS is the A operand, Q^T stays in registers as B) and
+//     O^T += V^T(t) P^T(t) (8 MFMAs; V^T read with the transposing
+//     ds_read_b64_tr_b16), then the global loads of tile t + 4;
+//   * vector phase V_t: mask and reference max of S(t), exponentials to P(t) in
+//     f16, row sums, the K operands of M_t and the LDS staging of tile t + 2.
+//   The S^T accumulator leaves lane (n, h) holding keys 8q + 4h + r (q, r < 4) of
+//   row n, and the 8 of them with q in {2c, 2c+1} are exactly the B operand of
+//   O^T += V^T P^T over key chunk c (16 keys), so P never leaves registers.
+//   Waves 4-7 run one phase behind waves 0-3; waves w and w + 4 share a SIMD,
+//   so its MFMA pipe works on one wave's matrix phase while the other wave's
+//   vector phase runs.
+// Softmax keeps a per-row reference max that is only raised (and O rescaled)
+// when some score exceeds it by more than 2^8, so P is bounded by 2^8 and goes
+// to the MFMA in f16; the common case needs no cross-lane reduction.
 #include "kernels.h"
 #include "pam_device.h"
 
@@ -36,7 +38,7 @@ constexpr int kPrefillWaves = 8;                               // one workgroup 
 constexpr int kPrefillRB = 1;                                  // 32-row blocks per wave
 constexpr int kPrefillRows = 32 * kPrefillRB * kPrefillWaves;  // query rows per workgroup
 constexpr int kPrefillKT = 32;                                 // keys per tile
-constexpr int kPrefillBufs = 3;                // LDS ring: t computed, t+1 scored, t+2 written
+constexpr int kPrefillBufs = 4;                // LDS ring of K/V tiles
 constexpr float kRescaleLog2 = 8.0f;           // lazy-rescale threshold (log2 units)
 constexpr int kBtCache = 2048;                 // block-table entries a workgroup keeps in LDS
 constexpr int kXcds = 8;                       // accelerator dies (each with its own L2)
@@ -140,7 +142,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
     // before they are written to LDS
     f16x8 kra[KPT], vra[KPT], krb[KPT], vrb[KPT];
     int blk0 = 0;  // first block of the block-table segment held in bt_lds
-    auto fetch = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+    // pool row of this thread's key(s) of a tile, then the loads from it
+    auto lookup = [&](int tile, uint32_t(&slot)[KPT]) {
 #pragma unroll
         for (int i = 0; i < KPT; i++) {
             int j = tile * KT + my_key + i * KEYS_PER_PASS;
@@ -148,11 +151,21 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             // data whose probability is zero after masking (and a block-table entry
             // of the current segment)
             j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
-            const uint32_t slot = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
-            const uint64_t off = (uint64_t)slot * row_stride;
+            slot[i] = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
+        }
+    };
+    auto load = [&](const uint32_t(&slot)[KPT], f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+#pragma unroll
+        for (int i = 0; i < KPT; i++) {
+            const uint64_t off = (uint64_t)slot[i] * row_stride;
             kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off);
             vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off);
         }
+    };
+    auto fetch = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+        uint32_t slot[KPT];
+        lookup(tile, slot);
+        load(slot, kreg, vreg);
     };
     int k_st[KPT], v_st[KPT];
 #pragma unroll
@@ -252,7 +265,21 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
         }
     };
 
-    f32x16 sacc[RB][KH], snext[RB][KH];
+    // Ping-pong schedule.  A tile's work splits into a matrix phase M_t (scores
+    // S(t+1) = K(t+1) Q^T and O += V(t) P(t), with the loads of tile t + 4) and a
+    // vector phase V_t (mask, reference max and exponentials of S(t), row sums,
+    // and the LDS staging of tile t + 2).  Each wave runs
+    // M_-1 V_0 M_0 V_1 M_1 ... with a workgroup barrier after every phase; waves
+    // 4-7 start one barrier late, so each SIMD (waves w and w + 4) has one wave in
+    // a matrix phase while the other is in a vector phase, and the MFMA and VALU
+    // pipes overlap.  LDS ring of 4 tiles: tile t + 2 is written (half by each
+    // wave group) at V_t, K(t) is read at M_t-1 and V(t) at M_t, so a buffer is
+    // rewritten only after both groups have left the phases that read it.
+    constexpr int NBUF = kPrefillBufs;
+    static_assert(NBUF == 4, "the ring schedule above needs 4 tiles");
+    const bool lag = wave >= kPrefillWaves / 2;
+    f32x16 sacc[RB][KH];
+    f16x8 pb[RB][2 * KH];
     // tiles run in segments whose block-table entries fit in bt_lds (one segment
     // covers kBtCache * block_size keys, so long contexts only)
     // (an even number of tiles: the loop below runs tiles in pairs, and a segment
@@ -260,7 +287,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
     const int seg_tiles = (((kBtCache - 1) << bsh) / KT) & ~1;
     for (int seg = t_lo; seg < t_hi; seg += seg_tiles) {
         const int seg_end = min(t_hi, seg + seg_tiles);
-        const int seg_pad = seg + ((seg_end - seg + 1) & ~1);
+        const int T = (seg_end - seg + 1) & ~1;
         blk0 = (seg * KT) >> bsh;
         const int nblk = (((min(seg_end * KT, kv_len) - 1) >> bsh) - blk0) + 1;
         __syncthreads();  // previous segment done with bt_lds and the ring
@@ -273,16 +300,27 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
         fetch(min(seg + 2, seg_end - 1), kra, vra);
         fetch(min(seg + 3, seg_end - 1), krb, vrb);
         __syncthreads();
-        score(0, sacc);
-        if (__any(prepare(seg, sacc))) rescale();
-        int buf = 0;
-        // iteration t: S(t+1) on MFMA while P(t) is exponentiated, then
-        // O += V(t) P(t) on MFMA while S(t+1) is masked and reduced
-        auto step = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
-            const int b1 = buf == kPrefillBufs - 1 ? 0 : buf + 1;
-            const int b2 = b1 == kPrefillBufs - 1 ? 0 : b1 + 1;
-            score(b1, snext);
-            f16x8 pb[RB][2 * KH];
+        if (lag) __syncthreads();
+        score(0, sacc);  // M_-1
+        __syncthreads();
+
+        // The vector phase requests the K operands of the next matrix phase (its
+        // tile is staged by then) and looks up the rows the matrix phase will
+        // load; the matrix phase requests its V operands first and runs the score
+        // MFMAs while they arrive.
+        f16x8 ka[KH][DC];
+        uint32_t nslot[KPT];
+        auto vphase = [&](int t, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+            if (t + 1 < T) {
+                const f16 *kt = k_lds[(t + 1) % NBUF];
+#pragma unroll
+                for (int e = 0; e < KH; e++)
+#pragma unroll
+                    for (int c = 0; c < DC; c++)
+                        ka[e][c] = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * kPrefillKL + 16 * c]);
+            }
+            lookup(min(seg + t + 4, seg_end - 1), nslot);
+            if (__any(prepare(seg + t, sacc))) rescale();
 #pragma unroll
             for (int b = 0; b < RB; b++) {
                 const float mref = m_use[b] == -INFINITY ? 0.0f : m_use[b];
@@ -301,35 +339,69 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
                 }
                 l_run[b] = ps;
             }
-            // O^T += V^T P^T, each V^T operand shared by the row blocks
-            const f16 *vt = v_lds[buf];
+            // P and the row sums are complete here: without this the compiler
+            // sinks the exponentials past the barrier into the matrix phase
+#pragma unroll
+            for (int b = 0; b < RB; b++) {
+#pragma unroll
+                for (int c = 0; c < 2 * KH; c++) asm volatile("" : "+v"(pb[b][c]));
+                asm volatile("" : "+v"(l_run[b]));
+            }
+            stage((t + 2) % NBUF, kreg, vreg);  // tile t + 2, fetched at M_t-2
+        };
+        auto mphase = [&](int t, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+            const f16 *vt = v_lds[t % NBUF];
+            f16x8 va[2 * KH][DT];
 #pragma unroll
             for (int c = 0; c < 2 * KH; c++)
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) {
                     const f16x4 lo = lds_read_tr16(vt + v_rd[dt] + 16 * c * kPrefillVL);
                     const f16x4 hi = lds_read_tr16(vt + v_rd[dt] + (16 * c + 8) * kPrefillVL);
-                    const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    va[c][dt] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+            if (t + 1 < T) {
+#pragma unroll
+                for (int e = 0; e < KH; e++) {
+#pragma unroll
+                    for (int b = 0; b < RB; b++) sacc[b][e] = (f32x16)0.0f;
+#pragma unroll
+                    for (int c = 0; c < DC; c++)
+#pragma unroll
+                        for (int b = 0; b < RB; b++)
+                            sacc[b][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[e][c], qv[b][c], sacc[b][e], 0, 0, 0);
+                }
+            }
+            // O^T += V^T P^T, each V^T operand shared by the row blocks
+#pragma unroll
+            for (int c = 0; c < 2 * KH; c++)
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                     for (int b = 0; b < RB; b++)
-                        o[b][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[b][c], o[b][dt], 0, 0, 0);
-                }
-            // the last tile's successor is not scored: never let it move the reference
-            const bool need = prepare(tile + 1, snext) && tile + 1 < seg_pad;
-            stage(b2, kreg, vreg);
-            fetch(min(tile + 4, seg_end - 1), kreg, vreg);
-            __syncthreads();
-            if (__any(need)) rescale();
+                        o[b][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[c][dt], pb[b][c], o[b][dt], 0, 0, 0);
+            // the matrix work stays in this phase (the compiler would otherwise move
+            // the last MFMAs past the barrier)
 #pragma unroll
-            for (int b = 0; b < RB; b++)
+            for (int b = 0; b < RB; b++) {
 #pragma unroll
-                for (int e = 0; e < KH; e++) sacc[b][e] = snext[b][e];
-            buf = b1;
+                for (int dt = 0; dt < DT; dt++) asm volatile("" : "+v"(o[b][dt]));
+#pragma unroll
+                for (int e = 0; e < KH; e++) asm volatile("" : "+v"(sacc[b][e]));
+            }
+            load(nslot, kreg, vreg);  // tile t + 4
         };
-        for (int tile = seg; tile < seg_pad; tile += 2) {
-            step(tile, kra, vra);
-            step(tile + 1, krb, vrb);
+        for (int t = 0; t < T; t += 2) {
+            vphase(t, kra, vra);
+            __syncthreads();
+            mphase(t, kra, vra);
+            __syncthreads();
+            vphase(t + 1, krb, vrb);
+            __syncthreads();
+            mphase(t + 1, krb, vrb);
+            __syncthreads();
         }
+        if (!lag) __syncthreads();
     }
 
     // finish: l summed over the two lane halves, O / l, rows in range only
