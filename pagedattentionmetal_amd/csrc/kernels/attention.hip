@@ -115,6 +115,9 @@ __device__ __forceinline__ f16x8 e4m3x8_to_f16x8(uint32_t w0, uint32_t w1) {
 constexpr int kMfmaWaves = 4;
 // Rows the stream-K form can index from LDS (its row prefix table).
 constexpr int kPersistentMaxRows = 2048;
+// Decode rows whose key ranges the stream-K form keeps in LDS (8 KiB: three
+// workgroups of the e4m3 kernel still fit a CU).
+constexpr int kStreamKRangeCache = 1024;
 // Fewest tiles per stream-K unit: shorter units would only add partials.
 constexpr int kStreamKMinTiles = 8;
 
@@ -531,39 +534,55 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
     constexpr int NO = S::NO, WT = S::WT;
     __shared__ __attribute__((aligned(16))) f16 tiles[kMfmaWaves * WT];
     __shared__ int32_t prefix[kPersistentMaxRows + 1];
-    __shared__ int32_t chunk_sum[64 * kMfmaWaves];
+    __shared__ int2 key_range[kStreamKRangeCache];  // decode rows: {k_lo, k_hi}
+    __shared__ int32_t wave_sum[kMfmaWaves];
     constexpr int NT = 64 * kMfmaWaves;
     const int tid = threadIdx.x;
     const int rows = p.rows;
-    // tiles per row (0 for a row without keys), prefix-summed in LDS
+    const bool cached = p.mode == kRowDecode && rows <= kStreamKRangeCache;
+    // tiles per row (0 for a row without keys), prefix-summed in LDS: each
+    // thread counts a contiguous run of rows, a wave scan plus the totals of
+    // the waves before it place the runs
     const int per = (rows + NT - 1) / NT;
     const int r0 = tid * per, r1 = r0 + per < rows ? r0 + per : rows;
     int32_t run = 0;
     for (int rr = r0; rr < r1; rr++) {
-        const PartRange whole = part_range(row_ctx(p, rr), 0, 1 << 30);
+        const RowCtx c = row_ctx(p, rr);
+        const PartRange whole = part_range(c, 0, 1 << 30);
+        if (cached) key_range[rr] = make_int2(c.k_lo, c.k_hi);
         prefix[rr] = run;
         run += whole.nparts > 0 ? whole.t_end - whole.t_begin : 0;
     }
-    chunk_sum[tid] = run;
-    __syncthreads();
-    // inclusive scan of the per-thread sums (Hillis-Steele)
-    for (int off = 1; off < NT; off <<= 1) {
-        const int32_t v = tid >= off ? chunk_sum[tid - off] : 0;
-        __syncthreads();
-        chunk_sum[tid] += v;
-        __syncthreads();
+    int32_t incl = run;  // inclusive scan over the wave's lanes
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int32_t v = __shfl_up(incl, off, 64);
+        if ((tid & 63) >= off) incl += v;
     }
-    const int32_t base = tid > 0 ? chunk_sum[tid - 1] : 0;
-    for (int rr = r0; rr < r1; rr++) prefix[rr] += base;
-    if (tid == NT - 1) prefix[rows] = chunk_sum[NT - 1];
+    if ((tid & 63) == 63) wave_sum[tid >> 6] = incl;
     __syncthreads();
+    int32_t base = incl - run;
+    for (int w = 0; w < (tid >> 6); w++) base += wave_sum[w];
+    for (int rr = r0; rr < r1; rr++) prefix[rr] += base;
+    if (tid == NT - 1) prefix[rows] = base + run;
+    __syncthreads();
+    // row context from the LDS copy where there is one (no global load)
+    auto ctx_of = [&](int r) -> RowCtx {
+        if (!cached) return row_ctx(p, r);
+        RowCtx c;
+        c.bt = p.block_tables + (int64_t)r * p.bt_stride;
+        c.k_lo = key_range[r].x;
+        c.k_hi = key_range[r].y;
+        c.out_row = r;
+        return c;
+    };
 
     const int H = p.num_heads, Hkv = p.num_kv_heads, G = H / Hkv;
     f16 *out = static_cast<f16 *>(p.out);
     // rows without keys: 0/0 as in the reference's m/l bookkeeping
     for (int rr = blockIdx.x; rr < rows; rr += gridDim.x)
         if (prefix[rr + 1] == prefix[rr]) {
-            const int orow = row_ctx(p, rr).out_row;
+            const int orow = ctx_of(rr).out_row;
             for (int idx = tid; idx < H * HD; idx += NT) out[(int64_t)orow * H * HD + idx] = (f16)__builtin_nanf("");
         }
 
@@ -598,7 +617,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
         const int64_t P = __builtin_amdgcn_readfirstlane(prefix[lo]);
         const int nt = __builtin_amdgcn_readfirstlane(prefix[lo + 1]) - (int)P;  // > 0: x lies inside this row
         const int64_t e = x1 < P + nt ? x1 : P + nt;
-        const RowCtx c = row_ctx(p, lo);
+        const RowCtx c = ctx_of(lo);
         const int tile0 = c.k_lo / 16;
         PartRange pr;
         pr.t_begin = tile0 + (int)(x - P);

@@ -153,3 +153,30 @@ def test_graceful_degradation_and_retries(torch):
     eng.decode(*args, out, 2, 3, layer)
     err = row_rel_err(to_host(out), ref)
     assert err <= TOL[1], f"rel err after retries {err:.3e}"
+
+
+def test_gpu_timing_switch(torch):
+    """pam_set_gpu_timing(false): no events, times read -1; the result is unchanged."""
+    from pagedattentionmetal_amd import PagedAttentionEngine, PagedLayerSpec
+    eng = PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    rng = np.random.default_rng(5)
+    H, hkv, d, bs = 32, 8, 128, 16
+    lens = np.array([300, 41], np.uint32)
+    k = rng.standard_normal((48, bs, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((48, bs, hkv, d)).astype(np.float16)
+    q = rng.standard_normal((2, H, d)).astype(np.float16)
+    bt = rng.permutation(48)[:38].astype(np.int32).reshape(2, 19)
+    args = (to_dev(q), to_dev(k), to_dev(v), to_dev(bt), to_dev(lens))
+    layer = PagedLayerSpec(d, H, hkv, bs, 1)
+    ref = oracle.decode(1, q, k, v, bt, lens, H)
+    for timing in (False, True):
+        eng.set_gpu_timing(timing)
+        out = torch.zeros((2, H, d), dtype=torch.float16, device="cuda")
+        eng.decode(*args, out, 2, 19, layer)
+        assert row_rel_err(to_host(out), ref) <= TOL[1]
+        st = eng.last_stats
+        if timing:
+            assert st["kernel_ms"] > 0 and st["elapsed_ms"] > 0
+        else:
+            assert st["kernel_ms"] == -1 and st["elapsed_ms"] == -1
