@@ -169,12 +169,35 @@ typedef struct pam_append_request {
     size_t keys_bytes, values_bytes, k_pool_bytes, v_pool_bytes, block_table_bytes;
 } pam_append_request;
 
+/* PagedAttentionFusedPrefillRequest (PagedAttentionTypes.swift:366-421): the new
+ * tokens' raw K/V [seq_len][num_kv_heads][head_dim] are appended at positions
+ * 0 .. seq_len-1 of the sequence's block table (FP8: quantised with the per-block
+ * scale rule of the append), then rows 0 .. seq_len-1 attend over the pool. */
+typedef struct pam_fused_prefill_request {
+    const void *q; /* [seq_len][num_heads][head_dim] */
+    const void *raw_k;
+    const void *raw_v;
+    const int32_t *block_table;
+    void *k_pool;
+    void *v_pool;
+    void *output;
+    int32_t seq_len;
+    pam_layer_spec layer;
+    bool causal;
+    uint16_t *k_scale;
+    uint16_t *v_scale;
+    size_t q_bytes, raw_k_bytes, raw_v_bytes, k_pool_bytes, v_pool_bytes, block_table_bytes, output_bytes;
+} pam_fused_prefill_request;
+
 /* PagedAttentionEngine.decode(_:) (PagedAttentionEngine.swift:533-546) */
 int32_t pam_engine_decode(void *context, const pam_decode_request *request);
 /* PagedAttentionEngine.prefill(_:) (PagedAttentionEngine.swift:405-418) */
 int32_t pam_engine_prefill(void *context, const pam_prefill_request *request);
 /* PagedAttentionEngine.appendToCache(_:) (PagedAttentionEngine.swift:585-597) */
 int32_t pam_engine_append(void *context, const pam_append_request *request);
+/* PagedAttentionEngine.fusedPrefill(_:) (PagedAttentionEngine.swift:633-710): append
+ * and prefill as one call, both launches on the context's stream */
+int32_t pam_engine_fused_prefill(void *context, const pam_fused_prefill_request *request);
 /* PagedAttentionEngine.lastStats (PagedAttentionEngine.swift:136-141) */
 int32_t pam_engine_last_stats(void *context, pam_stats *out);
 /* PagedAttentionEngine.enableGracefulDegradation / maxRetries (Engine.swift:126-129) */

@@ -43,6 +43,13 @@ class PrefillRequest(C.Structure):
                 ("output_bytes", SZ)]
 
 
+class FusedPrefillRequest(C.Structure):
+    _fields_ = [("q", P), ("raw_k", P), ("raw_v", P), ("block_table", P), ("k_pool", P), ("v_pool", P),
+                ("output", P), ("seq_len", I32), ("layer", LayerSpec), ("causal", C.c_bool), ("k_scale", P),
+                ("v_scale", P), ("q_bytes", SZ), ("raw_k_bytes", SZ), ("raw_v_bytes", SZ), ("k_pool_bytes", SZ),
+                ("v_pool_bytes", SZ), ("block_table_bytes", SZ), ("output_bytes", SZ)]
+
+
 class AppendRequest(C.Structure):
     _fields_ = [("keys", P), ("values", P), ("k_pool", P), ("v_pool", P), ("block_table", P), ("token_offset", I32),
                 ("num_new_tokens", I32), ("layer", LayerSpec), ("k_scale", P), ("v_scale", P), ("slot_mapping", P),
@@ -83,6 +90,7 @@ SIGNATURES = {
     "pam_engine_decode": (I32, [P, C.POINTER(DecodeRequest)]),
     "pam_engine_prefill": (I32, [P, C.POINTER(PrefillRequest)]),
     "pam_engine_append": (I32, [P, C.POINTER(AppendRequest)]),
+    "pam_engine_fused_prefill": (I32, [P, C.POINTER(FusedPrefillRequest)]),
     "pam_engine_last_stats": (I32, [P, C.POINTER(Stats)]),
     "pam_engine_set_graceful_degradation": (I32, [P, C.c_bool]),
     "pam_engine_set_max_retries": (I32, [P, I32]),

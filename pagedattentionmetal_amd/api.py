@@ -217,6 +217,16 @@ class PagedAttentionEngine:
             _nbytes(values), _nbytes(k_pool), _nbytes(v_pool), _nbytes(block_table))
         self._check(lib().pam_engine_append(self._ctx, C.byref(r)))
 
+    # --- PagedAttentionEngine.fusedPrefill (PagedAttentionEngine.swift:633-710)
+    def fused_prefill(self, q, raw_k, raw_v, block_table, k_pool, v_pool, output, seq_len, layer: PagedLayerSpec,
+                      causal=True, k_scale=None, v_scale=None):
+        """Append raw K/V rows 0 .. seq_len-1 into the pool and prefill over them, in one call."""
+        r = _lib.FusedPrefillRequest(
+            _ptr(q), _ptr(raw_k), _ptr(raw_v), _ptr(block_table), _ptr(k_pool), _ptr(v_pool), _ptr(output),
+            int(seq_len), layer.c(), bool(causal), _ptr(k_scale), _ptr(v_scale), _nbytes(q), _nbytes(raw_k),
+            _nbytes(raw_v), _nbytes(k_pool), _nbytes(v_pool), _nbytes(block_table), _nbytes(output))
+        self._check(lib().pam_engine_fused_prefill(self._ctx, C.byref(r)))
+
     # --- mixed continuous-batching step (no reference counterpart)
     def mixed_step(self, q, output, k_pool, v_pool, block_tables, context_lens, query_lens, layer: PagedLayerSpec,
                    new_keys=None, new_values=None, k_scale=None, v_scale=None):

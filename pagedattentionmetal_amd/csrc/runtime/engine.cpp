@@ -411,10 +411,11 @@ void Context::prefill(const pam_prefill_request &r) {
     }
 }
 
-void Context::prefill_gpu(const pam_prefill_request &r) {
+Context::PrefillPlan Context::plan_prefill(const pam_prefill_request &r) {
     const pam_layer_spec &l = r.layer;
     const int32_t G = l.num_heads / l.num_kv_heads;
-    AttnParams p{};
+    PrefillPlan pl{};
+    AttnParams &p = pl.p;
     p.q = r.q;
     p.out = r.output;
     p.k_pool = r.k_pool;
@@ -434,14 +435,13 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
     p.zero_page = zero_page_;
 
-    const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G, l.block_size) && decode_kernel_choice != 1;
-    bool use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size) && decode_kernel_choice != 1;
+    pl.dense = prefill_mfma_supported(l.data_type, l.head_dim, G, l.block_size) && decode_kernel_choice != 1;
+    pl.use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size) && decode_kernel_choice != 1;
     const int32_t nh = heads_per_wave(G);
     p.heads_per_wave = nh;
-    const int64_t kv_len = (int64_t)r.q_offset + r.seq_len;
-    const int64_t max_tiles = ceil_div(kv_len, 16) + 1;
-    int64_t tmp = 0;
-    if (dense) {
+    pl.kv_len = (int64_t)r.q_offset + r.seq_len;
+    const int64_t max_tiles = ceil_div(pl.kv_len, 16) + 1;
+    if (pl.dense) {
         const int4 ch = make_int4(0, r.q_offset, r.seq_len, 0);
         p.chunks = static_cast<const int4 *>(stage(4, &ch, sizeof(ch)));
         p.num_chunks = 1;
@@ -449,20 +449,97 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
         p.bt_stride = 0;
         p.max_parts = 1;
     } else {
-        const int64_t waves = (int64_t)r.seq_len * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-        tmp = plan_split(p, l.data_type, use_mfma, max_tiles, waves);
+        const int64_t waves = (int64_t)r.seq_len * (pl.use_mfma ? l.num_kv_heads : l.num_heads / nh);
+        pl.tmp = plan_split(p, l.data_type, pl.use_mfma, max_tiles, waves);
     }
+    return pl;
+}
+
+void Context::launch_prefill_plan(const PrefillPlan &pl, int32_t dtype) {
+    if (pl.dense)
+        check_launch(launch_prefill_mfma(pl.p, stream()), "prefill");
+    else
+        check_launch(launch_attention(pl.p, dtype, pl.use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "prefill");
+}
+
+void Context::prefill_gpu(const pam_prefill_request &r) {
+    const pam_layer_spec &l = r.layer;
+    const PrefillPlan pl = plan_prefill(r);
     with_retry("prefill", [&] {
         mark(ev0_);
-        if (dense)
-            check_launch(launch_prefill_mfma(p, stream()), "prefill");
-        else
-            check_launch(launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "prefill");
+        launch_prefill_plan(pl, l.data_type);
         mark(ev1_);
         finish("prefill");
     });
-    const int32_t op = (dense || use_mfma) ? PAM_OP_PREFILL_MMA : PAM_OP_PREFILL_TILED_PASS;
-    record_stats(op, 1, r.seq_len, (int32_t)ceil_div(kv_len, l.block_size), tmp, p.max_parts > 1 || p.seg_count != nullptr, !dense);
+    const int32_t op = (pl.dense || pl.use_mfma) ? PAM_OP_PREFILL_MMA : PAM_OP_PREFILL_TILED_PASS;
+    record_stats(op, 1, r.seq_len, (int32_t)ceil_div(pl.kv_len, l.block_size), pl.tmp,
+                 pl.p.max_parts > 1 || pl.p.seg_count != nullptr, !pl.dense);
+}
+
+// fusedPrefill (PagedAttentionEngine.swift:633-710).  The reference runs one kernel
+// that writes the raw rows into the pool and then attends over them; here the
+// append kernel and the prefill kernel run back to back on the stream within one
+// call (the append moves seq_len rows, a small fraction of the prefill's time).
+// FP8 blocks get the append's per-block scale rule, so the pool bytes equal a
+// separate append's.
+void Context::fused_prefill(const pam_fused_prefill_request &r) {
+    validate_layer(r.layer);
+    const pam_layer_spec &l = r.layer;
+    if (r.seq_len <= 0) throw invalid_configuration("seqLen must be positive.");
+    const int64_t nb = ceil_div(r.seq_len, l.block_size);
+    require(r.block_table_bytes, "blockTable", nb * 4);
+    require(r.output_bytes, "output", r.seq_len * q_bytes_per_token(l));
+    require(r.q_bytes, "Q", r.seq_len * q_bytes_per_token(l));
+    const int64_t in_row = (int64_t)l.num_kv_heads * l.head_dim * io_bytes(l.data_type);
+    require(r.raw_k_bytes, "raw keys", r.seq_len * in_row);
+    require(r.raw_v_bytes, "raw values", r.seq_len * in_row);
+    require(r.k_pool_bytes, "K pool", pool_bytes_for(nb, l));
+    require(r.v_pool_bytes, "V pool", pool_bytes_for(nb, l));
+    if (l.data_type == kFP8 && (r.k_scale == nullptr || r.v_scale == nullptr))
+        throw invalid_configuration("FP8 fused prefill needs the K and V scale pools.");
+    if (!r.q || !r.raw_k || !r.raw_v || !r.block_table || !r.k_pool || !r.v_pool || !r.output)
+        throw invalid_configuration("fused prefill request has a null buffer.");
+    ensure_device();
+    fused_prefill_gpu(r);
+}
+
+void Context::fused_prefill_gpu(const pam_fused_prefill_request &r) {
+    const pam_layer_spec &l = r.layer;
+    pam_append_request a{};
+    a.keys = r.raw_k;
+    a.values = r.raw_v;
+    a.k_pool = r.k_pool;
+    a.v_pool = r.v_pool;
+    a.block_table = r.block_table;
+    a.token_offset = 0;
+    a.num_new_tokens = r.seq_len;
+    a.layer = l;
+    a.k_scale = r.k_scale;
+    a.v_scale = r.v_scale;
+    pam_prefill_request q{};
+    q.q = r.q;
+    q.k_pool = r.k_pool;
+    q.v_pool = r.v_pool;
+    q.block_table = r.block_table;
+    q.output = r.output;
+    q.seq_len = r.seq_len;
+    q.q_offset = 0;
+    q.layer = l;
+    q.causal = r.causal;
+    q.k_scale = r.k_scale;
+    q.v_scale = r.v_scale;
+    const AppendParams ap = append_params(a);
+    const PrefillPlan pl = plan_prefill(q);
+    with_retry("fusedPrefill", [&] {
+        mark(ev0_);
+        check_launch(launch_append(ap, l.data_type, stream()), "fused prefill append");
+        launch_prefill_plan(pl, l.data_type);
+        mark(ev1_);
+        finish("fusedPrefill");
+    });
+    // the reference reports its fused kernel as prefillSinglePass
+    record_stats(PAM_OP_PREFILL_SINGLE_PASS, 1, r.seq_len, (int32_t)ceil_div(r.seq_len, l.block_size), pl.tmp,
+                 pl.p.max_parts > 1 || pl.p.seg_count != nullptr, false);
 }
 
 // ------------------------------------------------------------------ append
@@ -499,7 +576,7 @@ void Context::append(const pam_append_request &r) {
     }
 }
 
-void Context::append_gpu(const pam_append_request &r) {
+AppendParams Context::append_params(const pam_append_request &r) {
     const pam_layer_spec &l = r.layer;
     AppendParams p{};
     p.keys = r.keys;
@@ -515,6 +592,12 @@ void Context::append_gpu(const pam_append_request &r) {
     p.num_kv_heads = l.num_kv_heads;
     p.head_dim = l.head_dim;
     p.block_size = l.block_size;
+    return p;
+}
+
+void Context::append_gpu(const pam_append_request &r) {
+    const pam_layer_spec &l = r.layer;
+    const AppendParams p = append_params(r);
     with_retry(l.data_type == kFP8 ? "appendToCacheCheckedFP8" : "appendToCacheFlat", [&] {
         mark(ev0_);
         check_launch(launch_append(p, l.data_type, stream()), "append");

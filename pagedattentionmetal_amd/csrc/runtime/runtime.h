@@ -87,6 +87,7 @@ class Context {
     void prefill(const pam_prefill_request &r);
     void append(const pam_append_request &r);
     void mixed_step(const pam_mixed_request &r);
+    void fused_prefill(const pam_fused_prefill_request &r);
     void fp8_quantize(const uint16_t *v, const uint16_t *s, uint8_t *o, int64_t n);
     void fp8_dequant(const uint8_t *c, const uint16_t *s, uint16_t *o, int64_t n);
 
@@ -121,6 +122,16 @@ class Context {
     void decode_gpu(const pam_decode_request &r);
     void prefill_gpu(const pam_prefill_request &r);
     void append_gpu(const pam_append_request &r);
+    void fused_prefill_gpu(const pam_fused_prefill_request &r);
+    // a prefill's launch, planned (parameters, kernel choice, split workspace)
+    struct PrefillPlan {
+        AttnParams p;
+        bool dense, use_mfma;
+        int64_t tmp, kv_len;
+    };
+    PrefillPlan plan_prefill(const pam_prefill_request &r);
+    void launch_prefill_plan(const PrefillPlan &pl, int32_t dtype);
+    AppendParams append_params(const pam_append_request &r);
     int32_t choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma);
     int64_t plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves);
     void record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t blocks, int64_t tmp, bool split,

@@ -180,3 +180,62 @@ def test_gpu_timing_switch(torch):
             assert st["kernel_ms"] > 0 and st["elapsed_ms"] > 0
         else:
             assert st["kernel_ms"] == -1 and st["elapsed_ms"] == -1
+
+
+@pytest.mark.parametrize("dtype,H,hkv,d,bs,T,causal,window", [
+    (0, 4, 2, 64, 16, 16, False, 0),     # the reference's fusedPrefill test shape (Tests/...:927-1030)
+    (0, 8, 8, 32, 16, 40, True, 0),
+    (1, 32, 8, 128, 16, 300, True, 0),   # f16, d = 128: dense MFMA prefill kernel
+    (1, 32, 8, 128, 16, 200, True, 64),  # fixed window start
+    (1, 16, 4, 64, 8, 77, True, 0),      # row kernels, bs 8
+    (2, 32, 8, 128, 16, 100, True, 0),   # FP8: quantise on append, dequantise in attention
+])
+def test_fused_prefill_equals_append_then_prefill(torch, dtype, H, hkv, d, bs, T, causal, window):
+    """Pool bytes (and FP8 scales) equal a separate append; the output equals a
+    separate prefill over that pool, bit for bit, and the oracle within tolerance."""
+    from pagedattentionmetal_amd import PagedAttentionEngine, PagedLayerSpec
+    eng = PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    rng = np.random.default_rng(60 + T + dtype)
+    io = np.float32 if dtype == 0 else np.float16
+    tdt = torch.float32 if dtype == 0 else torch.float16
+    nbl = (T + bs - 1) // bs
+    nb = nbl + 5
+    bt = rng.permutation(nb)[:nbl].astype(np.int32)
+    q = to_dev(rng.standard_normal((T, H, d)).astype(io))
+    rk = to_dev(rng.standard_normal((T, hkv, d)).astype(io))
+    rv = to_dev(rng.standard_normal((T, hkv, d)).astype(io))
+    pdt = torch.uint8 if dtype == 2 else tdt
+    layer = PagedLayerSpec(d, H, hkv, bs, dtype, window)
+    pools = []
+    for _ in range(2):
+        kp = torch.zeros((nb, bs, hkv, d), dtype=pdt, device="cuda")
+        vp = torch.zeros_like(kp)
+        ks = vs = None
+        if dtype == 2:
+            ks = torch.zeros(nb, dtype=torch.float16, device="cuda")
+            vs = torch.zeros_like(ks)
+        pools.append((kp, vp, ks, vs))
+    btd = to_dev(bt)
+    out_f = torch.zeros((T, H, d), dtype=tdt, device="cuda")
+    kp, vp, ks, vs = pools[0]
+    eng.fused_prefill(q, rk, rv, btd, kp, vp, out_f, T, layer, causal=causal, k_scale=ks, v_scale=vs)
+    assert eng.last_stats["operation"] == 1  # reported as prefillSinglePass, as the reference does
+    out_s = torch.zeros_like(out_f)
+    kp2, vp2, ks2, vs2 = pools[1]
+    eng.append_to_cache(rk, rv, kp2, vp2, btd, 0, T, layer, k_scale=ks2, v_scale=vs2)
+    eng.prefill(q, kp2, vp2, btd, out_s, T, layer, causal=causal, k_scale=ks2, v_scale=vs2)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(kp).view(np.uint8), to_host(kp2).view(np.uint8))
+    assert np.array_equal(to_host(vp).view(np.uint8), to_host(vp2).view(np.uint8))
+    ksh = vsh = None
+    if dtype == 2:
+        assert np.array_equal(to_host(ks).view(np.uint16), to_host(ks2).view(np.uint16))
+        assert np.array_equal(to_host(vs).view(np.uint16), to_host(vs2).view(np.uint16))
+        ksh, vsh = to_host(ks).view(np.uint16), to_host(vs).view(np.uint16)
+    got = to_host(out_f)
+    assert np.array_equal(got.view(np.uint8), to_host(out_s).view(np.uint8)), "fused != separate"
+    ref = oracle.prefill(dtype, to_host(q), to_host(kp), to_host(vp), bt, 0, causal=causal, window=window,
+                         k_scale=ksh, v_scale=vsh)
+    err = row_rel_err(got, ref)
+    assert err <= TOL[dtype], f"rel err {err:.3e}"

@@ -314,3 +314,28 @@ def test_scheduler_quirks(pam, ctx):
     assert pam.pam_scheduler_step(s, buf, 16) == 5 and list(buf[:5]) == [0, 1, 2, 3, 4]
     pam.pam_scheduler_destroy(s)
     pam.pam_destroy_cache(cache)
+
+
+def test_fused_prefill_validation(pam, ctx):
+    """fusedPrefill checks (PagedAttentionEngine.swift:633-641) run before any device
+    work: seqLen must be positive, the block table and output must be large enough."""
+    from pagedattentionmetal_amd import _lib
+    lay = _lib.LayerSpec(64, 4, 2, 16, 0, 0)
+    fake = 0x10000  # never dereferenced: validation fails first
+    def req(seq_len, bt_bytes=0, out_bytes=0):
+        return _lib.FusedPrefillRequest(fake, fake, fake, fake, fake, fake, fake, seq_len, lay, False, None, None,
+                                        0, 0, 0, 0, 0, bt_bytes, out_bytes)
+    r = req(0)
+    assert pam.pam_engine_fused_prefill(ctx, C.byref(r)) == -1
+    assert b"seqLen must be positive." in pam.pam_last_error(ctx)
+    r = req(40, bt_bytes=8)  # 3 blocks of 16 need 12 bytes
+    assert pam.pam_engine_fused_prefill(ctx, C.byref(r)) == -1
+    assert b"blockTable" in pam.pam_last_error(ctx)
+    r = req(40, out_bytes=40 * 4 * 64 * 4 - 4)
+    assert pam.pam_engine_fused_prefill(ctx, C.byref(r)) == -1
+    assert b"output" in pam.pam_last_error(ctx)
+    bad = _lib.LayerSpec(64, 3, 2, 16, 0, 0)  # H % Hkv != 0
+    r = _lib.FusedPrefillRequest(fake, fake, fake, fake, fake, fake, fake, 16, bad, False, None, None,
+                                 0, 0, 0, 0, 0, 0, 0)
+    assert pam.pam_engine_fused_prefill(ctx, C.byref(r)) == -1
+    assert pam.pam_last_error(ctx)
