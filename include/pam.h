@@ -189,6 +189,26 @@ typedef struct pam_fused_prefill_request {
     size_t q_bytes, raw_k_bytes, raw_v_bytes, k_pool_bytes, v_pool_bytes, block_table_bytes, output_bytes;
 } pam_fused_prefill_request;
 
+/* PagedAttentionEngine.backward (PagedAttentionEngine.swift:1340-1396): gradients of
+ * non-causal attention of rows 0 .. seq_len-1 over keys [max(0, seq_len - W),
+ * seq_len), given the forward's row max m and sum l ([seq_len][num_heads] float,
+ * natural-log units).  d_q is written; d_k_pool / d_v_pool (pool layout) are
+ * accumulated into.  f32 and f16 caches. */
+typedef struct pam_backward_request {
+    const void *q;
+    const void *k_pool;
+    const void *v_pool;
+    const int32_t *block_table;
+    const void *d_out;
+    const float *m;
+    const float *l;
+    void *d_q;
+    void *d_k_pool;
+    void *d_v_pool;
+    int32_t seq_len;
+    pam_layer_spec layer;
+} pam_backward_request;
+
 /* PagedAttentionEngine.decode(_:) (PagedAttentionEngine.swift:533-546) */
 int32_t pam_engine_decode(void *context, const pam_decode_request *request);
 /* PagedAttentionEngine.prefill(_:) (PagedAttentionEngine.swift:405-418) */
@@ -198,6 +218,8 @@ int32_t pam_engine_append(void *context, const pam_append_request *request);
 /* PagedAttentionEngine.fusedPrefill(_:) (PagedAttentionEngine.swift:633-710): append
  * and prefill as one call, both launches on the context's stream */
 int32_t pam_engine_fused_prefill(void *context, const pam_fused_prefill_request *request);
+/* PagedAttentionEngine.backward(q:kPool:...) (PagedAttentionEngine.swift:1340-1396) */
+int32_t pam_engine_backward(void *context, const pam_backward_request *request);
 /* PagedAttentionEngine.lastStats (PagedAttentionEngine.swift:136-141) */
 int32_t pam_engine_last_stats(void *context, pam_stats *out);
 /* PagedAttentionEngine.enableGracefulDegradation / maxRetries (Engine.swift:126-129) */

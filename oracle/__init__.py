@@ -174,3 +174,66 @@ def merge(m, l, o):
     out = np.empty(o.shape[1], np.float64)
     lib().pamo_merge(len(m), _p(m), _p(l), _p(o), o.shape[1], _p(out))
     return out
+
+
+def _gather_rows(pool, block_table, seq_len):
+    """Pool rows of tokens 0 .. seq_len-1 of one sequence: [seq_len][Hkv][d] fp64."""
+    nb, bs, hkv, d = pool.shape
+    j = np.arange(seq_len)
+    return pool[np.asarray(block_table)[j // bs], j % bs].astype(np.float64)
+
+
+def forward_stats(q, k_pool, v_pool, block_table, window=0):
+    """Row max m and sum l (natural-log units, scores scaled by 1/sqrt(d)) of the
+    non-causal attention the backward differentiates (rows 0 .. T-1 over keys
+    [max(0, T - W), T)), as the forward's online softmax leaves them
+    (kernels.metal:1217-1260 reads them as inputs).  Returns (m, l, O) in fp64."""
+    T, H, d = q.shape
+    hkv = k_pool.shape[2]
+    G = H // hkv
+    ws = max(0, T - window) if window > 0 else 0
+    K = _gather_rows(k_pool, block_table, T)[ws:]
+    V = _gather_rows(v_pool, block_table, T)[ws:]
+    qf = q.astype(np.float64)
+    m = np.empty((T, H))
+    l = np.empty((T, H))
+    o = np.empty((T, H, d))
+    for h in range(H):
+        s = qf[:, h] @ K[:, h // G].T / np.sqrt(d)
+        m[:, h] = s.max(1)
+        e = np.exp(s - m[:, h:h + 1])
+        l[:, h] = e.sum(1)
+        o[:, h] = e @ V[:, h // G] / l[:, h:h + 1]
+    return m, l, o
+
+
+def backward(q, k_pool, v_pool, block_table, d_out, m, l, window=0):
+    """Gradients of paged attention (kernels.metal:1217-1314, paged_attention_backward):
+    with P = exp(s - m) / l over keys [max(0, T - W), T), dP = dO V^T,
+    D = rowsum(P * dP), dS = P (dP - D):
+      dQ = scale dS K;  dK_j = scale sum_i dS_ij q_i;  dV_j = sum_i P_ij dO_i,
+    the key gradients summed over the query heads of each kv head.  Returns
+    (dQ [T][H][d], dK [T][Hkv][d], dV [T][Hkv][d]) in fp64; keys before the window
+    get zero.  Pinned by central finite differences of the dense forward."""
+    T, H, d = q.shape
+    hkv = k_pool.shape[2]
+    G = H // hkv
+    ws = max(0, T - window) if window > 0 else 0
+    K = _gather_rows(k_pool, block_table, T)
+    V = _gather_rows(v_pool, block_table, T)
+    qf, go = q.astype(np.float64), d_out.astype(np.float64)
+    sc = 1.0 / np.sqrt(d)
+    dq = np.zeros((T, H, d))
+    dk = np.zeros((T, hkv, d))
+    dv = np.zeros((T, hkv, d))
+    for h in range(H):
+        g = h // G
+        s = qf[:, h] @ K[ws:, g].T * sc
+        P = np.exp(s - np.asarray(m, np.float64)[:, h:h + 1]) / np.asarray(l, np.float64)[:, h:h + 1]
+        dP = go[:, h] @ V[ws:, g].T
+        D = (P * dP).sum(1, keepdims=True)
+        dS = P * (dP - D)
+        dq[:, h] = sc * dS @ K[ws:, g]
+        dk[ws:, g] += sc * dS.T @ qf[:, h]
+        dv[ws:, g] += P.T @ go[:, h]
+    return dq, dk, dv

@@ -50,6 +50,11 @@ class FusedPrefillRequest(C.Structure):
                 ("v_pool_bytes", SZ), ("block_table_bytes", SZ), ("output_bytes", SZ)]
 
 
+class BackwardRequest(C.Structure):
+    _fields_ = [("q", P), ("k_pool", P), ("v_pool", P), ("block_table", P), ("d_out", P), ("m", P), ("l", P),
+                ("d_q", P), ("d_k_pool", P), ("d_v_pool", P), ("seq_len", I32), ("layer", LayerSpec)]
+
+
 class AppendRequest(C.Structure):
     _fields_ = [("keys", P), ("values", P), ("k_pool", P), ("v_pool", P), ("block_table", P), ("token_offset", I32),
                 ("num_new_tokens", I32), ("layer", LayerSpec), ("k_scale", P), ("v_scale", P), ("slot_mapping", P),
@@ -91,6 +96,7 @@ SIGNATURES = {
     "pam_engine_prefill": (I32, [P, C.POINTER(PrefillRequest)]),
     "pam_engine_append": (I32, [P, C.POINTER(AppendRequest)]),
     "pam_engine_fused_prefill": (I32, [P, C.POINTER(FusedPrefillRequest)]),
+    "pam_engine_backward": (I32, [P, C.POINTER(BackwardRequest)]),
     "pam_engine_last_stats": (I32, [P, C.POINTER(Stats)]),
     "pam_engine_set_graceful_degradation": (I32, [P, C.c_bool]),
     "pam_engine_set_max_retries": (I32, [P, I32]),

@@ -227,6 +227,14 @@ class PagedAttentionEngine:
             _nbytes(raw_v), _nbytes(k_pool), _nbytes(v_pool), _nbytes(block_table), _nbytes(output))
         self._check(lib().pam_engine_fused_prefill(self._ctx, C.byref(r)))
 
+    # --- PagedAttentionEngine.backward (PagedAttentionEngine.swift:1340-1396)
+    def backward(self, q, k_pool, v_pool, block_table, d_out, m, l, d_q, d_k_pool, d_v_pool, seq_len,
+                 layer: PagedLayerSpec):
+        """Gradients of non-causal paged attention: d_q written, d_k_pool / d_v_pool accumulated."""
+        r = _lib.BackwardRequest(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_table), _ptr(d_out), _ptr(m),
+                                 _ptr(l), _ptr(d_q), _ptr(d_k_pool), _ptr(d_v_pool), int(seq_len), layer.c())
+        self._check(lib().pam_engine_backward(self._ctx, C.byref(r)))
+
     # --- mixed continuous-batching step (no reference counterpart)
     def mixed_step(self, q, output, k_pool, v_pool, block_tables, context_lens, query_lens, layer: PagedLayerSpec,
                    new_keys=None, new_values=None, k_scale=None, v_scale=None):

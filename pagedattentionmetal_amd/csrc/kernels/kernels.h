@@ -103,6 +103,21 @@ struct AppendBatchParams {
 };
 hipError_t launch_append_batch(const AppendBatchParams &p, int32_t dtype, hipStream_t stream);
 
+// Attention gradients of one sequence (training path): non-causal rows
+// 0 .. seq_len-1 over keys [window_start, seq_len); m, l are the forward's row max
+// and sum (natural-log units), row_d is a [seq_len][H] float workspace.
+struct BackwardParams {
+    const void *q, *k_pool, *v_pool, *d_out;  // f32 or f16 (the cache type)
+    const int32_t *block_table;
+    const float *m, *l;
+    void *d_q, *d_k_pool, *d_v_pool;
+    float *row_d;
+    int32_t seq_len, window_start;
+    int32_t num_heads, num_kv_heads, head_dim, block_size;
+    float scale;  // 1 / sqrt(head_dim)
+};
+hipError_t launch_backward(const BackwardParams &p, int32_t dtype, hipStream_t stream);
+
 // Exhaustive codec entry points (used by the codec tests through the C ABI).
 hipError_t launch_fp8_quantize(const uint16_t *values, const uint16_t *scales, uint8_t *out, int64_t n,
                                hipStream_t stream);

@@ -267,6 +267,11 @@ PAM_API int32_t pam_engine_fused_prefill(void *context, const pam_fused_prefill_
     return guarded(context, [&](Context *ctx) { ctx->fused_prefill(*request); });
 }
 
+PAM_API int32_t pam_engine_backward(void *context, const pam_backward_request *request) {
+    if (!request) return -1;
+    return guarded(context, [&](Context *ctx) { ctx->backward(*request); });
+}
+
 PAM_API int32_t pam_engine_last_stats(void *context, pam_stats *out) {
     if (!out) return -1;
     return guarded(context, [&](Context *ctx) { *out = ctx->stats(); });

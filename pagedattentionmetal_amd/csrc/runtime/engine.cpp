@@ -542,6 +542,50 @@ void Context::fused_prefill_gpu(const pam_fused_prefill_request &r) {
                  pl.p.max_parts > 1 || pl.p.seg_count != nullptr, false);
 }
 
+// ------------------------------------------------------------------ backward
+
+// backward(q:kPool:vPool:...) (PagedAttentionEngine.swift:1340-1396): withRetry,
+// no degradation, f32 or f16.
+void Context::backward(const pam_backward_request &r) {
+    validate_layer(r.layer);
+    const pam_layer_spec &l = r.layer;
+    if (r.seq_len <= 0) throw invalid_configuration("seqLen must be positive.");
+    if (l.data_type == kFP8) throw PamError("Unsupported paged attention path: backward takes f32 or f16 caches.");
+    if (l.head_dim > 256) throw PamError("Unsupported paged attention path: backward needs headDim <= 256.");
+    if (!r.q || !r.k_pool || !r.v_pool || !r.block_table || !r.d_out || !r.m || !r.l || !r.d_q || !r.d_k_pool ||
+        !r.d_v_pool)
+        throw invalid_configuration("backward request has a null buffer.");
+    ensure_device();
+    BackwardParams p{};
+    p.q = r.q;
+    p.k_pool = r.k_pool;
+    p.v_pool = r.v_pool;
+    p.d_out = r.d_out;
+    p.block_table = r.block_table;
+    p.m = r.m;
+    p.l = r.l;
+    p.d_q = r.d_q;
+    p.d_k_pool = r.d_k_pool;
+    p.d_v_pool = r.d_v_pool;
+    p.seq_len = r.seq_len;
+    p.window_start = l.window_size > 0 ? std::max(0, r.seq_len - l.window_size) : 0;
+    p.num_heads = l.num_heads;
+    p.num_kv_heads = l.num_kv_heads;
+    p.head_dim = l.head_dim;
+    p.block_size = l.block_size;
+    p.scale = 1.0f / std::sqrt((float)l.head_dim);
+    const int64_t tmp = (int64_t)r.seq_len * l.num_heads * 4;
+    reserve_workspace((size_t)tmp);
+    p.row_d = static_cast<float *>(workspace_.ptr);
+    with_retry("backward", [&] {
+        mark(ev0_);
+        check_launch(launch_backward(p, l.data_type, stream()), "backward");
+        mark(ev1_);
+        finish("backward");
+    });
+    record_stats(PAM_OP_BACKWARD, 1, r.seq_len, (int32_t)ceil_div(r.seq_len, l.block_size), tmp, false, false);
+}
+
 // ------------------------------------------------------------------ append
 
 void Context::append(const pam_append_request &r) {

@@ -88,6 +88,7 @@ class Context {
     void append(const pam_append_request &r);
     void mixed_step(const pam_mixed_request &r);
     void fused_prefill(const pam_fused_prefill_request &r);
+    void backward(const pam_backward_request &r);
     void fp8_quantize(const uint16_t *v, const uint16_t *s, uint8_t *o, int64_t n);
     void fp8_dequant(const uint8_t *c, const uint16_t *s, uint16_t *o, int64_t n);
 

@@ -322,3 +322,42 @@ def test_fp8_decode_uses_dequantised_pool():
     vd = oracle.dequant_pool(vp, vs).astype(np.float32)
     ref = oracle.decode(0, q.astype(np.float32), kd, vd, bt, lens, H)
     assert np.allclose(out, ref, rtol=1e-12, atol=1e-14)
+
+
+def test_backward_matches_finite_differences():
+    """The backward restatement equals central differences of the dense fp64
+    forward loss sum(dO * O) in q, k and v (window and GQA included)."""
+    rng = np.random.default_rng(17)
+    T, H, hkv, d, bs, W = 6, 4, 2, 4, 2, 4
+    nb = 5
+    bt = np.array([3, 0, 4], np.int32)
+    kp = rng.standard_normal((nb, bs, hkv, d))
+    vp = rng.standard_normal((nb, bs, hkv, d))
+    q = rng.standard_normal((T, H, d))
+    go = rng.standard_normal((T, H, d))
+    m, l, _ = oracle.forward_stats(q, kp, vp, bt, window=W)
+    dq, dk, dv = oracle.backward(q, kp, vp, bt, go, m, l, window=W)
+
+    def loss(q_, kp_, vp_):
+        return float((oracle.forward_stats(q_, kp_, vp_, bt, window=W)[2] * go).sum())
+    eps = 1e-6
+    num_q = np.zeros_like(q)
+    for idx in np.ndindex(q.shape):
+        a, b = q.copy(), q.copy()
+        a[idx] += eps
+        b[idx] -= eps
+        num_q[idx] = (loss(a, kp, vp) - loss(b, kp, vp)) / (2 * eps)
+    assert np.allclose(dq, num_q, atol=1e-7, rtol=1e-6)
+    for pool, grad, which in ((kp, dk, "k"), (vp, dv, "v")):
+        for j in range(T):
+            for g in range(hkv):
+                for e in range(d):
+                    a, b = pool.copy(), pool.copy()
+                    blk, s = bt[j // bs], j % bs
+                    a[blk, s, g, e] += eps
+                    b[blk, s, g, e] -= eps
+                    num = ((loss(q, a, vp) - loss(q, b, vp)) if which == "k" else
+                           (loss(q, kp, a) - loss(q, kp, b))) / (2 * eps)
+                    assert abs(grad[j, g, e] - num) <= 1e-7 + 1e-6 * abs(num), (which, j, g, e)
+    # keys before the window start get no gradient
+    assert not dk[:T - W].any() and not dv[:T - W].any()
