@@ -296,7 +296,9 @@ void pam_buffer_free(void *context, void *ptr);
 int32_t pam_buffer_upload(void *context, void *device_dst, const void *host_src, size_t bytes);
 int32_t pam_buffer_download(void *context, void *host_dst, const void *device_src, size_t bytes);
 int32_t pam_buffer_zero(void *context, void *device_ptr, size_t bytes);
-/* Launch on an external hipStream_t (NULL = the device's default stream). */
+/* Launch on an external hipStream_t (NULL = the device's default stream).  Work the
+ * context issued on its previous stream is ordered before its work on the new one
+ * (an event wait), since its launches share one workspace. */
 int32_t pam_set_stream(void *context, void *hip_stream);
 /* Go back to launching on the context's own stream (a blocking stream: ordered
  * against work on the legacy default stream). */

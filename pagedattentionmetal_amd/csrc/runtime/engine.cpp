@@ -68,6 +68,7 @@ Context::~Context() {
     if (ev0_) (void)hipEventDestroy(ev0_);
     if (ev1_) (void)hipEventDestroy(ev1_);
     if (evmid_) (void)hipEventDestroy(evmid_);
+    if (handoff_) (void)hipEventDestroy(handoff_);
     if (zero_page_) (void)hipFree(zero_page_);
     if (staged_) (void)hipEventDestroy(staged_);
     if (own_stream_) (void)hipStreamDestroy(own_stream_);
@@ -86,6 +87,7 @@ void Context::ensure_device() {
     hip_check(hipEventCreate(&ev0_), "hipEventCreate");
     hip_check(hipEventCreate(&ev1_), "hipEventCreate");
     hip_check(hipEventCreate(&evmid_), "hipEventCreate");
+    hip_check(hipEventCreateWithFlags(&handoff_, hipEventDisableTiming), "hipEventCreate");
     hip_check(hipEventCreateWithFlags(&staged_, hipEventDisableTiming), "hipEventCreate");
     // zeros that masked lanes of the attention kernels load instead of pool rows
     hip_check(hipMalloc(&zero_page_, kZeroPageBytes), "hipMalloc zero page");
@@ -94,6 +96,16 @@ void Context::ensure_device() {
 }
 
 hipStream_t Context::stream() { return use_ext_stream_ ? ext_stream_ : own_stream_; }
+
+void Context::switch_stream(bool use_ext, hipStream_t s) {
+    const hipStream_t old = stream();
+    ext_stream_ = use_ext ? s : nullptr;
+    use_ext_stream_ = use_ext;
+    if (device_ready_ && stream() != old) {
+        hip_check(hipEventRecord(handoff_, old), "stream handoff");
+        hip_check(hipStreamWaitEvent(stream(), handoff_, 0), "stream handoff");
+    }
+}
 
 void Context::finish(const char *what) {
     hip_check(hipGetLastError(), what);

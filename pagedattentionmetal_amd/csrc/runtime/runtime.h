@@ -71,14 +71,13 @@ class Context {
     // --- device state (created on first GPU use)
     void ensure_device();
     hipStream_t stream();
-    void set_stream(hipStream_t s) {
-        ext_stream_ = s;
-        use_ext_stream_ = true;
-    }
-    void use_own_stream() {
-        ext_stream_ = nullptr;
-        use_ext_stream_ = false;
-    }
+    // Launch on a caller's stream (or back on the context's own).  Work the
+    // context already issued on the previous stream is ordered before anything
+    // it issues on the new one: its launches share the split workspace and the
+    // stream-K counters, so they must never overlap.
+    void set_stream(hipStream_t s) { switch_stream(true, s); }
+    void use_own_stream() { switch_stream(false, nullptr); }
+    void switch_stream(bool use_ext, hipStream_t s);
     bool synchronous = true;
     void finish(const char *what);  // synchronise when synchronous, surface GPU errors
 
@@ -143,7 +142,7 @@ class Context {
     int cus_ = 256;  // compute units of the device (set in ensure_device)
     hipStream_t own_stream_ = nullptr, ext_stream_ = nullptr;
     bool use_ext_stream_ = false;
-    hipEvent_t ev0_ = nullptr, ev1_ = nullptr, evmid_ = nullptr, staged_ = nullptr;
+    hipEvent_t ev0_ = nullptr, ev1_ = nullptr, evmid_ = nullptr, staged_ = nullptr, handoff_ = nullptr;
     void *zero_page_ = nullptr;
     bool stats_pending_ = false;
     bool stats_has_mid_ = false;

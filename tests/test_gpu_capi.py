@@ -239,3 +239,36 @@ def test_fused_prefill_equals_append_then_prefill(torch, dtype, H, hkv, d, bs, T
                          k_scale=ksh, v_scale=vsh)
     err = row_rel_err(got, ref)
     assert err <= TOL[dtype], f"rel err {err:.3e}"
+
+
+def test_stream_switch_orders_work(torch):
+    """Two asynchronous decodes that both need split-context partials (the shared
+    workspace and stream-K counters), issued by one context on two streams: the
+    switch orders the second after the first, so both are correct."""
+    from pagedattentionmetal_amd import PagedAttentionEngine, PagedLayerSpec
+    from helpers import make_case
+    eng = PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    rng = np.random.default_rng(123)
+    cases = []
+    for lens in ([9000, 7000, 300], [12000, 50]):
+        q, k, v, bt, ln = make_case(rng, len(lens), 32, 8, 128, 16, 1, lens)
+        cases.append((q, k, v, bt, ln, oracle.decode(1, q, k, v, bt, ln, 32, n_threads=8)))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    eng.synchronous = False
+    outs = []
+    try:
+        for (q, k, v, bt, ln, _), s in zip(cases, (s1, s2)):
+            eng.set_stream(s)
+            with torch.cuda.stream(s):
+                args = (to_dev(q), to_dev(k), to_dev(v), to_dev(bt), to_dev(ln))
+                out = torch.zeros((len(ln), 32, 128), dtype=torch.float16, device="cuda")
+            s.synchronize()  # inputs in place; the decodes themselves stay asynchronous
+            eng.decode(*args, out, len(ln), bt.shape[1], PagedLayerSpec(128, 32, 8, 16, 1))
+            outs.append((out, args))
+        torch.cuda.synchronize()
+    finally:
+        eng.synchronous = True
+        eng.set_stream(None)
+    for (out, _), case in zip(outs, cases):
+        assert row_rel_err(to_host(out), case[5]) <= TOL[1]
