@@ -124,6 +124,10 @@ hipError_t launch_fp8_quantize(const uint16_t *values, const uint16_t *scales, u
 hipError_t launch_fp8_dequant(const uint8_t *codes, const uint16_t *scales, uint16_t *out, int64_t n,
                               hipStream_t stream);
 
+// Copy `bytes` from mapped pinned host memory to the device, as a kernel on
+// `stream` (both pointers 16-byte aligned).
+hipError_t launch_stage_copy(const void *host_mapped, void *dst, size_t bytes, hipStream_t stream);
+
 // Calibration streams of known size (achievable HBM rates, counter scaling).
 hipError_t launch_stream_read(const void *src, size_t bytes, uint32_t *sink, int blocks, hipStream_t stream);
 hipError_t launch_stream_copy(const void *src, void *dst, size_t bytes, int blocks, hipStream_t stream);

@@ -227,8 +227,11 @@ PAM_API int32_t pam_decode(void *context, void *cache, const int64_t *batchIDs, 
             lens[i] = (uint32_t)s.length;
         }
         pam_decode_request r{};
-        r.block_tables = static_cast<const int32_t *>(ctx->stage(1, slab.data(), slab.size() * 4));
-        r.seq_lengths = static_cast<const uint32_t *>(ctx->stage(2, lens.data(), lens.size() * 4));
+        StageList sl;
+        const size_t o_slab = sl.add(slab.data(), slab.size() * 4), o_lens = sl.add(lens.data(), lens.size() * 4);
+        const char *base = static_cast<const char *>(ctx->stage(1, sl.blob.data(), sl.blob.size()));
+        r.block_tables = reinterpret_cast<const int32_t *>(base + o_slab);
+        r.seq_lengths = reinterpret_cast<const uint32_t *>(base + o_lens);
         r.block_tables_bytes = slab.size() * 4;
         r.seq_lengths_bytes = lens.size() * 4;
         r.q = query;

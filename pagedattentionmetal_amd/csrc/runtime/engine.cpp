@@ -150,14 +150,21 @@ void *Context::stage_into(void *dst, const void *host, size_t bytes) {
             pinned_ = nullptr;
             pinned_bytes_ = 0;
             size_t want = std::max<size_t>(need, 1 << 20);
-            hip_check(hipHostMalloc(&pinned_, want, hipHostMallocDefault), "hipHostMalloc");
+            hip_check(hipHostMalloc(&pinned_, want, hipHostMallocMapped), "hipHostMalloc");
+            hip_check(hipHostGetDevicePointer(&pinned_dev_, pinned_, 0), "hipHostGetDevicePointer");
             pinned_bytes_ = want;
         }
     }
     char *src = static_cast<char *>(pinned_) + pinned_used_;
     std::memcpy(src, host, bytes);
+    // a copy kernel on this stream (a DMA-engine copy would cost an engine
+    // hand-off around the call); destinations are 256-byte aligned allocations
+    const char *src_dev = static_cast<const char *>(pinned_dev_) + pinned_used_;
     pinned_used_ += need;
-    hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream()), "hipMemcpyAsync staging");
+    if (((uintptr_t)dst & 15) == 0)
+        hip_check(launch_stage_copy(src_dev, dst, bytes, stream()), "staging copy");
+    else
+        hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream()), "hipMemcpyAsync staging");
     hip_check(hipEventRecord(staged_, stream()), "hipEventRecord");
     return dst;
 }
@@ -716,15 +723,36 @@ void Context::mixed_step(const pam_mixed_request &r) {
     if (decode_kernel_choice == 1) use_mfma = false;
     const int32_t nh = heads_per_wave(G);
 
-    // device-side descriptors
-    const int4 *d_rows =
-        ragged_rows ? static_cast<const int4 *>(stage(0, rows.data(), rows.size() * sizeof(int4))) : nullptr;
-    const int4 *d_chunks =
-        chunks.empty() ? nullptr : static_cast<const int4 *>(stage(4, chunks.data(), chunks.size() * sizeof(int4)));
+    // device-side descriptors, staged with one copy (StageList)
+    StageList sl;
+    const size_t o_rows = sl.add(rows.data(), rows.size() * sizeof(int4));
+    const size_t o_chunks = sl.add(chunks.data(), chunks.size() * sizeof(int4));
     AppendBatchParams ab{};
     std::vector<int2> tok;
     std::vector<int4> work;
-    if (r.new_keys && r.new_values) {
+    size_t o_cu = 0, o_ctx = 0, o_work = 0, o_tok = 0;
+    const bool appending = r.new_keys && r.new_values;
+    if (appending) {
+        o_cu = sl.add(cu.data(), cu.size() * 4);
+        o_ctx = sl.add(r.context_lens, (size_t)r.num_seqs * 4);
+        if (l.data_type == kFP8) {
+            for (int32_t s = 0; s < r.num_seqs; s++) {
+                const int64_t c = r.context_lens[s], T = r.query_lens[s];
+                if (T <= 0) continue;
+                for (int64_t lb = c / bs; lb <= (c + T - 1) / bs; lb++) work.push_back(make_int4(s, (int)lb, 0, 0));
+            }
+            o_work = sl.add(work.data(), work.size() * sizeof(int4));
+        } else {
+            // per-token (sequence, position); the kernel resolves slots from the device table
+            for (int32_t s = 0; s < r.num_seqs; s++)
+                for (int64_t i = 0; i < r.query_lens[s]; i++) tok.push_back(make_int2(s, (int)(r.context_lens[s] + i)));
+            o_tok = sl.add(tok.data(), tok.size() * sizeof(int2));
+        }
+    }
+    const char *sbase = static_cast<const char *>(stage(0, sl.blob.data(), sl.blob.size()));
+    const int4 *d_rows = ragged_rows ? reinterpret_cast<const int4 *>(sbase + o_rows) : nullptr;
+    const int4 *d_chunks = chunks.empty() ? nullptr : reinterpret_cast<const int4 *>(sbase + o_chunks);
+    if (appending) {
         ab.keys = r.new_keys;
         ab.values = r.new_values;
         ab.k_pool = r.k_pool;
@@ -738,21 +766,13 @@ void Context::mixed_step(const pam_mixed_request &r) {
         ab.num_kv_heads = l.num_kv_heads;
         ab.head_dim = l.head_dim;
         ab.block_size = bs;
-        ab.cu_tokens = static_cast<const int32_t *>(stage(1, cu.data(), cu.size() * 4));
-        ab.token_offsets = static_cast<const int32_t *>(stage(2, r.context_lens, (size_t)r.num_seqs * 4));
+        ab.cu_tokens = reinterpret_cast<const int32_t *>(sbase + o_cu);
+        ab.token_offsets = reinterpret_cast<const int32_t *>(sbase + o_ctx);
         if (l.data_type == kFP8) {
-            for (int32_t s = 0; s < r.num_seqs; s++) {
-                const int64_t c = r.context_lens[s], T = r.query_lens[s];
-                if (T <= 0) continue;
-                for (int64_t lb = c / bs; lb <= (c + T - 1) / bs; lb++) work.push_back(make_int4(s, (int)lb, 0, 0));
-            }
-            ab.work = static_cast<const int4 *>(stage(3, work.data(), work.size() * sizeof(int4)));
+            ab.work = reinterpret_cast<const int4 *>(sbase + o_work);
             ab.num_work = (int32_t)work.size();
         } else {
-            // per-token (sequence, position); the kernel resolves slots from the device table
-            for (int32_t s = 0; s < r.num_seqs; s++)
-                for (int64_t i = 0; i < r.query_lens[s]; i++) tok.push_back(make_int2(s, (int)(r.context_lens[s] + i)));
-            ab.token_pos = static_cast<const int2 *>(stage(3, tok.data(), tok.size() * sizeof(int2)));
+            ab.token_pos = reinterpret_cast<const int2 *>(sbase + o_tok);
         }
     }
 

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstring>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -29,6 +30,19 @@ struct DeviceBuffer {
 };
 
 class Context;
+
+// Several host arrays staged to the device with one copy: parts are packed at
+// 16-byte offsets into one blob; after Context::stage of the blob, part i lives
+// at base + offset(i).
+struct StageList {
+    std::vector<char> blob;
+    size_t add(const void *p, size_t bytes) {
+        const size_t off = (blob.size() + 15) & ~(size_t)15;
+        blob.resize(off + bytes);
+        if (bytes) std::memcpy(blob.data() + off, p, bytes);
+        return off;
+    }
+};
 
 class KVCache {
    public:
@@ -150,6 +164,7 @@ class Context {
     DeviceBuffer seg_count_;  // stream-K counters: zero between launches
     DeviceBuffer scratch_[6];
     void *pinned_ = nullptr;
+    void *pinned_dev_ = nullptr;  // the device's address of pinned_
     size_t pinned_bytes_ = 0;
     size_t pinned_used_ = 0;
 };
