@@ -1,24 +1,26 @@
 // attention.hip - paged attention over query rows for gfx950.
 //
-// One wave64 owns (row, kv head | head group, split-context partition).  A row is
-// a decode query (kernels.metal:1417-1802 semantics), a prefill query position
-// (kernels.metal:693-917 semantics with an explicit query offset) or a ragged row
-// of a mixed continuous-batching step.  Keys are walked in 16-token tiles of the
-// logical sequence; the block table maps each token to its physical block, so
-// any block_size works and blocks may sit anywhere in the pool.
+// A row is a decode query (kernels.metal:1417-1802 semantics), a prefill query
+// position (kernels.metal:693-917 semantics with an explicit query offset) or a
+// ragged row of a mixed continuous-batching step.  Keys are walked in 16-token
+// tiles of the logical sequence; the block table maps each token to its
+// physical block, so blocks may sit anywhere in the pool.
 //
-// Two bodies:
-//  * attn_mfma_kernel - GQA groups 4..16, f16 or e4m3 KV.  S^T = K Q^T with
-//    v_mfma_f32_16x16x32_f16 (K rows feed the A operand straight from their
-//    16-byte HBM loads, query heads are the N columns), then O^T = V^T P^T with
-//    v_mfma_f32_16x16x16_f16: the S^T accumulator layout (lane%16 = head,
-//    lane/16 = token quad) is exactly the B-operand layout of P^T, so softmax
-//    needs no data movement; V is transposed through a padded LDS tile.
+// Bodies:
+//  * the MFMA tile loop (mfma_core) - GQA groups >= 4, f16 or e4m3 KV: token
+//    rows are loaded whole (16 lanes per 256-byte row), staged through LDS, and
+//    S^T = K Q^T (v_mfma_f32_16x16x32_f16, query heads on the N side) and
+//    O^T = V^T P^T (v_mfma_f32_16x16x16_f16, V^T read with the transposing
+//    ds_read_b64_tr_b16) run on them; the S^T accumulator layout is P^T's
+//    B-operand layout, so softmax needs no data movement.  Two work forms:
+//      - attn_mfma_streamk (up to kStreamKMaxRows rows): the resident grid
+//        splits all rows' tiles into equal units and merges split rows itself;
+//      - attn_mfma_kernel: one workgroup per (row, partition, kv head), its
+//        waves merged in LDS, partitions merged by attn_reduce_kernel;
 //  * attn_valu_kernel - any group and f32 KV: lanes split a token row into
 //    4-element slices, dot products reduce across the row's lanes.
-// Both keep the online-softmax state of Reference/paged_attention_sim.py:94-123
-// (in log2 units) and either finish the row or write a partial (m, l, O) for
-// the split-context reduce kernel.
+// All keep the online-softmax state of Reference/paged_attention_sim.py:94-123
+// (in log2 units).
 #include "kernels.h"
 #include "pam_device.h"
 
@@ -110,11 +112,12 @@ __device__ __forceinline__ f16x8 e4m3x8_to_f16x8(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(f16x8, h);
 }
 
-// Waves per workgroup of the MFMA kernel: they split one partition's tiles and
-// merge their softmax states in LDS.
+// Waves per workgroup of the MFMA kernels: in the workgroup form they split one
+// partition's tiles and merge in LDS; in the stream-K form they read up to four
+// kv heads of the same tiles side by side.
 constexpr int kMfmaWaves = 4;
 // Rows the stream-K form can index from LDS (its row prefix table).
-constexpr int kPersistentMaxRows = 2048;
+constexpr int kStreamKMaxRows = 2048;
 // Decode rows whose key ranges the stream-K form keeps in LDS (8 KiB: three
 // workgroups of the e4m3 kernel still fit a CU).
 constexpr int kStreamKRangeCache = 1024;
@@ -514,7 +517,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const AttnParams &p)
     return __builtin_amdgcn_make_buffer_rsrc(p.part_o, 0, (int)p.part_bytes, 0x00020000);
 }
 
-// Stream-K form (rows <= kPersistentMaxRows).  The key tiles of all rows are laid
+// Stream-K form (rows <= kStreamKMaxRows).  The key tiles of all rows are laid
 // end to end on one line, row after row.  The workgroups are taken in runs of
 // NHG = Hkv / NH (NH = 4, 2 or 1 kv heads, the largest dividing Hkv, read side by
 // side by the NH waves of a workgroup): the run of unit u covers tiles
@@ -535,7 +538,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
     using S = MfmaShape<KV, HD>;
     constexpr int NO = S::NO, WT = S::WT;
     __shared__ __attribute__((aligned(16))) f16 tiles[kMfmaWaves * WT];
-    __shared__ int32_t prefix[kPersistentMaxRows + 1];
+    __shared__ int32_t prefix[kStreamKMaxRows + 1];
     __shared__ int2 key_range[kStreamKRangeCache];  // decode rows: {k_lo, k_hi}
     __shared__ int32_t wave_sum[kMfmaWaves];
     constexpr int NT = 64 * kMfmaWaves;
@@ -944,7 +947,7 @@ template <typename KV, int HD, int BLK>
 static hipError_t launch_mfma_blk(const AttnParams &p, hipStream_t stream) {
     const dim3 block(64 * kMfmaWaves);
     if (p.seg_count != nullptr) {
-        if (p.rows > kPersistentMaxRows) return hipErrorInvalidValue;
+        if (p.rows > kStreamKMaxRows) return hipErrorInvalidValue;
         int grid = 0;
         const hipError_t e = streamk_grid<KV, HD, BLK>(&grid);
         if (e != hipSuccess) return e;
@@ -991,7 +994,7 @@ static hipError_t streamk_grid_kv(int head_dim, int block_size, int *grid) {
 }
 
 bool mfma_streamk_plan(const AttnParams &p, int32_t dtype, int64_t *part_slots, int64_t *counters) {
-    if (p.rows <= 0 || p.rows > kPersistentMaxRows) return false;
+    if (p.rows <= 0 || p.rows > kStreamKMaxRows) return false;
     if (!mfma_supported(dtype, p.head_dim, p.num_heads / p.num_kv_heads, p.block_size)) return false;
     int grid = 0;
     const hipError_t e = dtype == kF16 ? streamk_grid_kv<f16>(p.head_dim, p.block_size, &grid)

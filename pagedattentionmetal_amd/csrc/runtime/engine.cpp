@@ -244,23 +244,20 @@ pam_stats Context::stats() {
     return last_stats;
 }
 
-// Tokens per split-context partition.  Partitions are 16-token tiles; the grid
-// should hold a few thousand waves so all 256 CUs stay busy and ragged rows do
-// not leave a long tail.
-// Split-context partition length (tokens, a multiple of 16).
-//  MFMA kernel: in its persistent form one wave per (row, kv head, partition)
-//  item, eight or twelve waves resident per CU, items dealt in snake order.
-//  Long partitions (up to 1024 tokens) keep a wave's load pipeline full between
-//  per-item start-ups and keep the split-context partials small; they shrink
-//  until there are about three items per resident wave, which bounds the tail
-//  of ragged rows.
-//  VALU kernel: one wave per (row, head group, partition).
+// Split-context partition length (tokens, a multiple of 16) for the forms that
+// use fixed partitions (the stream-K form splits rows itself).
+//  MFMA workgroup form (more than 2048 rows): one workgroup per (row, kv head,
+//  partition).  Long partitions (up to 1024 tokens) keep the waves' load
+//  pipelines full between per-item start-ups and keep the partials small; they
+//  shrink until there are about three items per CU.
+//  VALU kernel: one wave per (row, head group, partition); a few thousand waves
+//  keep all CUs busy.
 int32_t Context::choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma) {
     if (max_tiles <= 0) return 16;
     if (part_tokens_override > 0) return std::max<int32_t>(16, part_tokens_override / 16 * 16);
     if (mfma) {
         int64_t tpp = 64;
-        while (tpp > 8 && items_per_part * ceil_div(max_tiles, tpp) < 3 * 8 * (int64_t)cus_) tpp /= 2;
+        while (tpp > 16 && items_per_part * ceil_div(max_tiles, tpp) < 3 * (int64_t)cus_) tpp /= 2;
         if (tpp >= max_tiles) tpp = max_tiles;
         return (int32_t)(tpp * 16);
     }
