@@ -95,21 +95,17 @@ struct KvTraits<uint8_t> {
 
 // ------------------------------------------------------------------ MFMA body
 
-// e4m3 byte -> binary16 carrying the same sign / exponent / mantissa bits, i.e.
-// the exact e4m3 value times 2^-8 (subnormal codes land on f16 subnormals).
-// Two bytes per 32-bit word: perm places them in the high byte of each half,
-// then the magnitude moves down one bit under the sign.
-__device__ __forceinline__ uint32_t e4m3x2_to_f16x2_bits(uint32_t w, uint32_t sel) {
-    const uint32_t t = __builtin_amdgcn_perm(0u, w, sel);
-    return (t & 0x80008000u) | ((t >> 1) & 0x3F803F80u);
-}
+// e4m3 bytes -> their exact binary16 values, two bytes per
+// v_cvt_scalef32_pk_f16_fp8 (scale 1.0; word_sel picks bytes 0-1 or 2-3).  The
+// hardware's OCP e4m3 decoding equals the reference's dequant_fp8 table
+// (kernels.metal:553-562) for every code except 0x7F / 0xFF, which the
+// reference's quantiser never writes (it saturates at 0x7E).
 __device__ __forceinline__ f16x8 e4m3x8_to_f16x8(uint32_t w0, uint32_t w1) {
-    uint4 h;
-    h.x = e4m3x2_to_f16x2_bits(w0, 0x010C000Cu);
-    h.y = e4m3x2_to_f16x2_bits(w0, 0x030C020Cu);
-    h.z = e4m3x2_to_f16x2_bits(w1, 0x010C000Cu);
-    h.w = e4m3x2_to_f16x2_bits(w1, 0x030C020Cu);
-    return __builtin_bit_cast(f16x8, h);
+    const auto a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+    const auto b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+    const auto c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+    const auto d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+    return (f16x8){(f16)a[0], (f16)a[1], (f16)b[0], (f16)b[1], (f16)c[0], (f16)c[1], (f16)d[0], (f16)d[1]};
 }
 
 // Waves per workgroup of the MFMA kernels: in the workgroup form they split one
@@ -297,9 +293,9 @@ __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, 
             if constexpr (!kFp8) {
                 *reinterpret_cast<u32x4 *>(d) = raw[u];
             } else if constexpr (kTileScale) {
-                // exact code value * 2^-8, times scale * 2^8 in one binary16
-                // multiply: the reference's half dequantisation (two half products,
-                // the second a power of two) up to results below the normal range
+                // exact code value times the block scale in one binary16 multiply:
+                // the reference's half dequantisation (two half products, the second
+                // a power of two) up to results below the normal range
                 const f16x8 s8 = (f16x8)tile_scale;
                 *reinterpret_cast<f16x8 *>(d) = e4m3x8_to_f16x8(raw[u][0], raw[u][1]) * s8;
                 *reinterpret_cast<f16x8 *>(d + 8) = e4m3x8_to_f16x8(raw[u][2], raw[u][3]) * s8;
@@ -330,12 +326,12 @@ __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, 
         // keep the scheduler from hoisting the next tile's work (and with it the
         // wait for its loads) into this one
         __builtin_amdgcn_sched_barrier(0);
-        // per-tile scales (a tile inside one block has one scale pair); 2^8 undoes
-        // the widening shift.  Otherwise each row is dequantised on staging.
+        // per-tile scales (a tile inside one block has one scale pair); otherwise
+        // each row is dequantised on staging
         f16 ks = (f16)1.0f, vs = (f16)1.0f;
         if constexpr (kTileScale) {
-            ks = (f16)((float)bits_to_f16(t.ksb[0]) * 256.0f);
-            vs = (f16)((float)bits_to_f16(t.vsb[0]) * 256.0f);
+            ks = bits_to_f16(t.ksb[0]);
+            vs = bits_to_f16(t.vsb[0]);
         }
         stage_rows(t.k, t.ksb, ks, kt, KL);
         stage_rows(t.v, t.vsb, vs, vt, VL);
