@@ -148,9 +148,10 @@ struct MfmaShape {
     static constexpr int VL = HD + 16;                        // V row in LDS (halves)
     static constexpr int NW = kMfmaWaves;
     // register tiles in flight per wave, and resident workgroups per CU the
-    // registers allow (f16 rows need twice the registers of e4m3 rows)
+    // registers allow (measured on gfx950: d = 128 runs best at two workgroups
+    // per CU for both f16 and e4m3; a third e4m3 workgroup forces spills)
     static constexpr int DEPTH = (sizeof(KV) == 2 && HD <= 128) ? 3 : 2;
-    static constexpr int OCC = HD >= 256 ? 1 : ((sizeof(KV) == 2 && HD == 128) ? 2 : 3);
+    static constexpr int OCC = HD >= 256 ? 1 : (HD == 128 ? 2 : 3);
     static constexpr int WT = 16 * (KL + VL);                 // halves of one wave's K and V tiles
     static constexpr int kSmemBytes = NW * WT * 2 > NW * 16 * HD * 4 ? NW * WT * 2 : NW * 16 * HD * 4;
     static_assert(64 % LPR == 0 && 16 % RPI == 0, "token rows must tile the wave");
