@@ -36,7 +36,11 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p, int64_t 
     }
 }
 
-// One workgroup per touched (sequence, logical block).
+// One workgroup per touched (sequence, logical block).  The block's new tokens
+// are consecutive rows of the input and consecutive slots of the physical block,
+// so both passes (the max for the scale rule, then the quantisation) stream one
+// contiguous range: 8 halves in, 8 codes out per thread and step when the rows
+// are 16-byte multiples, one element at a time otherwise.
 __global__ __launch_bounds__(256) void kv_append_fp8_kernel(AppendBatchParams p, int32_t first_lb,
                                                             int32_t single_offset) {
     int seq, lb;
@@ -57,13 +61,33 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(AppendBatchParams p,
     if (t0 < 0) t0 = 0;
     if (t1 > n_tok) t1 = n_tok;
     const int32_t phys = p.block_tables[(int64_t)seq * p.bt_stride + lb];
+    // input elements [t0 * row, t1 * row) -> pool elements from the slot of t0
+    const int64_t n = (t1 - t0) * row;
+    const f16 *kin = static_cast<const f16 *>(p.keys) + (tok_base + t0) * row;
+    const f16 *vin = static_cast<const f16 *>(p.values) + (tok_base + t0) * row;
+    const int64_t dst0 = ((int64_t)phys * bs + (off + t0 - (int64_t)lb * bs)) * row;
+    uint8_t *kp = static_cast<uint8_t *>(p.k_pool) + dst0;
+    uint8_t *vp = static_cast<uint8_t *>(p.v_pool) + dst0;
+    // 16-byte input rows and aligned buffers: every token row keeps the alignment
+    const bool vec = (row % 8) == 0 && (((uintptr_t)p.keys | (uintptr_t)p.values) & 15) == 0 &&
+                     (((uintptr_t)p.k_pool | (uintptr_t)p.v_pool) & 7) == 0;
 
-    const f16 *kin = static_cast<const f16 *>(p.keys) + tok_base * row;
-    const f16 *vin = static_cast<const f16 *>(p.values) + tok_base * row;
     float mk = 0.0f, mv = 0.0f;
-    for (int64_t e = t0 * row + threadIdx.x; e < t1 * row; e += blockDim.x) {
-        mk = fmaxf(mk, fabsf((float)kin[e]));
-        mv = fmaxf(mv, fabsf((float)vin[e]));
+    if (vec) {
+        for (int64_t e = (int64_t)threadIdx.x * 8; e < n; e += (int64_t)blockDim.x * 8) {
+            const f16x8 a = *reinterpret_cast<const f16x8 *>(kin + e);
+            const f16x8 b = *reinterpret_cast<const f16x8 *>(vin + e);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                mk = fmaxf(mk, fabsf((float)a[i]));
+                mv = fmaxf(mv, fabsf((float)b[i]));
+            }
+        }
+    } else {
+        for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
+            mk = fmaxf(mk, fabsf((float)kin[e]));
+            mv = fmaxf(mv, fabsf((float)vin[e]));
+        }
     }
     mk = wave_max_xor(mk, 1, 64);
     mv = wave_max_xor(mv, 1, 64);
@@ -86,14 +110,24 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(AppendBatchParams p,
     }
     __syncthreads();
     const f16 ks = bits_to_f16(scales[0]), vs = bits_to_f16(scales[1]);
-    uint8_t *kp = static_cast<uint8_t *>(p.k_pool);
-    uint8_t *vp = static_cast<uint8_t *>(p.v_pool);
-    for (int64_t e = t0 * row + threadIdx.x; e < t1 * row; e += blockDim.x) {
-        const int64_t t = e / row, i = e % row;
-        const int64_t pos = off + t;
-        const int64_t dst = ((int64_t)phys * bs + pos % bs) * row + i;
-        kp[dst] = (uint8_t)fp8_quantize(kin[e], ks);
-        vp[dst] = (uint8_t)fp8_quantize(vin[e], vs);
+    if (vec) {
+        for (int64_t e = (int64_t)threadIdx.x * 8; e < n; e += (int64_t)blockDim.x * 8) {
+            const f16x8 a = *reinterpret_cast<const f16x8 *>(kin + e);
+            const f16x8 b = *reinterpret_cast<const f16x8 *>(vin + e);
+            uint32_t kw[2] = {0u, 0u}, vw[2] = {0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                kw[i >> 2] |= fp8_quantize(a[i], ks) << (8 * (i & 3));
+                vw[i >> 2] |= fp8_quantize(b[i], vs) << (8 * (i & 3));
+            }
+            *reinterpret_cast<uint2 *>(kp + e) = make_uint2(kw[0], kw[1]);
+            *reinterpret_cast<uint2 *>(vp + e) = make_uint2(vw[0], vw[1]);
+        }
+    } else {
+        for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
+            kp[e] = (uint8_t)fp8_quantize(kin[e], ks);
+            vp[e] = (uint8_t)fp8_quantize(vin[e], vs);
+        }
     }
     if (threadIdx.x == 0) {
         p.k_scale[phys] = scales[0];
