@@ -505,11 +505,8 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
     mfma_item<KV, HD, BLK>(p, blockIdx.z, blockIdx.x, blockIdx.y, smem, sm_ml);
 }
 
-// Agent-scope (sc1) 16- and 8-byte accesses to the stream-K partials: stores
-// write through the XCD's L2 and loads do not hit a stale line there, so a
-// partial written on one XCD can be merged on another without a whole-L2
-// writeback.  Offsets are bytes from the partial area's base (< 2 GiB).
-constexpr int kSc1 = 16;  // cache-policy bits of an agent-scope access on gfx950
+// Stream-K partials are accessed with kSc1 (agent scope); offsets are bytes
+// from the partial area's base (< 2 GiB).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const AttnParams &p) {
     return __builtin_amdgcn_make_buffer_rsrc(p.part_o, 0, (int)p.part_bytes, 0x00020000);
 }

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace pam {
 
 enum DType : int32_t { kF32 = 0, kF16 = 1, kFP8 = 2 };
@@ -46,10 +48,17 @@ struct AttnParams {
     int32_t max_parts;
     int32_t heads_per_wave;    // VALU kernel: query heads handled by one wave
     float scale_log2;          // log2(e) / sqrt(d)
-    // dense prefill kernel: one entry per sequence chunk {bt_row, q_offset, len, row_base}
-    const int4 *chunks;
-    int32_t num_chunks;
-    int32_t max_chunk_len;
+    // dense prefill work list (prefill_split_plan): three int4 per segment
+    //   {bt_row, q_offset, len, row_base} of its chunk, {kv head, first token,
+    //   t_lo, t_hi} (key tiles), {slot0, piece, pieces, 0},
+    // a [first, last) segment range per workgroup, and the partial slots and
+    // counters of items split over several workgroups
+    const int4 *pf_work;
+    const int2 *pf_range;
+    float *pf_part;
+    int32_t *pf_count;         // one per slot, all 0 between launches
+    uint32_t pf_part_bytes;
+    int32_t pf_groups;         // workgroups of the launch
 };
 
 // Paged attention over rows (decode / prefill-as-rows / ragged).  Chooses the
@@ -134,6 +143,19 @@ hipError_t launch_stream_copy(const void *src, void *dst, size_t bytes, int bloc
 
 // Dense chunked-prefill (MFMA, f16): rows [q_offset, q_offset + T) of one sequence.
 hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream);
+// Work list of the dense prefill kernel for chunks {bt_row, q_offset, len,
+// row_base} (host memory).  An item is (chunk, kv head, block of 256 / G query rows)
+// over its key tiles; items are cut into segments so that the `groups`
+// workgroups get about the same number of tiles.  Fills p.pf_groups; the caller
+// stages `work` and `range` to the device and provides `slots` partial slots of
+// kPrefillSlotBytes and as many zeroed counters.
+struct PrefillSplit {
+    std::vector<int4> work;
+    std::vector<int2> range;
+    int64_t slots = 0;
+};
+constexpr int64_t kPrefillSlotBytes = 8 * 64 * (64 + 2) * 4;  // one workgroup's O^T, m, l
+void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t groups, PrefillSplit &out);
 bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size);
 
 }  // namespace pam

@@ -18,6 +18,12 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Cache-policy bits of an agent-scope buffer access on gfx950 (sc1): stores
+// write through the XCD's L2 and loads do not hit a stale line there, so data
+// written on one XCD can be read on another within a launch without a
+// whole-L2 writeback.
+constexpr int kSc1 = 16;
+
 __device__ __forceinline__ f16 bits_to_f16(uint16_t b) { return __builtin_bit_cast(f16, b); }
 __device__ __forceinline__ uint16_t f16_to_bits(f16 h) { return __builtin_bit_cast(uint16_t, h); }
 

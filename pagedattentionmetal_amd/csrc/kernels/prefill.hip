@@ -27,6 +27,10 @@
 // Softmax keeps a per-row reference max that is only raised (and O rescaled)
 // when some score exceeds it by more than 2^8, so P is bounded by 2^8 and goes
 // to the MFMA in f16; the common case needs no cross-lane reduction.
+#include <algorithm>
+#include <functional>
+#include <queue>
+
 #include "kernels.h"
 #include "pam_device.h"
 
@@ -90,337 +94,445 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
     const int G = p.num_heads / p.num_kv_heads, H = p.num_heads;
     const int tok_per_wg = ROWS / G;
-    // Workgroup -> (chunk, kv head, token block).  Workgroups are dispatched to
-    // the 8 XCDs round-robin by id, and each XCD has its own L2: all token
-    // blocks of one (chunk, kv head) get ids of one residue mod 8, so the K/V
-    // rows they share are fetched from HBM into one L2 only.  Chunks arrive
-    // longest first; within a group the latest (heaviest) token blocks go first.
-    const int nx = (p.max_chunk_len + tok_per_wg - 1) / tok_per_wg;
-    const int xcd = blockIdx.x & (kXcds - 1), r = blockIdx.x / kXcds;
-    const int grp = xcd + kXcds * (r / nx);
-    if (grp >= p.num_chunks * p.num_kv_heads) return;
-    const int4 ch = p.chunks[grp / p.num_kv_heads];  // {bt_row, q_offset, len, row_base}
-    const int kvh = grp % p.num_kv_heads;
-    const int tok0 = (nx - 1 - r % nx) * tok_per_wg;
-    if (tok0 >= ch.z) return;
-    const int32_t *bt = p.block_tables + (int64_t)ch.x * p.bt_stride;
+    // This workgroup's segments of the work list (prefill_split_plan): each is
+    // an item (chunk, kv head, block of 256 / G tokens) over key tiles
+    // [t_lo, t_hi), either all the item's tiles or one piece of them.
+    const int2 rg = p.pf_range[blockIdx.x];
+    __shared__ int32_t merge_flag;
     const int bsh = __builtin_ctz(p.block_size), bsm = p.block_size - 1;  // block_size is a power of two
-    const int kv_len = ch.y + ch.z;
-    const int ws = p.window > 0 ? (kv_len > p.window ? kv_len - p.window : 0) : 0;
-    const int tok_end = tok0 + tok_per_wg < ch.z ? tok0 + tok_per_wg : ch.z;
-    const int key_end = p.causal ? ch.y + tok_end : kv_len;  // exclusive
-    const int t_lo = ws / KT, t_hi = (key_end + KT - 1) / KT;
-    // tiles [full_lo, full_hi) need no mask for any row of the workgroup
-    const int full_lo = (ws + KT - 1) / KT;
-    int full_hi = kv_len / KT;
-    if (p.causal) full_hi = min(full_hi, (ch.y + tok0 + 1) / KT);
-
-    // this lane's query rows: column n of each of the wave's 32-row blocks
-    int my_tok[RB], my_head[RB], qpos[RB];
-    bool row_ok[RB];
-    f16x8 qv[RB][DC];
-#pragma unroll
-    for (int b = 0; b < RB; b++) {
-        const int rr = (wave * RB + b) * 32 + n;
-        my_tok[b] = tok0 + rr / G;
-        my_head[b] = rr % G;
-        row_ok[b] = my_tok[b] < tok_end;
-        qpos[b] = ch.y + my_tok[b];
-        const f16 *qp = static_cast<const f16 *>(p.q) +
-                        ((int64_t)(ch.w + (row_ok[b] ? my_tok[b] : tok0)) * H + kvh * G + my_head[b]) * HD + 8 * h;
-#pragma unroll
-        for (int c = 0; c < DC; c++) qv[b][c] = *reinterpret_cast<const f16x8 *>(qp + 16 * c);
+    // descriptors of the next segment are requested while this one runs
+    int4 nx_ch = make_int4(0, 0, 0, 0), nx_wa = nx_ch, nx_wb = nx_ch;
+    if (rg.x < rg.y) {
+        nx_ch = p.pf_work[3 * rg.x];
+        nx_wa = p.pf_work[3 * rg.x + 1];
+        nx_wb = p.pf_work[3 * rg.x + 2];
     }
-
-    // staging map: thread -> piece tid % 16 of keys tid / 16 (+ THREADS / 16)
-    // (16 lanes read one key row's 256 contiguous bytes)
-    const int my_piece = tid % PIECES, my_key = tid / PIECES;
-    const uint32_t row_stride = (uint32_t)(p.num_kv_heads * HD);  // halves per pool row (< 2^32)
-    const f16 *kpool = static_cast<const f16 *>(p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
-    const f16 *vpool = static_cast<const f16 *>(p.v_pool) + (int64_t)kvh * HD + my_piece * 8;
-    // two register sets in flight: a tile's rows are loaded two iterations
-    // before they are written to LDS
-    f16x8 kra[KPT], vra[KPT], krb[KPT], vrb[KPT];
-    int blk0 = 0;  // first block of the block-table segment held in bt_lds
-    // pool row of this thread's key(s) of a tile, then the loads from it
-    auto lookup = [&](int tile, uint32_t(&slot)[KPT]) {
-#pragma unroll
-        for (int i = 0; i < KPT; i++) {
-            int j = tile * KT + my_key + i * KEYS_PER_PASS;
-            // keys outside [ws, kv_len) read the nearest key inside instead: finite
-            // data whose probability is zero after masking (and a block-table entry
-            // of the current segment)
-            j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
-            slot[i] = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
+    int32_t pre_bt = 0;    // a block-table entry of the next segment, loaded ahead
+    bool pre_ok = false;
+    for (int sgi = rg.x; sgi < rg.y; sgi++) {
+        const bool use_pre = pre_ok;
+        pre_ok = false;
+        const int4 ch = nx_ch;  // {bt_row, q_offset, len, row_base}
+        const int4 wa = nx_wa;  // {kv head, first token, t_lo, t_hi}
+        const int4 wb = nx_wb;  // {slot0, piece, pieces, 0}
+        if (sgi + 1 < rg.y) {
+            nx_ch = p.pf_work[3 * sgi + 3];
+            nx_wa = p.pf_work[3 * sgi + 4];
+            nx_wb = p.pf_work[3 * sgi + 5];
         }
-    };
-    auto load = [&](const uint32_t(&slot)[KPT], f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
-#pragma unroll
-        for (int i = 0; i < KPT; i++) {
-            const uint64_t off = (uint64_t)slot[i] * row_stride;
-            kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off);
-            vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off);
-        }
-    };
-    auto fetch = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
-        uint32_t slot[KPT];
-        lookup(tile, slot);
-        load(slot, kreg, vreg);
-    };
-    int k_st[KPT], v_st[KPT];
-#pragma unroll
-    for (int i = 0; i < KPT; i++) {
-        k_st[i] = k_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
-        v_st[i] = v_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
-    }
-    auto stage = [&](int buf, const f16x8(&kreg)[KPT], const f16x8(&vreg)[KPT]) {
-#pragma unroll
-        for (int i = 0; i < KPT; i++) {
-            *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st[i]]) = kreg[i];
-            *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st[i]]) = vreg[i];
-        }
-    };
+        const int kvh = wa.x, tok0 = wa.y;
+        const int32_t *bt = p.block_tables + (int64_t)ch.x * p.bt_stride;
+        const int kv_len = ch.y + ch.z;
+        const int ws = p.window > 0 ? (kv_len > p.window ? kv_len - p.window : 0) : 0;
+        const int tok_end = tok0 + tok_per_wg < ch.z ? tok0 + tok_per_wg : ch.z;
+        const int t_lo = wa.z, t_hi = wa.w;
+        // keys at or past key_hi belong to later pieces (or do not exist)
+        const int key_hi = min(kv_len, t_hi * KT);
+        // tiles [full_lo, full_hi) need no mask for any row of the workgroup
+        const int full_lo = (ws + KT - 1) / KT;
+        int full_hi = min(kv_len / KT, t_hi);
+        if (p.causal) full_hi = min(full_hi, (ch.y + tok0 + 1) / KT);
 
-    // S^T: A operand of chunk c = K[key n][16c + 8h .. +7], shared by the row blocks
-    const int k_rd = k_lds_at(n, h);
-    auto score = [&](int buf, f32x16(&sc)[RB][KH]) {
-        const f16 *kt = k_lds[buf];
-#pragma unroll
-        for (int e = 0; e < KH; e++) {
-#pragma unroll
-            for (int b = 0; b < RB; b++) sc[b][e] = (f32x16)0.0f;
-#pragma unroll
-            for (int c = 0; c < DC; c++) {
-                const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * kPrefillKL + 16 * c]);
-#pragma unroll
-                for (int b = 0; b < RB; b++)
-                    sc[b][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[b][c], sc[b][e], 0, 0, 0);
-            }
-        }
-    };
-    // V^T operand of dim tile dt, key chunk c: lane (o = lane % 16 of its 16-lane
-    // group, half hh = (lane / 16) % 2, h) reads row 16c + 4h + 8jj + o/4
-    // (jj = 0, 1) at dims 32dt + 16hh + 4(o%4): two transposed loads give keys
-    // 16c + 4h + {0..3, 8..11} of dim 32dt + 16hh + o, the P slot order
-    int v_rd[DT];
-    {
-        const int o = lane & 15, hh = (lane >> 4) & 1;
-        const int row = 4 * h + (o >> 2);
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-            v_rd[dt] = v_lds_at(row, 4 * dt + 2 * hh + ((o & 3) >> 1)) + 4 * (o & 1);
-    }
-
-    float m_use[RB], l_run[RB], lmax[RB];
-    f32x16 o[RB][DT];
-#pragma unroll
-    for (int b = 0; b < RB; b++) {
-        m_use[b] = -INFINITY;
-        l_run[b] = 0.0f;
-        lmax[b] = -INFINITY;
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[b][dt] = (f32x16)0.0f;
-    }
-    const float sl2 = p.scale_log2;
-    const f16x2 ones = {(f16)1.0f, (f16)1.0f};
-
-    // accumulator register r of block e holds key 32e + 8(r/4) + 4h + r%4 of the tile
-    auto prepare = [&](int tile, f32x16(&sc)[RB][KH]) -> bool {
-        bool need = false;
+        // this lane's query rows: column n of each of the wave's 32-row blocks
+        int my_tok[RB], my_head[RB], qpos[RB];
+        bool row_ok[RB];
+        f16x8 qv[RB][DC];
 #pragma unroll
         for (int b = 0; b < RB; b++) {
-            if (!(tile >= full_lo && tile < full_hi)) {
+            const int rr = (wave * RB + b) * 32 + n;
+            my_tok[b] = tok0 + rr / G;
+            my_head[b] = rr % G;
+            row_ok[b] = my_tok[b] < tok_end;
+            qpos[b] = ch.y + my_tok[b];
+            const f16 *qp = static_cast<const f16 *>(p.q) +
+                            ((int64_t)(ch.w + (row_ok[b] ? my_tok[b] : tok0)) * H + kvh * G + my_head[b]) * HD + 8 * h;
 #pragma unroll
-                for (int e = 0; e < KH; e++)
+            for (int c = 0; c < DC; c++) qv[b][c] = *reinterpret_cast<const f16x8 *>(qp + 16 * c);
+        }
+
+        // staging map: thread -> piece tid % 16 of keys tid / 16 (+ THREADS / 16)
+        // (16 lanes read one key row's 256 contiguous bytes)
+        const int my_piece = tid % PIECES, my_key = tid / PIECES;
+        const uint32_t row_stride = (uint32_t)(p.num_kv_heads * HD);  // halves per pool row (< 2^32)
+        const f16 *kpool = static_cast<const f16 *>(p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
+        const f16 *vpool = static_cast<const f16 *>(p.v_pool) + (int64_t)kvh * HD + my_piece * 8;
+        // two register sets in flight: a tile's rows are loaded two iterations
+        // before they are written to LDS
+        f16x8 kra[KPT], vra[KPT], krb[KPT], vrb[KPT];
+        int blk0 = 0;  // first block of the block-table segment held in bt_lds
+        // pool row of this thread's key(s) of a tile, then the loads from it
+        auto lookup = [&](int tile, uint32_t(&slot)[KPT]) {
 #pragma unroll
-                    for (int r2 = 0; r2 < 16; r2++) {
-                        const int j = tile * KT + 32 * e + 8 * (r2 >> 2) + 4 * h + (r2 & 3);
-                        const bool ok = j >= ws && j < kv_len && (!p.causal || j <= qpos[b]);
-                        sc[b][e][r2] = ok ? sc[b][e][r2] : -INFINITY;
-                    }
+            for (int i = 0; i < KPT; i++) {
+                int j = tile * KT + my_key + i * KEYS_PER_PASS;
+                // keys outside [ws, kv_len) read the nearest key inside instead: finite
+                // data whose probability is zero after masking (and a block-table entry
+                // of the current segment)
+                j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
+                slot[i] = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
             }
-            float mx = -INFINITY;
+        };
+        auto load = [&](const uint32_t(&slot)[KPT], f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+#pragma unroll
+            for (int i = 0; i < KPT; i++) {
+                const uint64_t off = (uint64_t)slot[i] * row_stride;
+                kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off);
+                vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off);
+            }
+        };
+        auto fetch = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+            uint32_t slot[KPT];
+            lookup(tile, slot);
+            load(slot, kreg, vreg);
+        };
+        int k_st[KPT], v_st[KPT];
+#pragma unroll
+        for (int i = 0; i < KPT; i++) {
+            k_st[i] = k_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
+            v_st[i] = v_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
+        }
+        auto stage = [&](int buf, const f16x8(&kreg)[KPT], const f16x8(&vreg)[KPT]) {
+#pragma unroll
+            for (int i = 0; i < KPT; i++) {
+                *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st[i]]) = kreg[i];
+                *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st[i]]) = vreg[i];
+            }
+        };
+
+        // S^T: A operand of chunk c = K[key n][16c + 8h .. +7], shared by the row blocks
+        const int k_rd = k_lds_at(n, h);
+        auto score = [&](int buf, f32x16(&sc)[RB][KH]) {
+            const f16 *kt = k_lds[buf];
 #pragma unroll
             for (int e = 0; e < KH; e++) {
-                mx = vmax3(mx, sc[b][e][0], sc[b][e][1]);
 #pragma unroll
-                for (int r2 = 2; r2 < 16; r2 += 2) mx = vmax3(mx, sc[b][e][r2], sc[b][e][r2 + 1]);
+                for (int b = 0; b < RB; b++) sc[b][e] = (f32x16)0.0f;
+#pragma unroll
+                for (int c = 0; c < DC; c++) {
+                    const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * kPrefillKL + 16 * c]);
+#pragma unroll
+                    for (int b = 0; b < RB; b++)
+                        sc[b][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[b][c], sc[b][e], 0, 0, 0);
+                }
             }
-            lmax[b] = mx * sl2;
-            need |= lmax[b] > m_use[b] + kRescaleLog2;
+        };
+        // V^T operand of dim tile dt, key chunk c: lane (o = lane % 16 of its 16-lane
+        // group, half hh = (lane / 16) % 2, h) reads row 16c + 4h + 8jj + o/4
+        // (jj = 0, 1) at dims 32dt + 16hh + 4(o%4): two transposed loads give keys
+        // 16c + 4h + {0..3, 8..11} of dim 32dt + 16hh + o, the P slot order
+        int v_rd[DT];
+        {
+            const int o = lane & 15, hh = (lane >> 4) & 1;
+            const int row = 4 * h + (o >> 2);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+                v_rd[dt] = v_lds_at(row, 4 * dt + 2 * hh + ((o & 3) >> 1)) + 4 * (o & 1);
         }
-        return need;
-    };
-    // raise the reference max to the row max (rare: wave-uniform branch)
-    auto rescale = [&]() {
+
+        float m_use[RB], l_run[RB], lmax[RB];
+        f32x16 o[RB][DT];
 #pragma unroll
         for (int b = 0; b < RB; b++) {
-            const float mt = fmaxf(lmax[b], shfl_xor(lmax[b], 32));
-            const float m_new = fmaxf(m_use[b], mt);
-            const float corr = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use[b] - m_new);
-            l_run[b] *= corr;
+            m_use[b] = -INFINITY;
+            l_run[b] = 0.0f;
+            lmax[b] = -INFINITY;
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) o[b][dt] *= corr;
-            m_use[b] = m_new;
+            for (int dt = 0; dt < DT; dt++) o[b][dt] = (f32x16)0.0f;
         }
-    };
+        const float sl2 = p.scale_log2;
+        const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 
-    // Ping-pong schedule.  A tile's work splits into a matrix phase M_t (scores
-    // S(t+1) = K(t+1) Q^T and O += V(t) P(t), with the loads of tile t + 4) and a
-    // vector phase V_t (mask, reference max and exponentials of S(t), row sums,
-    // and the LDS staging of tile t + 2).  Each wave runs
-    // M_-1 V_0 M_0 V_1 M_1 ... with a workgroup barrier after every phase; waves
-    // 4-7 start one barrier late, so each SIMD (waves w and w + 4) has one wave in
-    // a matrix phase while the other is in a vector phase, and the MFMA and VALU
-    // pipes overlap.  LDS ring of 4 tiles: tile t + 2 is written (half by each
-    // wave group) at V_t, K(t) is read at M_t-1 and V(t) at M_t, so a buffer is
-    // rewritten only after both groups have left the phases that read it.
-    constexpr int NBUF = kPrefillBufs;
-    static_assert(NBUF == 4, "the ring schedule above needs 4 tiles");
-    const bool lag = wave >= kPrefillWaves / 2;
-    f32x16 sacc[RB][KH];
-    f16x8 pb[RB][2 * KH];
-    // tiles run in segments whose block-table entries fit in bt_lds (one segment
-    // covers kBtCache * block_size keys, so long contexts only)
-    // (an even number of tiles: the loop below runs tiles in pairs, and a segment
-    // of odd length gets one extra tile past the keys, fully masked)
-    const int seg_tiles = (((kBtCache - 1) << bsh) / KT) & ~1;
-    for (int seg = t_lo; seg < t_hi; seg += seg_tiles) {
-        const int seg_end = min(t_hi, seg + seg_tiles);
-        const int T = (seg_end - seg + 1) & ~1;
-        blk0 = (seg * KT) >> bsh;
-        const int nblk = (((min(seg_end * KT, kv_len) - 1) >> bsh) - blk0) + 1;
-        __syncthreads();  // previous segment done with bt_lds and the ring
-        for (int i = tid; i < nblk; i += THREADS) bt_lds[i] = bt[blk0 + i];
-        __syncthreads();
-        fetch(seg, kra, vra);
-        stage(0, kra, vra);
-        fetch(min(seg + 1, seg_end - 1), kra, vra);
-        stage(1, kra, vra);
-        fetch(min(seg + 2, seg_end - 1), kra, vra);
-        fetch(min(seg + 3, seg_end - 1), krb, vrb);
-        __syncthreads();
-        if (lag) __syncthreads();
-        score(0, sacc);  // M_-1
-        __syncthreads();
-
-        // The vector phase requests the K operands of the next matrix phase (its
-        // tile is staged by then) and looks up the rows the matrix phase will
-        // load; the matrix phase requests its V operands first and runs the score
-        // MFMAs while they arrive.
-        f16x8 ka[KH][DC];
-        uint32_t nslot[KPT];
-        auto vphase = [&](int t, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
-            if (t + 1 < T) {
-                const f16 *kt = k_lds[(t + 1) % NBUF];
-#pragma unroll
-                for (int e = 0; e < KH; e++)
-#pragma unroll
-                    for (int c = 0; c < DC; c++)
-                        ka[e][c] = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * kPrefillKL + 16 * c]);
-            }
-            lookup(min(seg + t + 4, seg_end - 1), nslot);
-            if (__any(prepare(seg + t, sacc))) rescale();
+        // accumulator register r of block e holds key 32e + 8(r/4) + 4h + r%4 of the tile
+        auto prepare = [&](int tile, f32x16(&sc)[RB][KH]) -> bool {
+            bool need = false;
 #pragma unroll
             for (int b = 0; b < RB; b++) {
-                const float mref = m_use[b] == -INFINITY ? 0.0f : m_use[b];
+                if (!(tile >= full_lo && tile < full_hi)) {
 #pragma unroll
-                for (int e = 0; e < KH; e++)
+                    for (int e = 0; e < KH; e++)
 #pragma unroll
-                    for (int r2 = 0; r2 < 16; r2++)
-                        pb[b][2 * e + (r2 >> 3)][r2 & 7] =
-                            (f16)__builtin_amdgcn_exp2f(fmaf(sacc[b][e][r2], sl2, -mref));
-                // row sum of the f16 probabilities the MFMA consumes
-                float ps = l_run[b];
-#pragma unroll
-                for (int k = 0; k < 8 * KH; k++) {
-                    const f16x2 pr = {pb[b][k >> 2][2 * (k & 3)], pb[b][k >> 2][2 * (k & 3) + 1]};
-                    ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
+                        for (int r2 = 0; r2 < 16; r2++) {
+                            const int j = tile * KT + 32 * e + 8 * (r2 >> 2) + 4 * h + (r2 & 3);
+                            const bool ok = j >= ws && j < key_hi && (!p.causal || j <= qpos[b]);
+                            sc[b][e][r2] = ok ? sc[b][e][r2] : -INFINITY;
+                        }
                 }
-                l_run[b] = ps;
-            }
-            // P and the row sums are complete here: without this the compiler
-            // sinks the exponentials past the barrier into the matrix phase
-#pragma unroll
-            for (int b = 0; b < RB; b++) {
-#pragma unroll
-                for (int c = 0; c < 2 * KH; c++) asm volatile("" : "+v"(pb[b][c]));
-                asm volatile("" : "+v"(l_run[b]));
-            }
-            stage((t + 2) % NBUF, kreg, vreg);  // tile t + 2, fetched at M_t-2
-        };
-        auto mphase = [&](int t, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
-            const f16 *vt = v_lds[t % NBUF];
-            f16x8 va[2 * KH][DT];
-#pragma unroll
-            for (int c = 0; c < 2 * KH; c++)
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) {
-                    const f16x4 lo = lds_read_tr16(vt + v_rd[dt] + 16 * c * kPrefillVL);
-                    const f16x4 hi = lds_read_tr16(vt + v_rd[dt] + (16 * c + 8) * kPrefillVL);
-                    va[c][dt] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                }
-            if (t + 1 < T) {
+                float mx = -INFINITY;
 #pragma unroll
                 for (int e = 0; e < KH; e++) {
+                    mx = vmax3(mx, sc[b][e][0], sc[b][e][1]);
 #pragma unroll
-                    for (int b = 0; b < RB; b++) sacc[b][e] = (f32x16)0.0f;
+                    for (int r2 = 2; r2 < 16; r2 += 2) mx = vmax3(mx, sc[b][e][r2], sc[b][e][r2 + 1]);
+                }
+                lmax[b] = mx * sl2;
+                need |= lmax[b] > m_use[b] + kRescaleLog2;
+            }
+            return need;
+        };
+        // raise the reference max to the row max (rare: wave-uniform branch)
+        auto rescale = [&]() {
 #pragma unroll
-                    for (int c = 0; c < DC; c++)
+            for (int b = 0; b < RB; b++) {
+                const float mt = fmaxf(lmax[b], shfl_xor(lmax[b], 32));
+                const float m_new = fmaxf(m_use[b], mt);
+                const float corr = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use[b] - m_new);
+                l_run[b] *= corr;
 #pragma unroll
-                        for (int b = 0; b < RB; b++)
-                            sacc[b][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[e][c], qv[b][c], sacc[b][e], 0, 0, 0);
+                for (int dt = 0; dt < DT; dt++) o[b][dt] *= corr;
+                m_use[b] = m_new;
+            }
+        };
+
+        // Ping-pong schedule.  A tile's work splits into a matrix phase M_t (scores
+        // S(t+1) = K(t+1) Q^T and O += V(t) P(t), with the loads of tile t + 4) and a
+        // vector phase V_t (mask, reference max and exponentials of S(t), row sums,
+        // and the LDS staging of tile t + 2).  Each wave runs
+        // M_-1 V_0 M_0 V_1 M_1 ... with a workgroup barrier after every phase; waves
+        // 4-7 start one barrier late, so each SIMD (waves w and w + 4) has one wave in
+        // a matrix phase while the other is in a vector phase, and the MFMA and VALU
+        // pipes overlap.  LDS ring of 4 tiles: tile t + 2 is written (half by each
+        // wave group) at V_t, K(t) is read at M_t-1 and V(t) at M_t, so a buffer is
+        // rewritten only after both groups have left the phases that read it.
+        constexpr int NBUF = kPrefillBufs;
+        static_assert(NBUF == 4, "the ring schedule above needs 4 tiles");
+        const bool lag = wave >= kPrefillWaves / 2;
+        f32x16 sacc[RB][KH];
+        f16x8 pb[RB][2 * KH];
+        // tiles run in segments whose block-table entries fit in bt_lds (one segment
+        // covers kBtCache * block_size keys, so long contexts only)
+        // (an even number of tiles: the loop below runs tiles in pairs, and a segment
+        // of odd length gets one extra tile past the keys, fully masked)
+        const int seg_tiles = (((kBtCache - 1) << bsh) / KT) & ~1;
+        for (int seg = t_lo; seg < t_hi; seg += seg_tiles) {
+            const int seg_end = min(t_hi, seg + seg_tiles);
+            const int T = (seg_end - seg + 1) & ~1;
+            blk0 = (seg * KT) >> bsh;
+            const int nblk = (((min(seg_end * KT, kv_len) - 1) >> bsh) - blk0) + 1;
+            __syncthreads();  // previous segment done with bt_lds and the ring
+            int i0 = tid;
+            if (seg == t_lo && use_pre) {  // entries loaded during the previous segment
+                if (tid < nblk) bt_lds[tid] = pre_bt;
+                i0 += THREADS;
+            }
+            for (int i = i0; i < nblk; i += THREADS) bt_lds[i] = bt[blk0 + i];
+            __syncthreads();
+            // the first four tiles are requested together
+            {
+                f16x8 kc[KPT], vc[KPT], kd[KPT], vd[KPT];
+                fetch(seg, kra, vra);
+                fetch(min(seg + 1, seg_end - 1), krb, vrb);
+                fetch(min(seg + 2, seg_end - 1), kc, vc);
+                fetch(min(seg + 3, seg_end - 1), kd, vd);
+                stage(0, kra, vra);
+                stage(1, krb, vrb);
+#pragma unroll
+                for (int i = 0; i < KPT; i++) {
+                    kra[i] = kc[i];
+                    vra[i] = vc[i];
+                    krb[i] = kd[i];
+                    vrb[i] = vd[i];
                 }
             }
-            // O^T += V^T P^T, each V^T operand shared by the row blocks
+            __syncthreads();
+            if (lag) __syncthreads();
+            score(0, sacc);  // M_-1
+            __syncthreads();
+            // request the first block-table entries of the workgroup's next segment
+            // (its descriptors arrived long ago); they are stored at its start
+            if (seg == t_lo && sgi + 1 < rg.y) {
+                const int kvn = nx_ch.y + nx_ch.z, tlo_n = nx_wa.z;
+                const int send = min(nx_wa.w, tlo_n + seg_tiles);
+                const int b0 = (tlo_n * KT) >> bsh;
+                const int nb = send > tlo_n ? (((min(send * KT, kvn) - 1) >> bsh) - b0) + 1 : 0;
+                if (tid < nb) pre_bt = p.block_tables[(int64_t)nx_ch.x * p.bt_stride + b0 + tid];
+                pre_ok = true;
+            }
+
+            // The vector phase requests the K operands of the next matrix phase (its
+            // tile is staged by then) and looks up the rows the matrix phase will
+            // load; the matrix phase requests its V operands first and runs the score
+            // MFMAs while they arrive.
+            f16x8 ka[KH][DC];
+            uint32_t nslot[KPT];
+            auto vphase = [&](int t, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+                if (t + 1 < T) {
+                    const f16 *kt = k_lds[(t + 1) % NBUF];
 #pragma unroll
-            for (int c = 0; c < 2 * KH; c++)
+                    for (int e = 0; e < KH; e++)
+#pragma unroll
+                        for (int c = 0; c < DC; c++)
+                            ka[e][c] = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * kPrefillKL + 16 * c]);
+                }
+                lookup(min(seg + t + 4, seg_end - 1), nslot);
+                if (__any(prepare(seg + t, sacc))) rescale();
+#pragma unroll
+                for (int b = 0; b < RB; b++) {
+                    const float mref = m_use[b] == -INFINITY ? 0.0f : m_use[b];
+#pragma unroll
+                    for (int e = 0; e < KH; e++)
+#pragma unroll
+                        for (int r2 = 0; r2 < 16; r2++)
+                            pb[b][2 * e + (r2 >> 3)][r2 & 7] =
+                                (f16)__builtin_amdgcn_exp2f(fmaf(sacc[b][e][r2], sl2, -mref));
+                    // row sum of the f16 probabilities the MFMA consumes
+                    float ps = l_run[b];
+#pragma unroll
+                    for (int k = 0; k < 8 * KH; k++) {
+                        const f16x2 pr = {pb[b][k >> 2][2 * (k & 3)], pb[b][k >> 2][2 * (k & 3) + 1]};
+                        ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
+                    }
+                    l_run[b] = ps;
+                }
+                // P and the row sums are complete here: without this the compiler
+                // sinks the exponentials past the barrier into the matrix phase
+#pragma unroll
+                for (int b = 0; b < RB; b++) {
+#pragma unroll
+                    for (int c = 0; c < 2 * KH; c++) asm volatile("" : "+v"(pb[b][c]));
+                    asm volatile("" : "+v"(l_run[b]));
+                }
+                stage((t + 2) % NBUF, kreg, vreg);  // tile t + 2, fetched at M_t-2
+            };
+            auto mphase = [&](int t, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+                const f16 *vt = v_lds[t % NBUF];
+                f16x8 va[2 * KH][DT];
+#pragma unroll
+                for (int c = 0; c < 2 * KH; c++)
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++) {
+                        const f16x4 lo = lds_read_tr16(vt + v_rd[dt] + 16 * c * kPrefillVL);
+                        const f16x4 hi = lds_read_tr16(vt + v_rd[dt] + (16 * c + 8) * kPrefillVL);
+                        va[c][dt] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    }
+                if (t + 1 < T) {
+#pragma unroll
+                    for (int e = 0; e < KH; e++) {
+#pragma unroll
+                        for (int b = 0; b < RB; b++) sacc[b][e] = (f32x16)0.0f;
+#pragma unroll
+                        for (int c = 0; c < DC; c++)
+#pragma unroll
+                            for (int b = 0; b < RB; b++)
+                                sacc[b][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[e][c], qv[b][c], sacc[b][e], 0, 0, 0);
+                    }
+                }
+                // O^T += V^T P^T, each V^T operand shared by the row blocks
+#pragma unroll
+                for (int c = 0; c < 2 * KH; c++)
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                        for (int b = 0; b < RB; b++)
+                            o[b][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[c][dt], pb[b][c], o[b][dt], 0, 0, 0);
+                // the matrix work stays in this phase (the compiler would otherwise move
+                // the last MFMAs past the barrier)
+#pragma unroll
+                for (int b = 0; b < RB; b++) {
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++) asm volatile("" : "+v"(o[b][dt]));
+#pragma unroll
+                    for (int e = 0; e < KH; e++) asm volatile("" : "+v"(sacc[b][e]));
+                }
+                load(nslot, kreg, vreg);  // tile t + 4
+            };
+            for (int t = 0; t < T; t += 2) {
+                vphase(t, kra, vra);
+                __syncthreads();
+                mphase(t, kra, vra);
+                __syncthreads();
+                vphase(t + 1, krb, vrb);
+                __syncthreads();
+                mphase(t + 1, krb, vrb);
+                __syncthreads();
+            }
+            if (!lag) __syncthreads();
+        }
+
+        // A piece of a split item publishes its state (O^T, reference max and row
+        // sums, per lane) in its slot with write-through stores and counts it;
+        // the workgroup that brings the count to the number of pieces merges all
+        // of them in piece order (the same result whichever workgroup merges),
+        // writes the rows and resets the counter.
+        if (wb.z > 1) {
+            static_assert(kPrefillSlotBytes == (int64_t)kPrefillWaves * 64 * RB * (16 * DT + 2) * 4, "slot size");
+            const __amdgpu_buffer_rsrc_t prs =
+                __builtin_amdgcn_make_buffer_rsrc(p.pf_part, 0, (int)p.pf_part_bytes, 0x00020000);
+            constexpr int NQ = RB * DT * 4;  // 16-byte pieces of O^T per lane
+            auto o_at = [&](int slot, int q) { return (int)(slot * kPrefillSlotBytes) + ((wave * NQ + q) * 64 + lane) * 16; };
+            auto ml_at = [&](int slot, int b) {
+                return (int)(slot * kPrefillSlotBytes) + kPrefillWaves * 64 * NQ * 16 + ((wave * RB + b) * 64 + lane) * 8;
+            };
+            const int mine = wb.x + wb.y;
+#pragma unroll
+            for (int b = 0; b < RB; b++) {
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-                    for (int b = 0; b < RB; b++)
-                        o[b][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[c][dt], pb[b][c], o[b][dt], 0, 0, 0);
-            // the matrix work stays in this phase (the compiler would otherwise move
-            // the last MFMAs past the barrier)
+                    for (int qq = 0; qq < 4; qq++) {
+                        const f32x4 v = {o[b][dt][4 * qq], o[b][dt][4 * qq + 1], o[b][dt][4 * qq + 2], o[b][dt][4 * qq + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(v, prs, o_at(mine, (b * DT + dt) * 4 + qq), 0, kSc1);
+                    }
+                // P was taken against 0 while the reference max is still unset
+                const f32x2 ml = {m_use[b] == -INFINITY ? 0.0f : m_use[b], l_run[b]};
+                __builtin_amdgcn_raw_buffer_store_b64(ml, prs, ml_at(mine, b), 0, kSc1);
+            }
+            // the stores have completed (written through) before the count
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __syncthreads();
+            if (tid == 0)
+                merge_flag = __hip_atomic_fetch_add(p.pf_count + wb.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                             wb.z - 1;
+            __syncthreads();
+            if (!merge_flag) continue;
 #pragma unroll
             for (int b = 0; b < RB; b++) {
+                float M = -INFINITY, den = 0.0f;
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++) asm volatile("" : "+v"(o[b][dt]));
+                for (int dt = 0; dt < DT; dt++) o[b][dt] = (f32x16)0.0f;
+                for (int k = 0; k < wb.z; k++) {
+                    const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(prs, ml_at(wb.x + k, b), 0, kSc1);
+                    f32x4 v[DT * 4];
 #pragma unroll
-                for (int e = 0; e < KH; e++) asm volatile("" : "+v"(sacc[b][e]));
+                    for (int q = 0; q < DT * 4; q++)
+                        v[q] = __builtin_amdgcn_raw_buffer_load_b128(prs, o_at(wb.x + k, b * DT * 4 + q), 0, kSc1);
+                    const float Mn = fmaxf(M, ml[0]);
+                    const float ca = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
+                    const float cb = __builtin_amdgcn_exp2f(ml[0] - Mn);
+                    den = den * ca + ml[1] * cb;
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                        for (int qq = 0; qq < 4; qq++)
+#pragma unroll
+                            for (int r2 = 0; r2 < 4; r2++)
+                                o[b][dt][4 * qq + r2] = o[b][dt][4 * qq + r2] * ca + v[dt * 4 + qq][r2] * cb;
+                    M = Mn;
+                }
+                l_run[b] = den;
             }
-            load(nslot, kreg, vreg);  // tile t + 4
-        };
-        for (int t = 0; t < T; t += 2) {
-            vphase(t, kra, vra);
-            __syncthreads();
-            mphase(t, kra, vra);
-            __syncthreads();
-            vphase(t + 1, krb, vrb);
-            __syncthreads();
-            mphase(t + 1, krb, vrb);
-            __syncthreads();
+            if (tid == 0) __hip_atomic_store(p.pf_count + wb.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        if (!lag) __syncthreads();
-    }
 
-    // finish: l summed over the two lane halves, O / l, rows in range only
+        // finish: l summed over the two lane halves, O / l, rows in range only
 #pragma unroll
-    for (int b = 0; b < RB; b++) {
-        const float l = l_run[b] + shfl_xor(l_run[b], 32);
-        if (!row_ok[b]) continue;
-        // no key in range (window past the row): 0/0, as the reference's m/l bookkeeping gives
-        const float inv = 1.0f / l;
-        f16 *op = static_cast<f16 *>(p.out) + ((int64_t)(ch.w + my_tok[b]) * H + kvh * G + my_head[b]) * HD + 4 * h;
+        for (int b = 0; b < RB; b++) {
+            const float l = l_run[b] + shfl_xor(l_run[b], 32);
+            if (!row_ok[b]) continue;
+            // no key in range (window past the row): 0/0, as the reference's m/l bookkeeping gives
+            const float inv = 1.0f / l;
+            f16 *op = static_cast<f16 *>(p.out) + ((int64_t)(ch.w + my_tok[b]) * H + kvh * G + my_head[b]) * HD + 4 * h;
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++)
+            for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                f16x4 v;
+                for (int q = 0; q < 4; q++) {
+                    f16x4 v;
 #pragma unroll
-                for (int r2 = 0; r2 < 4; r2++) v[r2] = (f16)(o[b][dt][4 * q + r2] * inv);
-                *reinterpret_cast<f16x4 *>(op + 32 * dt + 8 * q) = v;
-            }
+                    for (int r2 = 0; r2 < 4; r2++) v[r2] = (f16)(o[b][dt][4 * q + r2] * inv);
+                    *reinterpret_cast<f16x4 *>(op + 32 * dt + 8 * q) = v;
+                }
+        }
     }
 }
 
@@ -430,15 +542,194 @@ bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int3
 }
 
 hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream) {
-    if (p.chunks == nullptr || p.num_chunks <= 0 || p.max_chunk_len <= 0) return hipErrorInvalidValue;
+    if (p.pf_work == nullptr || p.pf_range == nullptr || p.pf_groups <= 0)
+        return hipErrorInvalidValue;
     const int G = p.num_heads / p.num_kv_heads;
     if (!prefill_mfma_supported(kF16, p.head_dim, G, p.block_size)) return hipErrorInvalidValue;
-    const int tok_per_wg = kPrefillRows / G;
-    const int nx = (p.max_chunk_len + tok_per_wg - 1) / tok_per_wg;
-    const int groups = p.num_chunks * p.num_kv_heads;
-    dim3 grid(kXcds * nx * ((groups + kXcds - 1) / kXcds));
-    hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB>), grid, dim3(64 * kPrefillWaves), 0, stream, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB>), dim3(p.pf_groups), dim3(64 * kPrefillWaves), 0,
+                       stream, p);
     return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ host plan
+//
+// Items are laid out group by group (chunk, kv head), token blocks in order, so
+// the items sharing a group's K/V run side by side.  Costs are in key tiles: a
+// segment costs its tiles plus kSegCost (Q load, block-table segment, ring fill,
+// the masked edge tiles and the output), and a piece of a split item kSplitCost
+// more (publishing and merging partials); these were measured per workgroup
+// with s_memtime on gfx950.  Workgroups are filled in line order up to a common
+// capacity, the smallest with which the line fits `groups` workgroups; an item
+// that does not fit is cut into pieces of an even number of tiles (>= kMinPiece;
+// the tile loop runs pairs).  Consecutive parts of the line go to workgroups of
+// one XCD (workgroup b runs on XCD b mod 8), so a group's pieces share its L2.
+namespace {
+constexpr int kSegCost = 12;
+constexpr int kSplitCost = 4;
+constexpr int kMinPiece = 8;
+
+struct PfItem {
+    int4 chunk;
+    int32_t kvh, tok0, t_lo, t_hi;
+};
+
+// Fills the line at capacity `cap`.  Returns the workgroups used; without `out`
+// it stops at groups + 1 once the line does not fit.
+int32_t pf_fill(const std::vector<PfItem> &items, int64_t cap, int32_t groups, PrefillSplit *out,
+                std::vector<int32_t> *part_first) {
+    int32_t wg = 0;
+    int64_t budget = cap;
+    bool used = false;  // workgroup wg has a segment
+    for (const PfItem &it : items) {
+        const int32_t n = it.t_hi - it.t_lo;
+        int32_t done = 0, pieces = 0;
+        const size_t first_seg = out ? out->work.size() / 3 : 0;
+        for (;;) {
+            const int32_t r = n - done;
+            const bool whole_fits = r <= budget - kSegCost - (pieces ? kSplitCost : 0);
+            if (used && !whole_fits && budget - kSegCost - kSplitCost < kMinPiece) {  // next workgroup
+                wg++;
+                budget = cap;
+                used = false;
+                if (!out && wg >= groups) return groups + 1;
+            }
+            int32_t take = r;
+            int64_t cost = kSegCost + r + (pieces ? kSplitCost : 0);
+            if (cost > budget) {
+                int64_t a = (budget - kSegCost - kSplitCost) & ~(int64_t)1;
+                if (r - a < kMinPiece) a = (r - kMinPiece) & ~1;
+                if (a >= kMinPiece) {
+                    take = (int32_t)a;
+                    cost = kSegCost + kSplitCost + a;
+                }  // else the whole rest, over capacity
+            }
+            if (!used && part_first) (*part_first)[wg] = (int32_t)(first_seg + pieces);
+            if (out) {
+                out->work.push_back(it.chunk);
+                out->work.push_back(make_int4(it.kvh, it.tok0, it.t_lo + done, it.t_lo + done + take));
+                out->work.push_back(make_int4(0, pieces, 1, 0));
+            }
+            used = true;
+            budget -= cost;
+            done += take;
+            pieces++;
+            if (done >= n) break;
+            wg++;
+            budget = cap;
+            used = false;
+            if (!out && wg >= groups) return groups + 1;
+        }
+        if (out && pieces > 1) {
+            for (int32_t k = 0; k < pieces; k++) {
+                int4 &b = out->work[3 * (first_seg + k) + 2];
+                b.x = (int32_t)out->slots;
+                b.z = pieces;
+            }
+            out->slots += pieces;
+        }
+    }
+    return wg + (used ? 1 : 0);
+}
+}  // namespace
+
+void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t groups, PrefillSplit &out) {
+    constexpr int KT = kPrefillKT;
+    const int32_t G = p.num_heads / p.num_kv_heads, tpw = kPrefillRows / G;
+    std::vector<PfItem> items;
+    int64_t total = 0;
+    for (int32_t c = 0; c < n; c++) {
+        const int4 ch = chunks[c];
+        const int32_t kv_len = ch.y + ch.z;
+        const int32_t ws = p.window > 0 ? std::max(0, kv_len - p.window) : 0;
+        for (int32_t kvh = 0; kvh < p.num_kv_heads; kvh++)
+            for (int32_t tok0 = 0; tok0 < ch.z; tok0 += tpw) {
+                const int32_t tok_end = std::min(tok0 + tpw, ch.z);
+                const int32_t key_end = p.causal ? ch.y + tok_end : kv_len;
+                const int32_t t_lo = ws / KT, t_hi = std::max(t_lo, (key_end + KT - 1) / KT);
+                items.push_back({ch, kvh, tok0, t_lo, t_hi});
+                total += t_hi - t_lo + kSegCost;
+            }
+    }
+    groups = std::max<int32_t>(1, groups);
+    out.work.clear();
+    out.range.clear();
+    out.slots = 0;
+
+    // Grid order: one item per workgroup, dispatched by the hardware in id
+    // order as CUs free up.  All token blocks of one (chunk, kv head) get ids of
+    // one residue mod 8, so they run side by side on one XCD and its L2 serves
+    // their shared K/V; longest chunks first, the heaviest token blocks of a
+    // group first.  Its makespan is estimated by list scheduling on `groups` CUs.
+    std::vector<int32_t> order(n);
+    for (int32_t c = 0; c < n; c++) order[c] = c;
+    std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
+        return chunks[a].y + chunks[a].z > chunks[b].y + chunks[b].z;
+    });
+    int32_t nx = 0;
+    for (int32_t c = 0; c < n; c++) nx = std::max(nx, (chunks[c].z + tpw - 1) / tpw);
+    const int64_t ngroups = (int64_t)n * p.num_kv_heads;
+    const int64_t grid_ids = (int64_t)kXcds * nx * ((ngroups + kXcds - 1) / kXcds);
+    // item index of (chunk c, kv head, token block) in `items`
+    std::vector<int64_t> item_base(n + 1, 0);
+    for (int32_t c = 0; c < n; c++)
+        item_base[c + 1] = item_base[c] + (int64_t)p.num_kv_heads * ((chunks[c].z + tpw - 1) / tpw);
+    std::vector<int64_t> grid_item(grid_ids, -1);
+    int64_t grid_makespan = 0;
+    {
+        std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> cu;
+        for (int32_t i = 0; i < groups; i++) cu.push(0);
+        for (int64_t b = 0; b < grid_ids; b++) {
+            const int64_t xcd = b % kXcds, r = b / kXcds;
+            const int64_t grp = xcd + kXcds * (r / nx);
+            if (grp >= ngroups) continue;
+            const int32_t c = order[grp / p.num_kv_heads], kvh = (int32_t)(grp % p.num_kv_heads);
+            const int32_t nb = (chunks[c].z + tpw - 1) / tpw, tb = nx - 1 - (int32_t)(r % nx);
+            if (tb >= nb) continue;
+            const int64_t it = item_base[c] + (int64_t)kvh * nb + tb;
+            grid_item[b] = it;
+            const int64_t t = cu.top() + items[it].t_hi - items[it].t_lo + kSegCost;
+            cu.pop();
+            cu.push(t);
+            grid_makespan = std::max(grid_makespan, t);
+        }
+    }
+
+    // smallest capacity that fits the line into `groups` workgroups
+    int64_t lo = std::max<int64_t>((total + groups - 1) / groups, kSegCost + kSplitCost + kMinPiece);
+    int64_t hi = std::max<int64_t>(lo, total + kSegCost);
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) / 2;
+        if (pf_fill(items, mid, groups, nullptr, nullptr) <= groups) hi = mid; else lo = mid + 1;
+    }
+    // The balanced split pays for its partials and, with many items per
+    // workgroup, loses the side-by-side L2 sharing of the grid order: it is
+    // taken only when it clearly shortens the estimated makespan.
+    if (grid_ids <= INT32_MAX && (double)lo > 0.95 * (double)grid_makespan) {
+        out.range.assign(grid_ids, make_int2(0, 0));
+        for (int64_t b = 0; b < grid_ids; b++) {
+            if (grid_item[b] < 0) continue;
+            const PfItem &it = items[grid_item[b]];
+            const int32_t k = (int32_t)(out.work.size() / 3);
+            out.work.push_back(it.chunk);
+            out.work.push_back(make_int4(it.kvh, it.tok0, it.t_lo, it.t_hi));
+            out.work.push_back(make_int4(0, 0, 1, 0));
+            out.range[b] = make_int2(k, k + 1);
+        }
+        p.pf_groups = (int32_t)grid_ids;
+        return;
+    }
+    std::vector<int32_t> first(groups + 1, 0);
+    const int32_t parts = pf_fill(items, lo, groups, &out, &first);
+    first[parts] = (int32_t)(out.work.size() / 3);
+    // workgroup b runs on XCD b % 8: consecutive parts on one XCD
+    const int32_t per = (parts + kXcds - 1) / kXcds;
+    const int32_t wgs = parts <= kXcds ? parts : kXcds * per;
+    out.range.assign(wgs, make_int2(0, 0));
+    for (int32_t b = 0; b < wgs; b++) {
+        const int32_t part = parts <= kXcds ? b : (b % kXcds) * per + b / kXcds;
+        if (part < parts) out.range[b] = make_int2(first[part], first[part + 1]);
+    }
+    p.pf_groups = wgs;
 }
 
 }  // namespace pam

@@ -287,16 +287,7 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
         p.part_o = static_cast<float *>(workspace_.ptr);
         p.part_ml = p.part_o + slots * p.head_dim;
         p.part_bytes = (uint32_t)bytes;
-        if ((size_t)counters * 4 > seg_count_.bytes) {
-            hip_check(hipStreamSynchronize(stream()), "counter resize");
-            if (seg_count_.ptr) hip_check(hipFree(seg_count_.ptr), "hipFree");
-            seg_count_.ptr = nullptr;
-            seg_count_.bytes = 0;
-            hip_check(hipMalloc(&seg_count_.ptr, (size_t)counters * 4), "hipMalloc counters");
-            hip_check(hipMemsetAsync(seg_count_.ptr, 0, (size_t)counters * 4, stream()), "counter clear");
-            hip_check(hipStreamSynchronize(stream()), "counter clear");
-            seg_count_.bytes = (size_t)counters * 4;
-        }
+        reserve_counters(seg_count_, (size_t)counters * 4);
         p.seg_count = static_cast<int32_t *>(seg_count_.ptr);
         return bytes;
     }
@@ -309,6 +300,52 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
     p.part_o = static_cast<float *>(workspace_.ptr);
     p.part_ml = p.part_o + slots_p * p.head_dim;
     return bytes;
+}
+
+void Context::reserve_counters(DeviceBuffer &b, size_t bytes) {
+    if (bytes <= b.bytes) return;
+    hip_check(hipStreamSynchronize(stream()), "counter resize");
+    if (b.ptr) hip_check(hipFree(b.ptr), "hipFree");
+    b.ptr = nullptr;
+    b.bytes = 0;
+    hip_check(hipMalloc(&b.ptr, bytes), "hipMalloc counters");
+    hip_check(hipMemsetAsync(b.ptr, 0, bytes, stream()), "counter clear");
+    hip_check(hipStreamSynchronize(stream()), "counter clear");
+    b.bytes = bytes;
+}
+
+Context::DensePlan Context::plan_dense_prefill(AttnParams &p, const int4 *chunks, int32_t n, StageList &sl) {
+    PrefillSplit ps;
+    prefill_split_plan(chunks, n, p, cus_, ps);
+    DensePlan d;
+    d.o_work = sl.add(ps.work.data(), ps.work.size() * sizeof(int4));
+    d.o_range = sl.add(ps.range.data(), ps.range.size() * sizeof(int2));
+    p.pf_part = nullptr;
+    p.pf_count = nullptr;
+    p.pf_part_bytes = 0;
+    if (ps.slots > 0) {
+        const int64_t bytes = ps.slots * kPrefillSlotBytes;
+        if (bytes >= ((int64_t)1 << 31)) throw PamError("prefill split workspace exceeds 2 GiB");
+        if ((size_t)bytes > pf_part_.bytes) {
+            hip_check(hipStreamSynchronize(stream()), "prefill workspace resize");
+            if (pf_part_.ptr) hip_check(hipFree(pf_part_.ptr), "hipFree");
+            pf_part_.ptr = nullptr;
+            pf_part_.bytes = 0;
+            hip_check(hipMalloc(&pf_part_.ptr, (size_t)bytes), "hipMalloc prefill workspace");
+            pf_part_.bytes = (size_t)bytes;
+        }
+        reserve_counters(pf_count_, (size_t)ps.slots * 4);
+        p.pf_part = static_cast<float *>(pf_part_.ptr);
+        p.pf_count = static_cast<int32_t *>(pf_count_.ptr);
+        p.pf_part_bytes = (uint32_t)bytes;
+        d.tmp = bytes;
+    }
+    return d;
+}
+
+void Context::bind_dense_prefill(AttnParams &p, const DensePlan &d, const char *base) {
+    p.pf_work = reinterpret_cast<const int4 *>(base + d.o_work);
+    p.pf_range = reinterpret_cast<const int2 *>(base + d.o_range);
 }
 
 static int32_t heads_per_wave(int32_t group) {
@@ -459,11 +496,12 @@ Context::PrefillPlan Context::plan_prefill(const pam_prefill_request &r) {
     const int64_t max_tiles = ceil_div(pl.kv_len, 16) + 1;
     if (pl.dense) {
         const int4 ch = make_int4(0, r.q_offset, r.seq_len, 0);
-        p.chunks = static_cast<const int4 *>(stage(4, &ch, sizeof(ch)));
-        p.num_chunks = 1;
-        p.max_chunk_len = r.seq_len;
         p.bt_stride = 0;
         p.max_parts = 1;
+        StageList sl;
+        const DensePlan d = plan_dense_prefill(p, &ch, 1, sl);
+        bind_dense_prefill(p, d, static_cast<const char *>(stage(4, sl.blob.data(), sl.blob.size())));
+        pl.tmp = d.tmp;
     } else {
         const int64_t waves = (int64_t)r.seq_len * (pl.use_mfma ? l.num_kv_heads : l.num_heads / nh);
         pl.tmp = plan_split(p, l.data_type, pl.use_mfma, max_tiles, waves);
@@ -684,7 +722,6 @@ void Context::mixed_step(const pam_mixed_request &r) {
     // multi-token chunks go to the dense prefill kernel where it applies
     const bool dense = prefill_mfma_supported(l.data_type, l.head_dim, G, l.block_size) && decode_kernel_choice != 1;
     std::vector<int4> rows, chunks;
-    int64_t max_chunk = 0;
     std::vector<int32_t> cu(r.num_seqs + 1, 0);
     int64_t max_tiles = 1;
     for (int32_t s = 0; s < r.num_seqs; s++) {
@@ -695,7 +732,6 @@ void Context::mixed_step(const pam_mixed_request &r) {
         const int64_t ws = W > 0 ? std::max<int64_t>(0, kv_len - W) : 0;
         if (dense && T > 1) {
             chunks.push_back(make_int4(s, (int32_t)c, (int32_t)T, cu[s]));
-            max_chunk = std::max<int64_t>(max_chunk, T);
             cu[s + 1] = cu[s] + (int32_t)T;
             continue;
         }
@@ -712,9 +748,6 @@ void Context::mixed_step(const pam_mixed_request &r) {
     }
     const int32_t total = cu[r.num_seqs];
     if (total == 0) return;
-    // longest chunks first: their workgroups are the slowest to finish
-    std::stable_sort(chunks.begin(), chunks.end(),
-                     [](const int4 &a, const int4 &b) { return a.y + a.z > b.y + b.z; });
     const int32_t ragged_rows = (int32_t)rows.size();
     bool use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size) && G >= 4;
     if (decode_kernel_choice == 1) use_mfma = false;
@@ -723,7 +756,6 @@ void Context::mixed_step(const pam_mixed_request &r) {
     // device-side descriptors, staged with one copy (StageList)
     StageList sl;
     const size_t o_rows = sl.add(rows.data(), rows.size() * sizeof(int4));
-    const size_t o_chunks = sl.add(chunks.data(), chunks.size() * sizeof(int4));
     AppendBatchParams ab{};
     std::vector<int2> tok;
     std::vector<int4> work;
@@ -746,9 +778,15 @@ void Context::mixed_step(const pam_mixed_request &r) {
             o_tok = sl.add(tok.data(), tok.size() * sizeof(int2));
         }
     }
+    AttnParams pf{};  // the dense prefill's work list and split workspace
+    pf.num_heads = l.num_heads;
+    pf.num_kv_heads = l.num_kv_heads;
+    pf.window = W;
+    pf.causal = 1;
+    DensePlan dense_plan;
+    if (!chunks.empty()) dense_plan = plan_dense_prefill(pf, chunks.data(), (int32_t)chunks.size(), sl);
     const char *sbase = static_cast<const char *>(stage(0, sl.blob.data(), sl.blob.size()));
     const int4 *d_rows = ragged_rows ? reinterpret_cast<const int4 *>(sbase + o_rows) : nullptr;
-    const int4 *d_chunks = chunks.empty() ? nullptr : reinterpret_cast<const int4 *>(sbase + o_chunks);
     if (appending) {
         ab.keys = r.new_keys;
         ab.values = r.new_values;
@@ -783,9 +821,6 @@ void Context::mixed_step(const pam_mixed_request &r) {
     p.block_tables = r.block_tables;
     p.row_info = d_rows;
     p.rows = ragged_rows;
-    p.chunks = d_chunks;
-    p.num_chunks = (int32_t)chunks.size();
-    p.max_chunk_len = (int32_t)max_chunk;
     p.bt_stride = r.bt_stride;
     p.max_num_blocks = r.bt_stride;
     p.num_heads = l.num_heads;
@@ -795,6 +830,13 @@ void Context::mixed_step(const pam_mixed_request &r) {
     p.window = W;
     p.mode = kRowRagged;
     p.causal = 1;  // prefill chunks are causal within the chunk (ragged rows carry it in k_hi)
+    if (!chunks.empty()) {
+        p.pf_part = pf.pf_part;
+        p.pf_count = pf.pf_count;
+        p.pf_part_bytes = pf.pf_part_bytes;
+        p.pf_groups = pf.pf_groups;
+        bind_dense_prefill(p, dense_plan, sbase);
+    }
     p.heads_per_wave = nh;
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
     p.zero_page = zero_page_;

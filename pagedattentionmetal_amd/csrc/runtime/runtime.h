@@ -148,6 +148,15 @@ class Context {
     AppendParams append_params(const pam_append_request &r);
     int32_t choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma);
     int64_t plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves);
+    // dense prefill: work list of host chunks (the order staged as p.chunks) added
+    // to `sl`, partial slots and counters reserved; after staging `sl` at `base`,
+    // bind_dense_prefill points p at the list
+    struct DensePlan {
+        size_t o_work = 0, o_range = 0;
+        int64_t tmp = 0;
+    };
+    DensePlan plan_dense_prefill(AttnParams &p, const int4 *chunks, int32_t n, StageList &sl);
+    static void bind_dense_prefill(AttnParams &p, const DensePlan &d, const char *base);
     void record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t blocks, int64_t tmp, bool split,
                       bool has_mid);
 
@@ -162,6 +171,9 @@ class Context {
     bool stats_has_mid_ = false;
     DeviceBuffer workspace_;
     DeviceBuffer seg_count_;  // stream-K counters: zero between launches
+    DeviceBuffer pf_part_;    // dense prefill: partial slots of split items
+    DeviceBuffer pf_count_;   // dense prefill: counters, zero between launches
+    void reserve_counters(DeviceBuffer &b, size_t bytes);
     DeviceBuffer scratch_[6];
     void *pinned_ = nullptr;
     void *pinned_dev_ = nullptr;  // the device's address of pinned_

@@ -307,6 +307,30 @@ def test_prefill_parity(engine, case):
     assert err <= TOL[dtype], f"rel err {err:.3e}"
 
 
+@pytest.mark.gpu
+def test_dense_prefill_split_repeatable(engine):
+    """The dense prefill kernel cuts long items into pieces merged in the kernel
+    (partial slots and counters): the merge order is fixed, so repeated calls give
+    the same bits, and the counters are back at zero after every call (a call
+    of another shape in between changes nothing)."""
+    import torch
+    rng = np.random.default_rng(77)
+    H, hkv, d, bs, T, off = 32, 8, 128, 16, 700, 2500
+    q, k, v, bt, _ = make_case(rng, 1, H, hkv, d, bs, 1, [off + T])
+    q = rng.standard_normal((T, H, d)).astype(np.float16)
+    kd, vd, qd, btd = to_dev(k), to_dev(v), to_dev(q), to_dev(bt[0])
+    outs = []
+    for t_len in (T, 90, T):
+        out = torch.zeros((t_len, H, d), dtype=torch.float16, device="cuda")
+        engine.prefill(qd[:t_len], kd, vd, btd, out, t_len, layer(H, hkv, d, bs, 1), causal=True, q_offset=off)
+        outs.append(to_host(out))
+    assert np.array_equal(outs[0].view(np.uint16), outs[2].view(np.uint16))
+    ref = oracle.prefill(1, q, k, v, bt[0], off, causal=True, n_threads=8)
+    assert row_rel_err(outs[0].astype(np.float64), ref) <= TOL[1]
+    ref90 = oracle.prefill(1, q[:90], k, v, bt[0], off, causal=True, n_threads=8)
+    assert row_rel_err(outs[1].astype(np.float64), ref90) <= TOL[1]
+
+
 # ---------------------------------------------------------------- mixed step
 
 @pytest.mark.parametrize("dtype", [1, 2, 0])
