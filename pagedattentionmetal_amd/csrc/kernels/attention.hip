@@ -112,6 +112,9 @@ __device__ __forceinline__ f16x8 e4m3x8_to_f16x8(uint32_t w0, uint32_t w1) {
 // partition's tiles and merge in LDS; in the stream-K form they read up to four
 // kv heads of the same tiles side by side.
 constexpr int kMfmaWaves = 4;
+// lazy online softmax: the reference max moves only when a score passes it by
+// this many log2 units, which bounds P by 2^8
+constexpr float kLazyRescaleLog2 = 8.0f;
 // Rows the stream-K form can index from LDS (its row prefix table).
 constexpr int kStreamKMaxRows = 2048;
 // Decode rows whose key ranges the stream-K form keeps in LDS (8 KiB: three
@@ -159,8 +162,9 @@ struct MfmaShape {
 
 // The tile loop shared by both work forms: tiles [t_begin, t_end) of row
 // context c for kv head kvh, on the calling wave alone, using its LDS tiles kt
-// (K) and kt + 16 * KL (V).  Leaves the wave's online-softmax state: m_run (log2
-// units, per head), l_run (this lane's share of the row sum) and o[i], lane
+// (K) and kt + 16 * KL (V).  Leaves the wave's online-softmax state: m_run (the
+// reference max in log2 units, per head; l and O are relative to it, and it is
+// -inf only while no key was seen), l_run (this lane's share of the row sum) and o[i], lane
 // (head `lane % 16`, quad `lane / 16`) holding dims 16i + 4 quad .. +4.
 //
 // Loads: 16 lanes (8 for e4m3) cover one token row's HD elements with 16-byte
@@ -348,7 +352,9 @@ __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, 
                                                        qv[i], s, 0, 0, 0);
         const float sc = p.scale_log2;
 
-        // online softmax on this lane's 4 tokens of head `row`
+        // online softmax on this lane's 4 tokens of head `row`.  The reference
+        // max m_run is raised (and l, O rescaled) only when a score passes it by
+        // 2^8, so P <= 2^8 fits the f16 operand and most tiles skip the rescale.
         float sv[4];
         float mt = -INFINITY;
 #pragma unroll
@@ -357,11 +363,18 @@ __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, 
             sv[q] = (j >= c.k_lo && j < j_hi) ? s[q] * sc : -INFINITY;
             mt = fmaxf(mt, sv[q]);
         }
-        mt = fmaxf(mt, shfl_xor(mt, 16));
-        mt = fmaxf(mt, shfl_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float corr = exp2f(m_run - m_use);
+        if (__any(mt > m_run + kLazyRescaleLog2)) {  // wave-uniform, rare after the first tile
+            mt = fmaxf(mt, shfl_xor(mt, 16));
+            mt = fmaxf(mt, shfl_xor(mt, 32));
+            const float m_new = mt > m_run + kLazyRescaleLog2 ? mt : m_run;
+            // 1 for heads that keep their reference; 0 while m_run is unset (l, O are 0)
+            const float corr = m_new == m_run ? 1.0f : exp2f(m_run - m_new);
+            l_run *= corr;
+#pragma unroll
+            for (int i = 0; i < NO; i++) o[i] *= corr;
+            m_run = m_new;
+        }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         f16x4 pb;
         float psum = 0.0f;
 #pragma unroll
@@ -370,10 +383,7 @@ __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, 
             psum += pq;
             pb[q] = (f16)pq;
         }
-        l_run = l_run * corr + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int i = 0; i < NO; i++) o[i] *= corr;
+        l_run += psum;
 
         // V^T operand of dims 16i..: lane (o, g) addresses row 4g + o/4, dims
         // 16i + 4(o%4); the transposed load hands it tokens 4g..4g+3 of dim 16i + o
