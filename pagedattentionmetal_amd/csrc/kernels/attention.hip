@@ -768,6 +768,8 @@ __device__ __forceinline__ void load_kv4<uint8_t>(const uint8_t *ptr, f16 scale,
     for (int i = 0; i < 4; i++) v[i] = (float)fp8_dequant((w >> (8 * i)) & 0xFFu, scale);
 }
 
+constexpr int kValuBatch = 8;  // steps of the VALU kernel whose loads are in flight together
+
 // lanes_per_row: power of two >= head_dim / 4 (<= 64); heads NH share one kv head.
 template <typename KV, typename QT, int NH>
 __global__ __launch_bounds__(64) void attn_valu_kernel(AttnParams p, int lanes_per_row) {
@@ -815,36 +817,67 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnParams p, int lanes_p
     const KV *vpool = static_cast<const KV *>(p.v_pool);
     const int bs = p.block_size;
 
-    for (int j0 = pr.t_begin * 16; j0 < pr.t_end * 16; j0 += TPI) {
-        const int j = j0 + sub;
-        const bool tok_ok = j >= c.k_lo && j < c.k_hi;
-        float kv[4] = {0.f, 0.f, 0.f, 0.f}, vv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (tok_ok && dim_ok) {
-            const int64_t phys = c.bt[j / bs];
-            const int64_t off = (phys * bs + j % bs) * row_stride + (int64_t)kvh * HD + d0;
-            f16 ks = (f16)1.0f, vs = (f16)1.0f;
-            if constexpr (sizeof(KV) == 1) {
-                ks = bits_to_f16(p.k_scale[phys]);
-                vs = bits_to_f16(p.v_scale[phys]);
+    // Tokens go in batches of kValuBatch steps of TPI tokens: the block-table
+    // entries of a batch are requested together, then its K/V slices, so a batch
+    // waits on two memory latencies; one online-softmax update covers the batch.
+    constexpr int UB = kValuBatch;
+    for (int j0 = pr.t_begin * 16; j0 < pr.t_end * 16; j0 += UB * TPI) {
+        bool ok[UB];
+        int64_t phys[UB];
+#pragma unroll
+        for (int u = 0; u < UB; u++) {
+            const int j = j0 + u * TPI + sub;
+            ok[u] = j >= c.k_lo && j < c.k_hi && j < pr.t_end * 16;
+            phys[u] = ok[u] ? (int64_t)c.bt[j / bs] : 0;
+        }
+        float kv[UB][4], vv[UB][4];
+#pragma unroll
+        for (int u = 0; u < UB; u++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) kv[u][e] = vv[u][e] = 0.0f;
+            if (ok[u] && dim_ok) {
+                const int j = j0 + u * TPI + sub;
+                const int64_t off = (phys[u] * bs + j % bs) * row_stride + (int64_t)kvh * HD + d0;
+                f16 ks = (f16)1.0f, vs = (f16)1.0f;
+                if constexpr (sizeof(KV) == 1) {
+                    ks = bits_to_f16(p.k_scale[phys[u]]);
+                    vs = bits_to_f16(p.v_scale[phys[u]]);
+                }
+                load_kv4<KV>(kpool + off, ks, kv[u]);
+                load_kv4<KV>(vpool + off, vs, vv[u]);
             }
-            load_kv4<KV>(kpool + off, ks, kv);
-            load_kv4<KV>(vpool + off, vs, vv);
         }
 #pragma unroll
         for (int hh = 0; hh < NH; hh++) {
-            float s = q[hh][0] * kv[0] + q[hh][1] * kv[1] + q[hh][2] * kv[2] + q[hh][3] * kv[3];
-            s = wave_sum_xor(s, 1, LPR);
-            s = tok_ok ? s * p.scale_log2 : -INFINITY;
-            const float mt = wave_max_xor(s, LPR, 64);
+            float sv[UB];
+            float mt = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < UB; u++) {
+                float sd = q[hh][0] * kv[u][0] + q[hh][1] * kv[u][1] + q[hh][2] * kv[u][2] + q[hh][3] * kv[u][3];
+                sd = wave_sum_xor(sd, 1, LPR);
+                sv[u] = ok[u] ? sd * p.scale_log2 : -INFINITY;
+                mt = fmaxf(mt, sv[u]);
+            }
+            mt = wave_max_xor(mt, LPR, 64);
             const float m_new = fmaxf(m[hh], mt);
-            // an iteration whose tokens all fall outside the key range keeps the state
+            // a batch whose tokens all fall outside the key range keeps the state
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
             const float corr = exp2f(m[hh] - m_use);
-            const float pj = exp2f(s - m_use);
-            l[hh] = l[hh] * corr + pj;
+            float ls = l[hh] * corr;
+            float a4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) a4[e] = acc[hh][e] * corr;
+#pragma unroll
+            for (int u = 0; u < UB; u++) {
+                const float pj = exp2f(sv[u] - m_use);
+                ls += pj;
+#pragma unroll
+                for (int e = 0; e < 4; e++) a4[e] += pj * vv[u][e];
+            }
+            l[hh] = ls;
             m[hh] = m_new;
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[hh][e] = acc[hh][e] * corr + pj * vv[e];
+            for (int e = 0; e < 4; e++) acc[hh][e] = a4[e];
         }
     }
 
@@ -892,11 +925,16 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnParams p) {
     if (np <= 1) return;
     const int HD = p.head_dim, H = p.num_heads;
     const int64_t base = ((int64_t)r * H + h) * p.max_parts;
-    float M = -INFINITY;
-    for (int i = lane; i < np; i += 64) M = fmaxf(M, p.part_ml[(base + i) * 2]);
-    M = wave_max_xor(M, 1, 64);
-    float den = 0.0f;
-    for (int i = lane; i < np; i += 64) den += exp2f(p.part_ml[(base + i) * 2] - M) * p.part_ml[(base + i) * 2 + 1];
+    // one pass over (m, l): each lane folds its partitions, then the lanes merge
+    float Ml = -INFINITY, dl = 0.0f;
+    for (int i = lane; i < np; i += 64) {
+        const float mi = p.part_ml[(base + i) * 2], li = p.part_ml[(base + i) * 2 + 1];
+        const float Mn = fmaxf(Ml, mi);
+        if (Mn != -INFINITY) dl = dl * exp2f(Ml - Mn) + li * exp2f(mi - Mn);
+        Ml = Mn;
+    }
+    const float M = wave_max_xor(Ml, 1, 64);
+    float den = Ml == -INFINITY ? 0.0f : dl * exp2f(Ml - M);
     den = wave_sum_xor(den, 1, 64);
     // lanes per group: HD/4 rounded up to a power of two (<= 64)
     int lpg = 1;
@@ -904,6 +942,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnParams p) {
     const int ng = 64 / lpg, g = lane / lpg, d0 = (lane % lpg) * 4;
     float a[4] = {0.f, 0.f, 0.f, 0.f};
     if (d0 < HD) {
+#pragma unroll 4
         for (int i = g; i < np; i += ng) {
             const float w = exp2f(p.part_ml[(base + i) * 2] - M);
             float v[4];

@@ -83,13 +83,32 @@ __device__ __forceinline__ f16 fp8_scale_rule(float new_max_abs, f16 old_scale) 
 // ---------------------------------------------------------------- wave64 shuffles
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
-__device__ __forceinline__ float wave_max_xor(float v, int lo, int hi) {
-    for (int m = lo; m < hi; m <<= 1) v = fmaxf(v, shfl_xor(v, m));
+// v moved across lanes by a DPP pattern (row_mask, bank_mask all lanes)
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Reduction of v over the lane distances lo, 2 lo, .., hi / 2 (powers of two):
+// lane i combines the lanes i ^ m for m in that range.  A reduction from lo = 1
+// runs its stages below 16 as DPP moves (quad_perm [1,0,3,2] and [2,3,0,1], then
+// the half-row and row mirrors, which pair the already reduced quads and
+// octets); other stages are ds_bpermute shuffles.
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce_xor(float v, int lo, int hi) {
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    int m = lo;
+    if (lo == 1) {
+        if (hi > 1) v = op(v, dpp_mov<0xB1>(v));
+        if (hi > 2) v = op(v, dpp_mov<0x4E>(v));
+        if (hi > 4) v = op(v, dpp_mov<0x141>(v));
+        if (hi > 8) v = op(v, dpp_mov<0x140>(v));
+        m = 16;
+    }
+    for (; m < hi; m <<= 1) v = op(v, shfl_xor(v, m));
     return v;
 }
-__device__ __forceinline__ float wave_sum_xor(float v, int lo, int hi) {
-    for (int m = lo; m < hi; m <<= 1) v += shfl_xor(v, m);
-    return v;
-}
+__device__ __forceinline__ float wave_max_xor(float v, int lo, int hi) { return wave_reduce_xor<true>(v, lo, hi); }
+__device__ __forceinline__ float wave_sum_xor(float v, int lo, int hi) { return wave_reduce_xor<false>(v, lo, hi); }
 
 }  // namespace pam

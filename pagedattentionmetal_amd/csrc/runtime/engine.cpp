@@ -262,8 +262,11 @@ int32_t Context::choose_part_tokens(int64_t items_per_part, int64_t max_tiles, b
         return (int32_t)(tpp * 16);
     }
     if (items_per_part >= 8192) return (int32_t)(max_tiles * 16);  // enough rows: one partition per row
+    // VALU kernel: a wave works through its tokens in batches of 8 steps whose
+    // loads are in flight together; few rows are split down to one-tile
+    // partitions, so each wave's latency chain stays short
     int64_t tpp = 16;
-    while (tpp > 4 && items_per_part * ceil_div(max_tiles, tpp) < 4096) tpp /= 2;
+    while (tpp > 1 && items_per_part * ceil_div(max_tiles, tpp) < 4096) tpp /= 2;
     if (tpp >= max_tiles) tpp = max_tiles;
     return (int32_t)(tpp * 16);
 }
