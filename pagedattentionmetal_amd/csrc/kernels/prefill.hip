@@ -24,6 +24,9 @@
 //   Waves 4-7 run one phase behind waves 0-3; waves w and w + 4 share a SIMD,
 //   so its MFMA pipe works on one wave's matrix phase while the other wave's
 //   vector phase runs.
+// A workgroup runs the segments the host's work list gives it (one item, or
+// pieces of items whose partial states are merged by the last workgroup to
+// finish one; prefill_split_plan below).
 // Softmax keeps a per-row reference max that is only raised (and O rescaled)
 // when some score exceeds it by more than 2^8, so P is bounded by 2^8 and goes
 // to the MFMA in f16; the common case needs no cross-lane reduction.
@@ -553,16 +556,19 @@ hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream) {
 
 // ------------------------------------------------------------------ host plan
 //
-// Items are laid out group by group (chunk, kv head), token blocks in order, so
-// the items sharing a group's K/V run side by side.  Costs are in key tiles: a
-// segment costs its tiles plus kSegCost (Q load, block-table segment, ring fill,
-// the masked edge tiles and the output), and a piece of a split item kSplitCost
-// more (publishing and merging partials); these were measured per workgroup
-// with s_memtime on gfx950.  Workgroups are filled in line order up to a common
-// capacity, the smallest with which the line fits `groups` workgroups; an item
-// that does not fit is cut into pieces of an even number of tiles (>= kMinPiece;
-// the tile loop runs pairs).  Consecutive parts of the line go to workgroups of
-// one XCD (workgroup b runs on XCD b mod 8), so a group's pieces share its L2.
+// Two schedules, chosen by estimated makespan (costs in key tiles: a segment
+// costs its tiles plus kSegCost for the Q load, block-table segment, ring fill,
+// masked edge tiles and output; a piece of a split item kSplitCost more for
+// publishing and merging partials; both measured per workgroup with s_memtime
+// on gfx950):
+//  * grid order: one item per workgroup, hardware-dispatched (see below);
+//  * balanced split, one workgroup per CU: items are laid out group by group
+//    (chunk, kv head), token blocks in order, and workgroups are filled in line
+//    order up to a common capacity, the smallest with which the line fits
+//    `groups` workgroups.  An item that does not fit is cut into pieces of an
+//    even number of tiles (>= kMinPiece; the tile loop runs pairs).  Consecutive
+//    parts of the line go to workgroups of one XCD (workgroup b runs on XCD
+//    b mod 8), so a group's pieces share its L2.
 namespace {
 constexpr int kSegCost = 12;
 constexpr int kSplitCost = 4;
