@@ -7,10 +7,12 @@ fp16 ragged decode, B=64, L~U[128,4096], 32 query / 8 KV heads, d=128, bs=16,
 prefill TFLOP/s of the c3 mixed continuous-batching step.  A step is one decode
 of the whole batch with Q, pools and tables already resident in HBM.
 
-  python bench.py [--steps K] [--warmup W] [--all] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--no-configs] [--no-cpu]
 
-Prints one JSON line.  --all adds per-configuration lines for c1, c4, c5 under
-"configs".  The roofline block times the dominant kernel (the decode attention
+Prints one JSON line.  "configs" holds the c1, c4 and c5 decode lines (skipped
+with --no-configs).  Every configuration carries a CPU baseline: the oracle on
+the host's cores over a bounded sample of the same inputs (skipped with
+--no-cpu).  The roofline block times the dominant kernel (the decode attention
 kernel) with HIP events on the stream it is launched on.
 """
 from __future__ import annotations
@@ -160,21 +162,39 @@ def time_mixed(torch, eng, w, t, steps, warmup):
     return ms, sum(kern) / len(kern)
 
 
+def compact_rows(torch, w, t, B):
+    """Host copies of the pool blocks that rows 0..B-1 read (their window only),
+    gathered on the device, and the tables renumbered to them."""
+    import numpy as np
+    q, kp, vp, bt, lens, out, layer, ks, vs = t
+    L = w.seq_lens[:B].astype(np.int64)
+    bs = w.block_size
+    need = {}
+    new_bt = np.zeros((B, w.max_num_blocks), np.int32)
+    for b in range(B):
+        first = max(0, int(L[b]) - w.window) // bs if w.window > 0 else 0
+        for i in range(first, (int(L[b]) + bs - 1) // bs):
+            new_bt[b, i] = need.setdefault(int(w.block_tables[b, i]), len(need))
+    order = torch.tensor(sorted(need, key=need.get), dtype=torch.long, device=kp.device)
+    kh, vh = kp.index_select(0, order).cpu().numpy(), vp.index_select(0, order).cpu().numpy()
+    if w.data_type == 2:
+        ksh = ks.index_select(0, order).cpu().numpy().view(np.uint16)
+        vsh = vs.index_select(0, order).cpu().numpy().view(np.uint16)
+    else:
+        ksh = vsh = None
+    return q[:B].cpu().numpy(), kh, vh, ksh, vsh, new_bt
+
+
 def cpu_baseline_decode(torch, w, t, threads, batch=None, min_seconds=2.0, max_reps=5):
     """The oracle (C restatement of the reference's paged attention) on host cores:
     the first `batch` sequences of the step (all by default), repeated until
-    `min_seconds` of wall time (at most `max_reps` passes); returns GB/s and seconds."""
+    `min_seconds` of wall time (at most `max_reps` passes); returns GB/s, seconds
+    and passes."""
     import numpy as np
 
     import oracle
-    q, kp, vp, bt, lens, out, layer, ks, vs = t
     B = w.batch if batch is None else batch
-    qh = q[:B].cpu().numpy()
-    if w.data_type == 2:
-        kh, vh = kp.cpu().numpy(), vp.cpu().numpy()
-        ksh, vsh = ks.cpu().numpy().view(np.uint16), vs.cpu().numpy().view(np.uint16)
-    else:
-        kh, vh, ksh, vsh = kp.cpu().numpy(), vp.cpu().numpy(), None, None
+    qh, kh, vh, ksh, vsh, bt = compact_rows(torch, w, t, B)
     L = w.seq_lens[:B].astype(np.int64)
     if w.window > 0:
         L = np.minimum(L, w.window)
@@ -182,7 +202,7 @@ def cpu_baseline_decode(torch, w, t, threads, batch=None, min_seconds=2.0, max_r
     nbytes = int(L.sum()) * w.num_kv_heads * w.head_dim * 2 * elem
     reps, t0 = 0, time.perf_counter()
     while True:
-        oracle.decode(w.data_type, qh, kh, vh, w.block_tables[:B], w.seq_lens[:B], w.num_heads, window=w.window,
+        oracle.decode(w.data_type, qh, kh, vh, bt, w.seq_lens[:B], w.num_heads, window=w.window,
                       k_scale=ksh, v_scale=vsh, n_threads=threads)
         reps += 1
         dt = time.perf_counter() - t0
@@ -191,12 +211,39 @@ def cpu_baseline_decode(torch, w, t, threads, batch=None, min_seconds=2.0, max_r
     return nbytes * reps / dt / 1e9, dt, reps
 
 
+def cpu_baseline_prefill(torch, w3, t3, threads, rows=64, min_seconds=1.0, max_reps=5):
+    """The oracle's causal prefill on host cores for the first `rows` rows of the
+    first c3 chunk (its cached context included); returns TFLOP/s, seconds,
+    passes and the sample's description."""
+    import numpy as np
+
+    import oracle
+    q, kp, vp, bt, nk, nv, out, layer = t3
+    ctx, ql = int(w3.context_lens[0]), int(w3.query_lens[0])
+    T = min(rows, ql)
+    kv_len = ctx + T
+    nb = (kv_len + w3.block_size - 1) // w3.block_size
+    blocks = torch.from_numpy(w3.block_tables[0, :nb].astype(np.int64)).to(kp.device)
+    kh, vh = kp.index_select(0, blocks).cpu().numpy(), vp.index_select(0, blocks).cpu().numpy()
+    qh = q[:T].cpu().numpy()
+    flops = 4 * w3.head_dim * w3.num_heads * (T * ctx + T * (T + 1) // 2)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.prefill(1, qh, kh, vh, np.arange(nb, dtype=np.int32), ctx, causal=True, n_threads=threads)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds or reps >= max_reps:
+            break
+    return flops * reps / dt / 1e12, dt, reps, f"rows [{ctx}, {ctx + T}) of a causal prefill at context {ctx} (chunk 0)"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--all", action="store_true", help="also measure c1, c4, c5")
+    ap.add_argument("--all", action="store_true", help="measure c1, c4, c5 too (the default; kept for old command lines)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the c1, c4, c5 lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the 1 GiB read and copy calibration streams (achievable HBM rate; "
@@ -226,6 +273,13 @@ def main():
     pflops = w3.prefill_flops()
     tflops = pflops / (pk_ms * 1e-3) / 1e12
     log(f"bench: c3 mixed step {ms3:.4f} ms; prefill kernel {pk_ms:.4f} ms = {tflops:.1f} TFLOP/s")
+    cpu3 = None
+    if not args.no_cpu:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        log("bench: CPU baseline for the c3 prefill rows")
+        ctf, cdt, creps, what = cpu_baseline_prefill(torch, w3, t3, threads)
+        cpu3 = {"value": round(ctf, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                "sample": f"{creps} x {what} through the C oracle on {threads} host threads, {cdt:.2f} s"}
     del t3, e3
     torch.cuda.empty_cache()
 
@@ -281,7 +335,7 @@ def main():
                     "tokens_per_s": round(w3.total_rows / (ms3 * 1e-3), 1),
                     "prefill_kernel": "prefill_mfma_kernel<128>", "prefill_kernel_ms": round(pk_ms, 5),
                     "flops_per_launch": pflops, "tflops": round(tflops, 2), "peak_tflops": FP16_PEAK_TFLOPS,
-                    "frac": round(tflops / FP16_PEAK_TFLOPS, 4)},
+                    "frac": round(tflops / FP16_PEAK_TFLOPS, 4), "cpu_baseline": cpu3},
     }
 
     if args.calibrate:
@@ -297,9 +351,11 @@ def main():
                                  "bytes": gib}
         del src, dst
 
-    if args.all:
+    if not args.no_configs:
+        # the other decode configurations, each beside the oracle on a bounded
+        # sample of its rows (c1 whole; c4 and c5 the first 16 and 4 rows)
         cfgs = {}
-        for k in (1, 4, 5):
+        for k, sample in ((1, None), (4, 16), (5, 4)):
             log(f"bench: c{k} decode")
             wk, ek, tk = decode_setup(k, torch, api, workloads)
             msk, kk, rk = time_decode(torch, ek, wk, tk, args.steps, args.warmup)
@@ -308,6 +364,16 @@ def main():
                              "kernel_ms": round(kk, 5), "reduce_ms": round(rk, 5),
                              "kernel_frac_hbm": round(b / (kk * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                              "tokens_per_s": round(wk.batch / (msk * 1e-3), 1)}
+            if not args.no_cpu:
+                threads = max(1, min(16, os.cpu_count() or 1))
+                # (c1 is a few MB: its passes repeat until half a second has passed)
+                cg, cd, cr = cpu_baseline_decode(torch, wk, tk, threads, batch=sample,
+                                                 min_seconds=0.5 if sample is None else 1.0,
+                                                 max_reps=100000 if sample is None else 5)
+                rows = wk.batch if sample is None else sample
+                cfgs[f"c{k}"]["cpu_baseline"] = {
+                    "value": round(cg, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+                    "sample": f"{cr} x the first {rows} rows of the c{k} step through the C oracle, {cd:.2f} s"}
             del tk, ek
             torch.cuda.empty_cache()
         result["configs"] = cfgs
