@@ -400,3 +400,56 @@ def test_mixed_step_parity(engine, dtype):
         assert np.array_equal(to_host(ksd).view(np.uint16), ks.view(np.uint16))
     err = row_rel_err(to_host(out), ref)
     assert err <= TOL[dtype], f"rel err {err:.3e}; worst (row, head, err): {worst_rows(to_host(out), ref)}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed,H,hkv,bs,window", [(1, 32, 8, 16, 0), (2, 16, 8, 8, 0), (3, 32, 4, 16, 700),
+                                                  (4, 64, 8, 32, 0)])
+def test_mixed_step_random_ragged_chunks(engine, seed, H, hkv, bs, window):
+    """Many ragged f16 prefill chunks (2..600 new tokens after 0..2500 cached ones)
+    beside decode rows: the dense prefill's work list cuts the larger items into
+    pieces merged in the kernel.  Every row is checked against the oracle."""
+    import torch
+    rng = np.random.default_rng(900 + seed)
+    d = 128
+    nch, ndec = 10, 5
+    ctx = np.concatenate([rng.integers(0, 2501, nch), rng.integers(1, 2000, ndec)]).astype(np.int32)
+    ql = np.concatenate([rng.integers(2, 601, nch), np.ones(ndec)]).astype(np.int32)
+    order = rng.permutation(nch + ndec)  # chunks and decode rows interleaved
+    ctx, ql = ctx[order], ql[order]
+    total = ctx + ql
+    nblk = (total + bs - 1) // bs
+    nb = int(nblk.sum()) + 7
+    perm = rng.permutation(nb).astype(np.int32)
+    bt = np.zeros((len(ctx), int(nblk.max())), np.int32)
+    c = 0
+    for s, n in enumerate(nblk):
+        bt[s, :n] = perm[c:c + n]
+        c += n
+    kp = rng.standard_normal((nb, bs, hkv, d)).astype(np.float16)
+    vp = rng.standard_normal((nb, bs, hkv, d)).astype(np.float16)
+    rows = int(ql.sum())
+    q = rng.standard_normal((rows, H, d)).astype(np.float16)
+    new_k = rng.standard_normal((rows, hkv, d)).astype(np.float16)
+    new_v = rng.standard_normal((rows, hkv, d)).astype(np.float16)
+    kd, vd = to_dev(kp), to_dev(vp)
+    out = torch.zeros((rows, H, d), dtype=torch.float16, device="cuda")
+    engine.mixed_step(to_dev(q), out, kd, vd, to_dev(bt), ctx, ql, layer(H, hkv, d, bs, 1, window),
+                      new_keys=to_dev(new_k), new_values=to_dev(new_v))
+    r0 = 0
+    for s in range(len(ctx)):
+        T = int(ql[s])
+        oracle.append(1, new_k[r0:r0 + T], new_v[r0:r0 + T], kp, vp, bt[s], int(ctx[s]))
+        r0 += T
+    assert np.array_equal(to_host(kd).view(np.uint16), kp.view(np.uint16)), "pool bytes differ after the append"
+    got = to_host(out).astype(np.float64)
+    r0 = 0
+    for s in range(len(ctx)):
+        T = int(ql[s])
+        ref = oracle.prefill(1, q[r0:r0 + T], kp, vp, bt[s], int(ctx[s]), causal=True, window=window,
+                             n_threads=8)
+        fin = np.isfinite(ref).all(axis=-1)
+        assert np.isnan(got[r0:r0 + T][~fin]).all()
+        err = row_rel_err(got[r0:r0 + T][fin], ref[fin]) if fin.any() else 0.0
+        assert err <= TOL[1], f"sequence {s} (context {ctx[s]}, {T} new): rel err {err:.3e}"
+        r0 += T
