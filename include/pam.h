@@ -216,7 +216,10 @@ int32_t pam_engine_prefill(void *context, const pam_prefill_request *request);
 /* PagedAttentionEngine.appendToCache(_:) (PagedAttentionEngine.swift:585-597) */
 int32_t pam_engine_append(void *context, const pam_append_request *request);
 /* PagedAttentionEngine.fusedPrefill(_:) (PagedAttentionEngine.swift:633-710): append
- * and prefill as one call, both launches on the context's stream */
+ * and prefill as one call on the context's stream.  f16 caches with head_dim 128
+ * run one kernel that reads the new keys and values from raw_k / raw_v and writes
+ * them into the pools; other shapes and dtypes append first, then attend.  The
+ * pools end up equal to a separate append in every case. */
 int32_t pam_engine_fused_prefill(void *context, const pam_fused_prefill_request *request);
 /* PagedAttentionEngine.backward(q:kPool:...) (PagedAttentionEngine.swift:1340-1396) */
 int32_t pam_engine_backward(void *context, const pam_backward_request *request);

@@ -59,6 +59,11 @@ struct AttnParams {
     int32_t *pf_count;         // one per slot, all 0 between launches
     uint32_t pf_part_bytes;
     int32_t pf_groups;         // workgroups of the launch
+    // dense prefill, fused append (f16): the chunks' new keys and values
+    // [rows][Hkv][d] (row = the chunk's row_base + token).  Keys at or past a
+    // chunk's q_offset are read from here, and the kernel writes them into the
+    // pools.  Null: all keys come from the pools.
+    const void *fuse_k, *fuse_v;
 };
 
 // Paged attention over rows (decode / prefill-as-rows / ragged).  Chooses the

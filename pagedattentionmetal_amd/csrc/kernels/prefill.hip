@@ -77,7 +77,7 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
     return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
-template <int HD, int RB>
+template <int HD, int RB, bool FUSED>
 __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(AttnParams p) {
     static_assert(HD == 128, "layouts assume d = 128");
     constexpr int KT = kPrefillKT;
@@ -136,6 +136,25 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
         int full_hi = min(kv_len / KT, t_hi);
         if (p.causal) full_hi = min(full_hi, (ch.y + tok0 + 1) / KT);
 
+        // Fused append: the first piece of an item writes its tokens' rows of kv
+        // head kvh into the pools (readers of these keys use the inputs).
+        if constexpr (FUSED) {
+            if (wb.y == 0) {
+                const int64_t rs = (int64_t)p.num_kv_heads * HD;
+                for (int idx = tid; idx < (tok_end - tok0) * (HD / 8); idx += 64 * kPrefillWaves) {
+                    const int tk = tok0 + idx / (HD / 8), pc = idx % (HD / 8);
+                    const int pos = ch.y + tk;
+                    const int64_t slot = ((int64_t)bt[pos >> bsh] << bsh) | (pos & bsm);
+                    const int64_t src = (int64_t)(ch.w + tk) * rs + kvh * HD + 8 * pc;
+                    const int64_t dst = slot * rs + kvh * HD + 8 * pc;
+                    *reinterpret_cast<f16x8 *>(static_cast<f16 *>(const_cast<void *>(p.k_pool)) + dst) =
+                        *reinterpret_cast<const f16x8 *>(static_cast<const f16 *>(p.fuse_k) + src);
+                    *reinterpret_cast<f16x8 *>(static_cast<f16 *>(const_cast<void *>(p.v_pool)) + dst) =
+                        *reinterpret_cast<const f16x8 *>(static_cast<const f16 *>(p.fuse_v) + src);
+                }
+            }
+        }
+
         // this lane's query rows: column n of each of the wave's 32-row blocks
         int my_tok[RB], my_head[RB], qpos[RB];
         bool row_ok[RB];
@@ -159,6 +178,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
         const uint32_t row_stride = (uint32_t)(p.num_kv_heads * HD);  // halves per pool row (< 2^32)
         const f16 *kpool = static_cast<const f16 *>(p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
         const f16 *vpool = static_cast<const f16 *>(p.v_pool) + (int64_t)kvh * HD + my_piece * 8;
+        // fused append: rows of the chunk's new tokens (same row stride as the pools)
+        const f16 *kin = FUSED ? static_cast<const f16 *>(p.fuse_k) + (int64_t)kvh * HD + my_piece * 8 : nullptr;
+        const f16 *vin = FUSED ? static_cast<const f16 *>(p.fuse_v) + (int64_t)kvh * HD + my_piece * 8 : nullptr;
         // two register sets in flight: a tile's rows are loaded two iterations
         // before they are written to LDS
         f16x8 kra[KPT], vra[KPT], krb[KPT], vrb[KPT];
@@ -173,14 +195,17 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
                 // of the current segment)
                 j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
                 slot[i] = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
+                // fused append: a new token's row of the inputs (top bit set)
+                if (FUSED && j >= ch.y) slot[i] = 0x80000000u | (uint32_t)(ch.w + j - ch.y);
             }
         };
         auto load = [&](const uint32_t(&slot)[KPT], f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
 #pragma unroll
             for (int i = 0; i < KPT; i++) {
-                const uint64_t off = (uint64_t)slot[i] * row_stride;
-                kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off);
-                vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off);
+                const uint64_t off = (uint64_t)(slot[i] & 0x7FFFFFFFu) * row_stride;
+                const bool in = FUSED && (slot[i] >> 31);
+                kreg[i] = *reinterpret_cast<const f16x8 *>((in ? kin : kpool) + off);
+                vreg[i] = *reinterpret_cast<const f16x8 *>((in ? vin : vpool) + off);
             }
         };
         auto fetch = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
@@ -549,8 +574,12 @@ hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream) {
         return hipErrorInvalidValue;
     const int G = p.num_heads / p.num_kv_heads;
     if (!prefill_mfma_supported(kF16, p.head_dim, G, p.block_size)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB>), dim3(p.pf_groups), dim3(64 * kPrefillWaves), 0,
-                       stream, p);
+    if (p.fuse_k != nullptr)
+        hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, true>), dim3(p.pf_groups), dim3(64 * kPrefillWaves),
+                           0, stream, p);
+    else
+        hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, false>), dim3(p.pf_groups), dim3(64 * kPrefillWaves),
+                           0, stream, p);
     return hipGetLastError();
 }
 

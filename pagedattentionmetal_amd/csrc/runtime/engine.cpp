@@ -586,10 +586,17 @@ void Context::fused_prefill_gpu(const pam_fused_prefill_request &r) {
     q.k_scale = r.k_scale;
     q.v_scale = r.v_scale;
     const AppendParams ap = append_params(a);
-    const PrefillPlan pl = plan_prefill(q);
+    PrefillPlan pl = plan_prefill(q);
+    // the dense f16 kernel appends as it reads: one launch; other cases append
+    // first, then attend
+    const bool one_kernel = pl.dense && l.data_type == kF16;
+    if (one_kernel) {
+        pl.p.fuse_k = r.raw_k;
+        pl.p.fuse_v = r.raw_v;
+    }
     with_retry("fusedPrefill", [&] {
         mark(ev0_);
-        check_launch(launch_append(ap, l.data_type, stream()), "fused prefill append");
+        if (!one_kernel) check_launch(launch_append(ap, l.data_type, stream()), "fused prefill append");
         launch_prefill_plan(pl, l.data_type);
         mark(ev1_);
         finish("fusedPrefill");

@@ -187,12 +187,16 @@ def test_gpu_timing_switch(torch):
     (0, 8, 8, 32, 16, 40, True, 0),
     (1, 32, 8, 128, 16, 300, True, 0),   # f16, d = 128: dense MFMA prefill kernel
     (1, 32, 8, 128, 16, 200, True, 64),  # fixed window start
+    (1, 32, 16, 128, 32, 1000, True, 0),  # one-kernel fused path, items split over workgroups
+    (1, 8, 8, 128, 16, 150, False, 0),   # one-kernel fused path, G = 1, full attention
     (1, 16, 4, 64, 8, 77, True, 0),      # row kernels, bs 8
     (2, 32, 8, 128, 16, 100, True, 0),   # FP8: quantise on append, dequantise in attention
 ])
 def test_fused_prefill_equals_append_then_prefill(torch, dtype, H, hkv, d, bs, T, causal, window):
     """Pool bytes (and FP8 scales) equal a separate append; the output equals a
-    separate prefill over that pool, bit for bit, and the oracle within tolerance."""
+    separate prefill over that pool, bit for bit, and the oracle within tolerance.
+    (f16 with d = 128 runs as one kernel that reads the new keys from the inputs
+    and writes them into the pools; the other cases append, then attend.)"""
     from pagedattentionmetal_amd import PagedAttentionEngine, PagedLayerSpec
     eng = PagedAttentionEngine()
     eng.set_graceful_degradation(False)
