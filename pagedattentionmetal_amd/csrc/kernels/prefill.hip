@@ -178,9 +178,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
         const uint32_t row_stride = (uint32_t)(p.num_kv_heads * HD);  // halves per pool row (< 2^32)
         const f16 *kpool = static_cast<const f16 *>(p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
         const f16 *vpool = static_cast<const f16 *>(p.v_pool) + (int64_t)kvh * HD + my_piece * 8;
-        // fused append: rows of the chunk's new tokens (same row stride as the pools)
-        const f16 *kin = FUSED ? static_cast<const f16 *>(p.fuse_k) + (int64_t)kvh * HD + my_piece * 8 : nullptr;
-        const f16 *vin = FUSED ? static_cast<const f16 *>(p.fuse_v) + (int64_t)kvh * HD + my_piece * 8 : nullptr;
+        // fused append: rows of the chunk's new tokens have the pools' row stride;
+        // a load of one adds the (uniform) distance from the pool to the input
+        // (in halves; both buffers hold f16, so the byte distance is even)
+        const int64_t kin_d = FUSED ? (int64_t)((uintptr_t)p.fuse_k - (uintptr_t)p.k_pool) / 2 : 0;
+        const int64_t vin_d = FUSED ? (int64_t)((uintptr_t)p.fuse_v - (uintptr_t)p.v_pool) / 2 : 0;
         // two register sets in flight: a tile's rows are loaded two iterations
         // before they are written to LDS
         f16x8 kra[KPT], vra[KPT], krb[KPT], vrb[KPT];
@@ -204,8 +206,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             for (int i = 0; i < KPT; i++) {
                 const uint64_t off = (uint64_t)(slot[i] & 0x7FFFFFFFu) * row_stride;
                 const bool in = FUSED && (slot[i] >> 31);
-                kreg[i] = *reinterpret_cast<const f16x8 *>((in ? kin : kpool) + off);
-                vreg[i] = *reinterpret_cast<const f16x8 *>((in ? vin : vpool) + off);
+                kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off + (in ? kin_d : 0));
+                vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off + (in ? vin_d : 0));
             }
         };
         auto fetch = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
