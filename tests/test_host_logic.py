@@ -339,3 +339,18 @@ def test_fused_prefill_validation(pam, ctx):
                                  0, 0, 0, 0, 0, 0, 0)
     assert pam.pam_engine_fused_prefill(ctx, C.byref(r)) == -1
     assert pam.pam_last_error(ctx)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one MI355X: --gpus N > 1 (or a multi-rank launch) exits
+    with a message before touching the GPU."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "single GPU" in r.stderr
+    env = dict(os.environ, WORLD_SIZE="4")
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py")], capture_output=True, text=True, timeout=120,
+                       env=env)
+    assert r.returncode == 2 and "single GPU" in r.stderr
