@@ -95,18 +95,6 @@ struct KvTraits<uint8_t> {
 
 // ------------------------------------------------------------------ MFMA body
 
-// e4m3 bytes -> their exact binary16 values, two bytes per
-// v_cvt_scalef32_pk_f16_fp8 (scale 1.0; word_sel picks bytes 0-1 or 2-3).  The
-// hardware's OCP e4m3 decoding equals the reference's dequant_fp8 table
-// (kernels.metal:553-562) for every code except 0x7F / 0xFF, which the
-// reference's quantiser never writes (it saturates at 0x7E).
-__device__ __forceinline__ f16x8 e4m3x8_to_f16x8(uint32_t w0, uint32_t w1) {
-    const auto a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
-    const auto b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
-    const auto c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
-    const auto d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
-    return (f16x8){(f16)a[0], (f16)a[1], (f16)b[0], (f16)b[1], (f16)c[0], (f16)c[1], (f16)d[0], (f16)d[1]};
-}
 
 // Waves per workgroup of the MFMA kernels: in the workgroup form they split one
 // partition's tiles and merge in LDS; in the stream-K form they read up to four

@@ -147,7 +147,8 @@ hipError_t launch_stream_read(const void *src, size_t bytes, uint32_t *sink, int
 hipError_t launch_stream_copy(const void *src, void *dst, size_t bytes, int blocks, hipStream_t stream);
 
 // Dense chunked-prefill (MFMA, f16): rows [q_offset, q_offset + T) of one sequence.
-hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream);
+// Dense prefill (MFMA): f16 or e4m3 KV, d = 128; Q and O f16.
+hipError_t launch_prefill_mfma(const AttnParams &p, int32_t dtype, hipStream_t stream);
 // Work list of the dense prefill kernel for chunks {bt_row, q_offset, len,
 // row_base} (host memory).  An item is (chunk, kv head, block of 256 / G query rows)
 // over its key tiles; items are cut into segments so that the `groups`

@@ -33,6 +33,7 @@
 #include <algorithm>
 #include <functional>
 #include <queue>
+#include <type_traits>
 
 #include "kernels.h"
 #include "pam_device.h"
@@ -77,8 +78,11 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
     return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
-template <int HD, int RB, bool FUSED>
+template <int HD, int RB, bool FUSED, typename KV>
 __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(AttnParams p) {
+    // KV: f16 pools, or e4m3 codes (uint8_t) with a half scale per physical block
+    constexpr bool FP8 = sizeof(KV) == 1;
+    static_assert(!(FUSED && FP8), "the fused append is f16 only");
     static_assert(HD == 128, "layouts assume d = 128");
     constexpr int KT = kPrefillKT;
     constexpr int KH = KT / 32;       // 32-key score blocks per tile
@@ -176,16 +180,22 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
         // (16 lanes read one key row's 256 contiguous bytes)
         const int my_piece = tid % PIECES, my_key = tid / PIECES;
         const uint32_t row_stride = (uint32_t)(p.num_kv_heads * HD);  // halves per pool row (< 2^32)
-        const f16 *kpool = static_cast<const f16 *>(p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
-        const f16 *vpool = static_cast<const f16 *>(p.v_pool) + (int64_t)kvh * HD + my_piece * 8;
+        const KV *kpool = static_cast<const KV *>(p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
+        const KV *vpool = static_cast<const KV *>(p.v_pool) + (int64_t)kvh * HD + my_piece * 8;
         // fused append: rows of the chunk's new tokens have the pools' row stride;
         // a load of one adds the (uniform) distance from the pool to the input
         // (in halves; both buffers hold f16, so the byte distance is even)
         const int64_t kin_d = FUSED ? (int64_t)((uintptr_t)p.fuse_k - (uintptr_t)p.k_pool) / 2 : 0;
         const int64_t vin_d = FUSED ? (int64_t)((uintptr_t)p.fuse_v - (uintptr_t)p.v_pool) / 2 : 0;
         // two register sets in flight: a tile's rows are loaded two iterations
-        // before they are written to LDS
-        f16x8 kra[KPT], vra[KPT], krb[KPT], vrb[KPT];
+        // before they are written to LDS.  A thread's piece of a row is 8
+        // elements: 16 bytes of f16, or 8 e4m3 codes plus the block's scales.
+        using Raw = typename std::conditional<FP8, uint2, f16x8>::type;
+        struct Regs {
+            Raw k[KPT], v[KPT];
+            uint32_t ks[KPT], vs[KPT];  // e4m3: half scale bits of the row's block
+        };
+        Regs ra, rb;
         int blk0 = 0;  // first block of the block-table segment held in bt_lds
         // pool row of this thread's key(s) of a tile, then the loads from it
         auto lookup = [&](int tile, uint32_t(&slot)[KPT]) {
@@ -201,19 +211,27 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
                 if (FUSED && j >= ch.y) slot[i] = 0x80000000u | (uint32_t)(ch.w + j - ch.y);
             }
         };
-        auto load = [&](const uint32_t(&slot)[KPT], f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+        auto load = [&](const uint32_t(&slot)[KPT], Regs &r) {
 #pragma unroll
             for (int i = 0; i < KPT; i++) {
-                const uint64_t off = (uint64_t)(slot[i] & 0x7FFFFFFFu) * row_stride;
-                const bool in = FUSED && (slot[i] >> 31);
-                kreg[i] = *reinterpret_cast<const f16x8 *>(kpool + off + (in ? kin_d : 0));
-                vreg[i] = *reinterpret_cast<const f16x8 *>(vpool + off + (in ? vin_d : 0));
+                const uint32_t row = slot[i] & 0x7FFFFFFFu;
+                const uint64_t off = (uint64_t)row * row_stride;
+                if constexpr (FP8) {
+                    r.k[i] = *reinterpret_cast<const uint2 *>(kpool + off);
+                    r.v[i] = *reinterpret_cast<const uint2 *>(vpool + off);
+                    r.ks[i] = p.k_scale[row >> bsh];
+                    r.vs[i] = p.v_scale[row >> bsh];
+                } else {
+                    const bool in = FUSED && (slot[i] >> 31);
+                    r.k[i] = *reinterpret_cast<const f16x8 *>(kpool + off + (in ? kin_d : 0));
+                    r.v[i] = *reinterpret_cast<const f16x8 *>(vpool + off + (in ? vin_d : 0));
+                }
             }
         };
-        auto fetch = [&](int tile, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+        auto fetch = [&](int tile, Regs &r) {
             uint32_t slot[KPT];
             lookup(tile, slot);
-            load(slot, kreg, vreg);
+            load(slot, r);
         };
         int k_st[KPT], v_st[KPT];
 #pragma unroll
@@ -221,11 +239,20 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             k_st[i] = k_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
             v_st[i] = v_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
         }
-        auto stage = [&](int buf, const f16x8(&kreg)[KPT], const f16x8(&vreg)[KPT]) {
+        auto stage = [&](int buf, const Regs &r) {
 #pragma unroll
             for (int i = 0; i < KPT; i++) {
-                *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st[i]]) = kreg[i];
-                *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st[i]]) = vreg[i];
+                if constexpr (FP8) {
+                    // exact code values times the block scale in one binary16
+                    // multiply: the reference's half dequantisation, as in decode
+                    const f16x8 ks8 = (f16x8)bits_to_f16((uint16_t)r.ks[i]);
+                    const f16x8 vs8 = (f16x8)bits_to_f16((uint16_t)r.vs[i]);
+                    *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st[i]]) = e4m3x8_to_f16x8(r.k[i].x, r.k[i].y) * ks8;
+                    *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st[i]]) = e4m3x8_to_f16x8(r.v[i].x, r.v[i].y) * vs8;
+                } else {
+                    *reinterpret_cast<f16x8 *>(&k_lds[buf][k_st[i]]) = r.k[i];
+                    *reinterpret_cast<f16x8 *>(&v_lds[buf][v_st[i]]) = r.v[i];
+                }
             }
         };
 
@@ -348,20 +375,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             __syncthreads();
             // the first four tiles are requested together
             {
-                f16x8 kc[KPT], vc[KPT], kd[KPT], vd[KPT];
-                fetch(seg, kra, vra);
-                fetch(min(seg + 1, seg_end - 1), krb, vrb);
-                fetch(min(seg + 2, seg_end - 1), kc, vc);
-                fetch(min(seg + 3, seg_end - 1), kd, vd);
-                stage(0, kra, vra);
-                stage(1, krb, vrb);
-#pragma unroll
-                for (int i = 0; i < KPT; i++) {
-                    kra[i] = kc[i];
-                    vra[i] = vc[i];
-                    krb[i] = kd[i];
-                    vrb[i] = vd[i];
-                }
+                Regs rc, rd;
+                fetch(seg, ra);
+                fetch(min(seg + 1, seg_end - 1), rb);
+                fetch(min(seg + 2, seg_end - 1), rc);
+                fetch(min(seg + 3, seg_end - 1), rd);
+                stage(0, ra);
+                stage(1, rb);
+                ra = rc;
+                rb = rd;
             }
             __syncthreads();
             if (lag) __syncthreads();
@@ -384,7 +406,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             // MFMAs while they arrive.
             f16x8 ka[KH][DC];
             uint32_t nslot[KPT];
-            auto vphase = [&](int t, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+            auto vphase = [&](int t, Regs &r) {
                 if (t + 1 < T) {
                     const f16 *kt = k_lds[(t + 1) % NBUF];
 #pragma unroll
@@ -421,9 +443,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
                     for (int c = 0; c < 2 * KH; c++) asm volatile("" : "+v"(pb[b][c]));
                     asm volatile("" : "+v"(l_run[b]));
                 }
-                stage((t + 2) % NBUF, kreg, vreg);  // tile t + 2, fetched at M_t-2
+                stage((t + 2) % NBUF, r);  // tile t + 2, fetched at M_t-2
             };
-            auto mphase = [&](int t, f16x8(&kreg)[KPT], f16x8(&vreg)[KPT]) {
+            auto mphase = [&](int t, Regs &r) {
                 const f16 *vt = v_lds[t % NBUF];
                 f16x8 va[2 * KH][DT];
 #pragma unroll
@@ -463,16 +485,16 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
 #pragma unroll
                     for (int e = 0; e < KH; e++) asm volatile("" : "+v"(sacc[b][e]));
                 }
-                load(nslot, kreg, vreg);  // tile t + 4
+                load(nslot, r);  // tile t + 4
             };
             for (int t = 0; t < T; t += 2) {
-                vphase(t, kra, vra);
+                vphase(t, ra);
                 __syncthreads();
-                mphase(t, kra, vra);
+                mphase(t, ra);
                 __syncthreads();
-                vphase(t + 1, krb, vrb);
+                vphase(t + 1, rb);
                 __syncthreads();
-                mphase(t + 1, krb, vrb);
+                mphase(t + 1, rb);
                 __syncthreads();
             }
             if (!lag) __syncthreads();
@@ -567,21 +589,23 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
 }
 
 bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size) {
-    return dtype == kF16 && head_dim == 128 && group >= 1 && group <= 32 && (kPrefillRows % group) == 0 &&
-           block_size > 0 && (block_size & (block_size - 1)) == 0;
+    return (dtype == kF16 || dtype == kFP8) && head_dim == 128 && group >= 1 && group <= 32 &&
+           (kPrefillRows % group) == 0 && block_size > 0 && (block_size & (block_size - 1)) == 0;
 }
 
-hipError_t launch_prefill_mfma(const AttnParams &p, hipStream_t stream) {
-    if (p.pf_work == nullptr || p.pf_range == nullptr || p.pf_groups <= 0)
-        return hipErrorInvalidValue;
+hipError_t launch_prefill_mfma(const AttnParams &p, int32_t dtype, hipStream_t stream) {
+    if (p.pf_work == nullptr || p.pf_range == nullptr || p.pf_groups <= 0) return hipErrorInvalidValue;
     const int G = p.num_heads / p.num_kv_heads;
-    if (!prefill_mfma_supported(kF16, p.head_dim, G, p.block_size)) return hipErrorInvalidValue;
-    if (p.fuse_k != nullptr)
-        hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, true>), dim3(p.pf_groups), dim3(64 * kPrefillWaves),
-                           0, stream, p);
-    else
-        hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, false>), dim3(p.pf_groups), dim3(64 * kPrefillWaves),
-                           0, stream, p);
+    if (!prefill_mfma_supported(dtype, p.head_dim, G, p.block_size)) return hipErrorInvalidValue;
+    const dim3 grid(p.pf_groups), block(64 * kPrefillWaves);
+    if (dtype == kFP8) {
+        if (p.fuse_k != nullptr || p.k_scale == nullptr || p.v_scale == nullptr) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, false, uint8_t>), grid, block, 0, stream, p);
+    } else if (p.fuse_k != nullptr) {
+        hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, true, f16>), grid, block, 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, false, f16>), grid, block, 0, stream, p);
+    }
     return hipGetLastError();
 }
 

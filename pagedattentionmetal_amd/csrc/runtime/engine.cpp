@@ -514,7 +514,7 @@ Context::PrefillPlan Context::plan_prefill(const pam_prefill_request &r) {
 
 void Context::launch_prefill_plan(const PrefillPlan &pl, int32_t dtype) {
     if (pl.dense)
-        check_launch(launch_prefill_mfma(pl.p, stream()), "prefill");
+        check_launch(launch_prefill_mfma(pl.p, dtype, stream()), "prefill");
     else
         check_launch(launch_attention(pl.p, dtype, pl.use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "prefill");
 }
@@ -855,7 +855,7 @@ void Context::mixed_step(const pam_mixed_request &r) {
     with_retry("mixedStep", [&] {
         mark(ev0_);
         if (ab.keys) check_launch(launch_append_batch(ab, l.data_type, stream()), "mixed append");
-        if (!chunks.empty()) check_launch(launch_prefill_mfma(p, stream()), "mixed prefill");
+        if (!chunks.empty()) check_launch(launch_prefill_mfma(p, l.data_type, stream()), "mixed prefill");
         if (ragged_rows > 0)
             check_launch(launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "mixed attention");
         else

@@ -277,6 +277,11 @@ PREFILL_CASES = [
     (200, 64, 64, 8, 128, 32, 1, True, 100),  # G = 8, window cuts inside the chunk
     (97, 13, 16, 8, 128, 16, 1, True, 0),   # G = 2
     (40, 9000, 8, 2, 128, 4, 1, True, 0),   # bs 4: block table streamed through LDS in segments
+    # dense MFMA prefill over e4m3 pools (dequantised as it stages tiles)
+    (300, 1000, 32, 8, 128, 16, 2, True, 0),
+    (200, 64, 64, 8, 128, 32, 2, True, 100),  # G = 8, window cuts inside the chunk
+    (130, 0, 16, 1, 128, 8, 2, True, 0),      # G = 16, bs 8
+    (77, 5, 8, 8, 128, 16, 2, False, 0),      # G = 1, full attention
 ]
 
 
