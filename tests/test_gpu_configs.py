@@ -139,3 +139,66 @@ def test_mixed_step_c3_full_size(torch):
             # prefill restates a chunk at [q_offset, q_offset + 16): its keys end at q_offset + 16 <= total
             e = row_rel_err(got[rows_], ref)
             assert e <= TOL[1], f"chunk {s} rows {i0}..{i0 + 16}: rel err {e:.3e}"
+
+
+def test_mixed_step_c3_full_size_fp8(torch):
+    """The c3 step over e4m3 pools: the cached context is quantised through the
+    append kernel, the step appends the new tokens (FP8 rule) and attends with
+    the dense prefill and the decode rows dequantising as they read.  Decode rows
+    all, prefill chunks on three 16-row slices each, against the oracle on the
+    pools the GPU wrote (compared after dequantisation)."""
+    from pagedattentionmetal_amd import api, workloads
+    w = workloads.mixed_config()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(w.seed)
+    shape = (w.pool_blocks, w.block_size, w.num_kv_heads, w.head_dim)
+    src_k = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
+    src_v = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
+    rows = w.total_rows
+    q = torch.randn((rows, w.num_heads, w.head_dim), generator=g, device="cuda", dtype=torch.float32).half()
+    nk = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
+    nv = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
+    bt = torch.from_numpy(w.block_tables).cuda()
+    bs = w.block_size
+    kp = torch.zeros(shape, dtype=torch.uint8, device="cuda")
+    vp = torch.zeros_like(kp)
+    ks = torch.zeros(w.pool_blocks, dtype=torch.float16, device="cuda")
+    vs = torch.zeros_like(ks)
+    eng = api.PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    lay_kv = api.PagedLayerSpec(w.head_dim, w.num_kv_heads, w.num_kv_heads, bs, 2)
+    for s in range(len(w.context_lens)):
+        L = int(w.context_lens[s])
+        if L == 0:
+            continue
+        tok = torch.arange(L, device="cuda")
+        phys = bt[s][tok // bs].long()
+        eng.append_to_cache(src_k[phys, tok % bs].contiguous(), src_v[phys, tok % bs].contiguous(), kp, vp,
+                            bt[s].contiguous(), 0, L, lay_kv, k_scale=ks, v_scale=vs)
+    out = torch.empty_like(q)
+    layer = api.PagedLayerSpec(w.head_dim, w.num_heads, w.num_kv_heads, bs, 2)
+    eng.mixed_step(q, out, kp, vp, bt, w.context_lens, w.query_lens, layer, new_keys=nk, new_values=nv,
+                   k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+
+    ctx, ql = w.context_lens.astype(np.int64), w.query_lens.astype(np.int64)
+    total = ctx + ql
+    host, cbt = compact_pools(torch, w.block_tables, total, 0, bs, (kp, vp), (ks, vs))
+    kh, vh, ksh, vsh = host
+    ksh, vsh = ksh.view(np.uint16), vsh.view(np.uint16)
+    qh, got = to_host(q), to_host(out)
+    assert np.isfinite(got).all()
+    cu = np.concatenate([[0], np.cumsum(ql)])
+    dec = np.nonzero(ql == 1)[0]
+    ref_dec = oracle.decode(2, qh[cu[dec]], kh, vh, cbt[dec], total[dec].astype(np.uint32), w.num_heads,
+                            k_scale=ksh, v_scale=vsh, n_threads=16)
+    err = row_rel_err(got[cu[dec]], ref_dec)
+    assert err <= TOL[2], f"decode rows: rel err {err:.3e}"
+    for s in np.nonzero(ql > 1)[0]:
+        T = int(ql[s])
+        for i0 in (0, T // 2 - 8, T - 16):
+            rows_ = slice(cu[s] + i0, cu[s] + i0 + 16)
+            ref = oracle.prefill(2, qh[rows_], kh, vh, cbt[s], int(ctx[s]) + i0, causal=True, k_scale=ksh,
+                                 v_scale=vsh, n_threads=16)
+            e = row_rel_err(got[rows_], ref)
+            assert e <= TOL[2], f"chunk {s} rows {i0}..{i0 + 16}: rel err {e:.3e}"
