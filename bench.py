@@ -7,10 +7,11 @@ fp16 ragged decode, B=64, L~U[128,4096], 32 query / 8 KV heads, d=128, bs=16,
 prefill TFLOP/s of the c3 mixed continuous-batching step.  A step is one decode
 of the whole batch with Q, pools and tables already resident in HBM.
 
-  python bench.py [--steps K] [--warmup W] [--no-configs] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--no-configs] [--no-trace] [--no-cpu]
 
 Prints one JSON line.  "configs" holds the c1, c4 and c5 decode lines (skipped
-with --no-configs).  Every configuration carries a CPU baseline: the oracle on
+with --no-configs); "trace_c5" the 200-step scheduler trace of c5 (skipped with
+--no-trace).  Every configuration carries a CPU baseline: the oracle on
 the host's cores over a bounded sample of the same inputs (skipped with
 --no-cpu).  The roofline block times the dominant kernel (the decode attention
 kernel) with HIP events on the stream it is launched on.
@@ -237,6 +238,50 @@ def cpu_baseline_prefill(torch, w3, t3, threads, rows=64, min_seconds=1.0, max_r
     return flops * reps / dt / 1e12, dt, reps, f"rows [{ctx}, {ctx + T}) of a causal prefill at context {ctx} (chunk 0)"
 
 
+def run_trace_c5(torch, api, steps=200, seed=0x5EED0005):
+    """BASELINE c5's serving trace: `steps` ContinuousBatchingScheduler steps with
+    Poisson(2) arrivals, prompts U[64,8192], outputs U[16,512], max batch 32,
+    on the c5 layer (64/8 heads, d=128, bs=16, fp16, 4096-token window) with a
+    block pool of 60% of the GPU's memory.  Each step is one mixed prefill +
+    decode launch set on synthetic Q and K/V."""
+    from pagedattentionmetal_amd.inference import PagedAttentionInference, poisson_trace
+    H, hkv, d, bs, W = 64, 8, 128, 16, 4096
+    _, total = torch.cuda.mem_get_info()
+    blocks = int(0.6 * total / (2 * bs * hkv * d * 2))
+    eng = api.PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    cache = api.KVCacheManager(eng, blocks, bs, d, hkv, 1)
+    sched = api.ContinuousBatchingScheduler(32, 1024)  # maxSequences raised: completed ones still count
+    layer = api.PagedLayerSpec(d, H, hkv, bs, 1, W)
+    inf = PagedAttentionInference(eng, cache, sched, layer, seed=seed)
+    eng.set_stream(torch.cuda.current_stream())
+    gpu_ms = []
+    prev = [0]
+
+    def on_step(i):
+        if inf.prefill_tokens + inf.decoded_tokens != prev[0]:  # the step launched work
+            gpu_ms.append(eng.last_stats["kernel_ms"])
+            prev[0] = inf.prefill_tokens + inf.decoded_tokens
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    admitted = poisson_trace(inf, steps, 2.0, (64, 8192), (16, 512), seed, on_step=on_step)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    tokens = inf.prefill_tokens + inf.decoded_tokens
+    gpu = sum(gpu_ms) * 1e-3
+    out = {"workload": f"c5 trace: {steps} scheduler steps, Poisson(2) arrivals, prompts U[64,8192], outputs "
+                       f"U[16,512], max batch 32, 64/8 heads, d=128, bs=16, fp16, window {W}, pool {blocks} blocks "
+                       f"(60% of HBM); one mixed prefill + decode launch set per step",
+           "requests_admitted": admitted, "completed": inf.completed_count, "preemptions": inf.preemptions,
+           "prefill_tokens": inf.prefill_tokens, "decoded_tokens": inf.decoded_tokens,
+           "wall_s": round(wall, 4), "tokens_per_s_wall": round(tokens / wall, 1),
+           "gpu_s": round(gpu, 4), "tokens_per_s_gpu": round(tokens / gpu, 1) if gpu > 0 else None}
+    del inf, cache, eng
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -246,6 +291,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--all", action="store_true", help="measure c1, c4, c5 too (the default; kept for old command lines)")
     ap.add_argument("--no-configs", action="store_true", help="skip the c1, c4, c5 lines")
+    ap.add_argument("--no-trace", action="store_true", help="skip the c5 scheduler trace")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the 1 GiB read and copy calibration streams (achievable HBM rate; "
@@ -383,6 +429,9 @@ def main():
             del tk, ek
             torch.cuda.empty_cache()
         result["configs"] = cfgs
+    if not args.no_trace:
+        log("bench: c5 scheduler trace")
+        result["trace_c5"] = run_trace_c5(torch, api)
     print(json.dumps(result), flush=True)
 
 

@@ -1,0 +1,209 @@
+"""Serving-loop driver: the semantics of the reference's PagedAttentionInference
+(Sources/PagedAttentionMetal/PagedAttentionInference.swift:119-299) over libpam.
+
+Each ``step()`` takes the scheduler's batch (``ContinuousBatchingScheduler.step``,
+Scheduler.swift:78-114) and splits it, as ``step`` does (:119-149), into
+newcomers and sequences already prefilled:
+
+* newcomers (``handlePrefill``, :172-219): blocks for the prompt are made
+  available (preempting under memory pressure), the sequence is (re)allocated
+  and its prompt tokens appended to the cache manager;
+* prefilled sequences (``handleDecode``, :221-278): the blocks one more token
+  needs are made available, and after the attention each gets one token, is
+  marked decoded and is completed (its blocks freed) once done;
+* ``ensureBlocksAvailable`` (:280-299): the scheduler's memory-pressure handler
+  pauses running sequences, newest first, until enough blocks are free, then
+  their blocks are released and they must be prefilled again later.
+
+The attention of a step runs as ONE ``mixed_step`` launch set: the newcomers'
+prompts as causal prefill chunks and the prefilled sequences as single-token
+decode rows, with synthetic new K/V appended at their positions (the
+reference issues a prefill per newcomer and then one batched decode, on
+uninitialised Q buffers and without writing K/V).  Sequences the step
+preempts are left out of its launch (the reference would still decode them
+from freed blocks).  Q and the new K/V are synthetic: there is no model.
+
+With a sliding window W, a prompt longer than W has one window start,
+len - W, for all its rows (the reference's prefill window), so its first
+len - W rows attend to no key and come out 0/0 (NaN), as the reference's do.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .api import KVCacheManager, ContinuousBatchingScheduler, PagedAttentionEngine, PagedAttentionError, \
+    PagedLayerSpec
+
+
+class OutOfBlocks(PagedAttentionError):
+    """KVCacheError.outOfMemory raised by ensureBlocksAvailable (PagedAttentionInference.swift:295-297)."""
+
+
+class PagedAttentionInference:
+    def __init__(self, engine: PagedAttentionEngine, cache: KVCacheManager, scheduler: ContinuousBatchingScheduler,
+                 layer: PagedLayerSpec, attend: bool = True, seed: int = 0):
+        """`attend=False` keeps the bookkeeping only (no GPU work), for host tests."""
+        self.engine = engine
+        self.cache = cache
+        self.scheduler = scheduler
+        self.layer = layer
+        self.attend = attend
+        self.prefilled: set[int] = set()
+        self.step_count = 0
+        self.total_tokens_generated = 0  # prompt tokens prefilled + decoded tokens, as the reference counts
+        self.decoded_tokens = 0
+        self.prefill_tokens = 0
+        self.preemptions = 0
+        self._rng = np.random.default_rng(seed)
+        self._buf_rows = 0
+        self._max_new: dict[int, int] = {}
+        self.last_launch = None  # (context lengths, query lengths) of the last mixed_step, rows in that order
+
+    # --- requests (PagedAttentionInference.swift:100-113)
+    def add_request(self, prompt_token_count: int, max_new_tokens: int) -> int:
+        """-1 when the scheduler holds max_sequences sequences (Scheduler.swift:59-70)."""
+        sid = self.scheduler.add_request(prompt_token_count, max_new_tokens)
+        if sid >= 0:
+            self._max_new[sid] = max_new_tokens
+        return sid
+
+    def complete_sequence(self, sid: int):
+        self.scheduler.complete_sequence(sid)
+        self.cache.free_sequence(sid)
+        self.prefilled.discard(sid)
+
+    @property
+    def waiting_count(self):
+        return self.scheduler.waiting_count
+
+    @property
+    def running_count(self):
+        return self.scheduler.running_count
+
+    @property
+    def completed_count(self):
+        return self.scheduler.completed_count
+
+    # --- one step (PagedAttentionInference.swift:119-149)
+    def step(self):
+        batch = self.scheduler.step()
+        if not batch:
+            return []
+        newcomers = [s for s in batch if s not in self.prefilled]
+        decoding = [s for s in batch if s in self.prefilled]
+        bs = self.cache.block_size
+        dropped: set[int] = set()
+
+        prompts = {}
+        for sid in newcomers:  # handlePrefill's block work (:172-186)
+            prompt = self.scheduler.sequence(sid)["prompt"]
+            dropped |= self._ensure_blocks((prompt + bs - 1) // bs)
+            try:
+                self.cache.allocate_sequence(sid)
+            except PagedAttentionError:
+                self.cache.free_sequence(sid)
+                self.cache.allocate_sequence(sid)
+            self.cache.append_tokens(sid, prompt)
+            prompts[sid] = prompt
+
+        decoding = [s for s in decoding if s not in dropped]
+        lens = {sid: self.cache.get_sequence_length(sid) for sid in decoding}
+        extras = sum((L + 1 + bs - 1) // bs - (L + bs - 1) // bs for L in lens.values())
+        if extras > 0:  # handleDecode (:225-233)
+            dropped |= self._ensure_blocks(extras)
+        newcomers = [s for s in newcomers if s not in dropped]
+        decoding = [s for s in decoding if s not in dropped]
+        for sid in decoding:
+            self.cache.append_tokens(sid, 1)  # the new token's slot, written by the step
+
+        if self.attend and (newcomers or decoding):
+            self._launch(newcomers, decoding, prompts, lens)
+
+        for sid in newcomers:  # :205-217
+            self.scheduler.mark_prefilled(sid)
+            self.prefilled.add(sid)
+            self.total_tokens_generated += prompts[sid]
+            self.prefill_tokens += prompts[sid]
+        for sid in decoding:  # :260-276
+            self.scheduler.mark_decoded(sid)
+            self.total_tokens_generated += 1
+            self.decoded_tokens += 1
+            info = self.scheduler.sequence(sid)
+            if info["generated"] >= self._max_new[sid]:  # SchedulerSequence.isDone
+                self.complete_sequence(sid)
+        self.step_count += 1
+        return batch
+
+    def run_all(self, max_steps: int = 1 << 30):
+        """runAll (:151-157): steps while some sequence is waiting or running, so
+        it returns when only paused (preempted) sequences are left, as the
+        reference's does."""
+        while (self.waiting_count > 0 or self.running_count > 0) and max_steps > 0:
+            if not self.step():
+                break
+            max_steps -= 1
+
+    # --- internals
+    def _ensure_blocks(self, needed: int) -> set:
+        """ensureBlocksAvailable (:280-299): returns the sequences it preempted."""
+        if self.cache.available_blocks >= needed:
+            return set()
+        victims = self.scheduler.handle_memory_pressure(needed, self.cache)
+        for pid in victims:
+            self.cache.free_sequence(pid)
+            self.prefilled.discard(pid)
+        self.preemptions += len(victims)
+        if self.cache.available_blocks < needed:
+            raise OutOfBlocks(f"{needed} blocks needed, {self.cache.available_blocks} available")
+        return set(victims)
+
+    def _buffers(self, rows):
+        import torch
+        L = self.layer
+        if rows > self._buf_rows:
+            n = max(rows, 2 * self._buf_rows, 4096)
+            g = torch.Generator(device="cuda")
+            g.manual_seed(int(self._rng.integers(1 << 31)))
+            self._q = torch.randn((n, L.num_heads, L.head_dim), generator=g, device="cuda", dtype=torch.float16)
+            self._out = torch.empty_like(self._q)
+            self._nk = torch.randn((n, L.num_kv_heads, L.head_dim), generator=g, device="cuda",
+                                   dtype=torch.float16).mul_(0.5)
+            self._nv = torch.randn_like(self._nk).mul_(0.5)
+            self._buf_rows = n
+        return self._q[:rows], self._out[:rows], self._nk[:rows], self._nv[:rows]
+
+    def _launch(self, newcomers, decoding, prompts, lens):
+        import torch
+        ids = newcomers + decoding
+        ctx = np.array([0] * len(newcomers) + [lens[s] for s in decoding], np.int32)
+        ql = np.array([prompts[s] for s in newcomers] + [1] * len(decoding), np.int32)
+        bs = self.cache.block_size
+        width = int(((ctx + ql + bs - 1) // bs).max())
+        bt = torch.zeros((len(ids), width), dtype=torch.int32, device="cuda")
+        sl = torch.zeros(len(ids), dtype=torch.int32, device="cuda")
+        self.cache.batch_view(ids, bt, sl, width)
+        rows = int(ql.sum())
+        self.last_launch = (ctx, ql)
+        q, out, nk, nv = self._buffers(rows)
+        c = self.cache
+        self.engine.mixed_step(q, out, c.k_pool(), c.v_pool(), bt, ctx, ql, self.layer, new_keys=nk, new_values=nv,
+                               k_scale=c.k_scale(), v_scale=c.v_scale())
+
+
+def poisson_trace(inference: PagedAttentionInference, steps: int, rate: float, prompt_range, output_range,
+                  seed: int, on_step=None):
+    """The BASELINE c5 driver: `steps` scheduler steps with Poisson(`rate`) arrivals
+    before each, prompts and output lengths uniform over the given inclusive
+    ranges.  Returns the number of requests admitted."""
+    rng = np.random.default_rng(seed)
+    admitted = 0
+    for i in range(steps):
+        for _ in range(int(rng.poisson(rate))):
+            prompt = int(rng.integers(prompt_range[0], prompt_range[1] + 1))
+            out = int(rng.integers(output_range[0], output_range[1] + 1))
+            if inference.add_request(prompt, out) >= 0:
+                admitted += 1
+        inference.step()
+        if on_step is not None:
+            on_step(i)
+    return admitted

@@ -1,0 +1,97 @@
+"""The serving-loop driver (inference.py), the semantics of the reference's
+PagedAttentionInference (PagedAttentionInference.swift:119-299) over the native
+scheduler and cache manager.
+
+CPU: bookkeeping with a host-only cache and a pool small enough to force the
+scheduler's memory-pressure preemption (which pauses every running sequence,
+Scheduler.swift:135-152), run to completion.  GPU: a short Poisson trace whose
+steps run as mixed prefill + decode launches on the real pools.
+"""
+import numpy as np
+import pytest
+
+from pagedattentionmetal_amd.api import SequenceStatus
+
+
+def _driver(max_blocks, max_batch=8, max_sequences=64, attend=False, layer_kw=None):
+    from pagedattentionmetal_amd import api
+    from pagedattentionmetal_amd.inference import PagedAttentionInference
+    kw = dict(head_dim=128, num_heads=8, num_kv_heads=2, block_size=16, data_type=1)
+    kw.update(layer_kw or {})
+    eng = api.PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    cache = api.KVCacheManager(eng, max_blocks, kw["block_size"], kw["head_dim"], kw["num_kv_heads"],
+                               kw["data_type"], device=attend)
+    sched = api.ContinuousBatchingScheduler(max_batch, max_sequences)
+    layer = api.PagedLayerSpec(kw["head_dim"], kw["num_heads"], kw["num_kv_heads"], kw["block_size"],
+                               kw["data_type"], kw.get("window", 0))
+    return PagedAttentionInference(eng, cache, sched, layer, attend=attend), cache, sched
+
+
+def test_driver_preempts_under_pressure_and_completes():
+    inf, cache, sched = _driver(max_blocks=40)
+    a = inf.add_request(300, 40)  # 19 blocks each: two fit in 40, their growth (22 each) does not
+    b = inf.add_request(300, 40)
+    assert (a, b) == (0, 1)
+    # runAll (PagedAttentionInference.swift:151-157) stops once no sequence is
+    # waiting or running: the pressure event pauses both, and it returns
+    inf.run_all(max_steps=500)
+    assert inf.preemptions == 2 and inf.completed_count == 0
+    assert sched.count(SequenceStatus.paused) == 2
+    # stepping on resumes the paused sequences (re-prefilled) until they finish
+    for _ in range(500):
+        if not inf.step():
+            break
+    assert inf.completed_count == 2 and inf.waiting_count == 0 and inf.running_count == 0
+    assert cache.available_blocks == 40  # every block returned
+    assert inf.decoded_tokens == 80  # 40 per request; re-prefills keep the generated count
+    # every prefill (first ones and the re-prefills after preemption) counts its prompt
+    assert inf.prefill_tokens % 300 == 0 and inf.prefill_tokens >= 600
+    assert inf.total_tokens_generated == inf.prefill_tokens + inf.decoded_tokens
+
+
+def test_driver_rejects_past_max_sequences():
+    inf, cache, sched = _driver(max_blocks=100, max_sequences=2)
+    assert inf.add_request(10, 2) == 0 and inf.add_request(10, 2) == 1
+    assert inf.add_request(10, 2) == -1  # Scheduler.swift:59-70: completed ones still count
+    inf.run_all()
+    assert inf.completed_count == 2
+    assert inf.add_request(10, 2) == -1
+
+
+def test_driver_out_of_blocks_for_a_prompt_that_cannot_fit():
+    from pagedattentionmetal_amd.inference import OutOfBlocks
+    inf, cache, sched = _driver(max_blocks=4)
+    inf.add_request(200, 3)  # 13 blocks
+    with pytest.raises(OutOfBlocks):
+        inf.step()
+
+
+@pytest.mark.gpu
+def test_poisson_trace_on_the_gpu():
+    W = 256
+    import torch
+    from pagedattentionmetal_amd.inference import poisson_trace
+    inf, cache, sched = _driver(max_blocks=600, max_batch=16, max_sequences=256, attend=True,
+                                layer_kw=dict(num_heads=32, num_kv_heads=8, window=W))
+    checked = []
+
+    def on_step(i):
+        # every row is finite except a prompt's first len - W rows, which see no key under the
+        # prefill's single window start len - W (kernels.metal:116-154)
+        if inf.last_launch is None:
+            return
+        ctx, ql = inf.last_launch
+        o = inf._out[:int(ql.sum())].float()
+        nan_rows = torch.isnan(o).any(-1).any(-1).cpu().numpy()
+        want = np.concatenate([np.arange(q) < (q - W if c == 0 else 0) for c, q in zip(ctx, ql)])
+        assert (nan_rows == want).all(), (i, ctx, ql)
+        assert torch.isfinite(o[torch.from_numpy(~want).cuda()]).all()
+        checked.append(i)
+
+    admitted = poisson_trace(inf, steps=40, rate=2.0, prompt_range=(16, 700), output_range=(4, 24), seed=3,
+                             on_step=on_step)
+    assert admitted > 40 and 30 < inf.step_count <= 40  # an empty batch is not a step (PagedAttentionInference.swift:120)
+    assert inf.decoded_tokens > 0 and inf.prefill_tokens > 0 and inf.completed_count > 0
+    assert len(checked) > 30
+    assert inf.preemptions > 0  # the pool was sized to force it
