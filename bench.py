@@ -292,6 +292,8 @@ def main():
     ap.add_argument("--all", action="store_true", help="measure c1, c4, c5 too (the default; kept for old command lines)")
     ap.add_argument("--no-configs", action="store_true", help="skip the c1, c4, c5 lines")
     ap.add_argument("--no-trace", action="store_true", help="skip the c5 scheduler trace")
+    ap.add_argument("--trace-only", action="store_true",
+                    help="run only the c5 scheduler trace and print its JSON object (for profiling it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the 1 GiB read and copy calibration streams (achievable HBM rate; "
@@ -307,6 +309,9 @@ def main():
     from pagedattentionmetal_amd import api, workloads
 
     torch.cuda.set_device(0)
+    if args.trace_only:
+        print(json.dumps({"trace_c5": run_trace_c5(torch, api)}), flush=True)
+        return
     log("bench: c2 decode setup")
     w, eng, t = decode_setup(2, torch, api, workloads)
     ms, kern_ms, red_ms = time_decode(torch, eng, w, t, args.steps, args.warmup)
