@@ -259,6 +259,25 @@ def test_decode_empty_sequence_is_nan(engine):
     assert np.isnan(o[0]).all() and np.isfinite(o[1]).all()
 
 
+@pytest.mark.gpu
+def test_sim_example_through_the_engine(engine):
+    """The sim's seeded example (Reference/paged_attention_sim.py:141-238): 8 query
+    rows over 8 keys in physical blocks [3, 7] of 4 tokens, d = 8, unscaled and
+    non-causal.  The f32 prefill (scale 1/sqrt(d), so q is passed times sqrt(d))
+    matches the sim restatement within the sim's own 1e-5."""
+    import torch
+    from test_oracle import sim_main_fixture
+    q, kp, vp, bt, bs = sim_main_fixture()
+    S, d = q.shape
+    ref, _, _ = oracle.sim_forward(q, kp, vp, bt, bs)
+    qs = (q.astype(np.float64) * np.sqrt(d)).astype(np.float32).reshape(S, 1, d)
+    out = torch.zeros((S, 1, d), dtype=torch.float32, device="cuda")
+    engine.prefill(to_dev(qs), to_dev(kp.reshape(16, bs, 1, d)), to_dev(vp.reshape(16, bs, 1, d)), to_dev(bt), out,
+                   S, layer(1, 1, d, bs, 0), causal=False)
+    o = to_host(out).reshape(S, d).astype(np.float64)
+    assert np.abs(o - ref).max() < 1e-5
+
+
 # ---------------------------------------------------------------- prefill rows
 
 PREFILL_CASES = [

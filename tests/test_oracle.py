@@ -172,13 +172,24 @@ def test_append_fp8_per_block_scales():
 
 # ---------------------------------------------------------------- attention
 
-def test_sim_matches_dense_attention_and_histories():
-    rng = np.random.default_rng(42)
+def sim_main_fixture():
+    """The inputs of the sim's own example (Reference/paged_attention_sim.py:141-178):
+    numpy's legacy generator seeded with 42, drawn in the same order (q, then the
+    K pool, then the V pool), 16 physical blocks of 4 tokens, d = 8, table [3, 7]."""
+    rs = np.random.RandomState(42)
     S, bs, d = 8, 4, 8
-    q = rng.standard_normal((S, d)).astype(np.float32)
-    kp = rng.standard_normal((16, bs, d)).astype(np.float32)
-    vp = rng.standard_normal((16, bs, d)).astype(np.float32)
-    bt = np.array([3, 7], np.int32)
+    q = rs.randn(S, d).astype(np.float32)
+    kp = rs.randn(16, bs, d).astype(np.float32)
+    vp = rs.randn(16, bs, d).astype(np.float32)
+    return q, kp, vp, np.array([3, 7], np.int32), bs
+
+
+def test_sim_matches_dense_attention_and_histories():
+    """The sim's self-check on its own seeded example (:204-236): the paged result
+    equals dense softmax(q k^T) v (threshold 1e-5 there; fp64 here), and the m/l
+    histories equal the running max and sum after each logical block."""
+    q, kp, vp, bt, bs = sim_main_fixture()
+    S = q.shape[0]
     out, mh, lh = oracle.sim_forward(q, kp, vp, bt, bs)
     keys = np.concatenate([kp[3], kp[7]]).astype(np.float64)
     vals = np.concatenate([vp[3], vp[7]]).astype(np.float64)
