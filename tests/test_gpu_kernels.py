@@ -284,6 +284,7 @@ PREFILL_CASES = [
     # T, q_offset, H, Hkv, d, bs, dtype, causal, window
     (16, 0, 4, 2, 64, 16, 0, False, 0),   # reference fusedPrefill / fp8Quantization shapes (f32)
     (8, 0, 1, 1, 32, 16, 0, True, 0),     # causalMasking shape
+    (16, 0, 1, 1, 64, 16, 0, False, 0),   # correctnessVsCPU shape (Tests/...Tests.swift:70-120)
     (64, 0, 32, 8, 128, 16, 1, True, 0),
     (40, 100, 32, 8, 128, 16, 1, True, 0),  # chunk with cached context
     (33, 17, 8, 8, 128, 8, 0, True, 0),
