@@ -243,43 +243,62 @@ def run_trace_c5(torch, api, steps=200, seed=0x5EED0005):
     Poisson(2) arrivals, prompts U[64,8192], outputs U[16,512], max batch 32,
     on the c5 layer (64/8 heads, d=128, bs=16, fp16, 4096-token window) with a
     block pool of 60% of the GPU's memory.  Each step is one mixed prefill +
-    decode launch set on synthetic Q and K/V."""
+    decode launch set on synthetic Q and K/V.
+
+    Two passes over the same seeded trace: the first in the engine's default
+    synchronous mode with per-call HIP events (GPU time per step); the second
+    as a serving loop runs, asynchronous and without events, for the
+    wall-clock rate (host scheduling overlapping the GPU)."""
+    import gc
     from pagedattentionmetal_amd.inference import PagedAttentionInference, poisson_trace
     H, hkv, d, bs, W = 64, 8, 128, 16, 4096
     _, total = torch.cuda.mem_get_info()
     blocks = int(0.6 * total / (2 * bs * hkv * d * 2))
-    eng = api.PagedAttentionEngine()
-    eng.set_graceful_degradation(False)
-    cache = api.KVCacheManager(eng, blocks, bs, d, hkv, 1)
-    sched = api.ContinuousBatchingScheduler(32, 1024)  # maxSequences raised: completed ones still count
-    layer = api.PagedLayerSpec(d, H, hkv, bs, 1, W)
-    inf = PagedAttentionInference(eng, cache, sched, layer, seed=seed)
-    eng.set_stream(torch.cuda.current_stream())
-    gpu_ms = []
-    prev = [0]
 
-    def on_step(i):
-        if inf.prefill_tokens + inf.decoded_tokens != prev[0]:  # the step launched work
-            gpu_ms.append(eng.last_stats["kernel_ms"])
-            prev[0] = inf.prefill_tokens + inf.decoded_tokens
+    def one_pass(timed):
+        eng = api.PagedAttentionEngine()
+        eng.set_graceful_degradation(False)
+        eng.set_stream(torch.cuda.current_stream())
+        if not timed:
+            eng.synchronous = False
+            eng.set_gpu_timing(False)
+        cache = api.KVCacheManager(eng, blocks, bs, d, hkv, 1)
+        sched = api.ContinuousBatchingScheduler(32, 1024)  # maxSequences raised: completed ones still count
+        inf = PagedAttentionInference(eng, cache, sched, api.PagedLayerSpec(d, H, hkv, bs, 1, W), seed=seed)
+        gpu_ms = []
+        seen = [None]
 
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    admitted = poisson_trace(inf, steps, 2.0, (64, 8192), (16, 512), seed, on_step=on_step)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    tokens = inf.prefill_tokens + inf.decoded_tokens
-    gpu = sum(gpu_ms) * 1e-3
-    out = {"workload": f"c5 trace: {steps} scheduler steps, Poisson(2) arrivals, prompts U[64,8192], outputs "
-                       f"U[16,512], max batch 32, 64/8 heads, d=128, bs=16, fp16, window {W}, pool {blocks} blocks "
-                       f"(60% of HBM); one mixed prefill + decode launch set per step",
-           "requests_admitted": admitted, "completed": inf.completed_count, "preemptions": inf.preemptions,
-           "prefill_tokens": inf.prefill_tokens, "decoded_tokens": inf.decoded_tokens,
-           "wall_s": round(wall, 4), "tokens_per_s_wall": round(tokens / wall, 1),
-           "gpu_s": round(gpu, 4), "tokens_per_s_gpu": round(tokens / gpu, 1) if gpu > 0 else None}
-    del inf, cache, eng
-    torch.cuda.empty_cache()
-    return out
+        def on_step(i):
+            if timed and inf.last_launch is not seen[0]:  # the step launched work
+                gpu_ms.append(eng.last_stats["kernel_ms"])
+                seen[0] = inf.last_launch
+
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        admitted = poisson_trace(inf, steps, 2.0, (64, 8192), (16, 512), seed, on_step=on_step)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        res = dict(admitted=admitted, completed=inf.completed_count, preemptions=inf.preemptions,
+                   prefill=inf.prefill_tokens, decoded=inf.decoded_tokens, wall=wall, gpu=sum(gpu_ms) * 1e-3)
+        inf = None
+        cache.close()
+        eng.close()
+        gc.collect()
+        torch.cuda.empty_cache()
+        return res
+
+    a = one_pass(True)
+    b = one_pass(False)
+    assert (a["prefill"], a["decoded"], a["preemptions"]) == (b["prefill"], b["decoded"], b["preemptions"])
+    tokens = b["prefill"] + b["decoded"]
+    return {"workload": f"c5 trace: {steps} scheduler steps, Poisson(2) arrivals, prompts U[64,8192], outputs "
+                        f"U[16,512], max batch 32, 64/8 heads, d=128, bs=16, fp16, window {W}, pool {blocks} blocks "
+                        f"(60% of HBM); one mixed prefill + decode launch set per step",
+            "requests_admitted": b["admitted"], "completed": b["completed"], "preemptions": b["preemptions"],
+            "prefill_tokens": b["prefill"], "decoded_tokens": b["decoded"],
+            "wall_s": round(b["wall"], 4), "tokens_per_s_wall": round(tokens / b["wall"], 1),
+            "wall_s_synchronous": round(a["wall"], 4),
+            "gpu_s": round(a["gpu"], 4), "tokens_per_s_gpu": round(tokens / a["gpu"], 1) if a["gpu"] > 0 else None}
 
 
 def main():
