@@ -353,7 +353,7 @@ def main():
     if not args.no_cpu:
         threads = max(1, min(16, os.cpu_count() or 1))
         log("bench: CPU baseline for the c3 prefill rows")
-        ctf, cdt, creps, what = cpu_baseline_prefill(torch, w3, t3, threads)
+        ctf, cdt, creps, what = cpu_baseline_prefill(torch, w3, t3, threads, min_seconds=5.0, max_reps=100)
         cpu3 = {"value": round(ctf, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
                 "sample": f"{creps} x {what} through the C oracle on {threads} host threads, {cdt:.2f} s"}
     del t3, e3
@@ -369,7 +369,7 @@ def main():
     if not args.no_cpu:
         threads = max(1, min(16, os.cpu_count() or 1))
         log(f"bench: CPU baseline (oracle, {threads} threads) on the full c2 batch")
-        cgbs, cdt, creps = cpu_baseline_decode(torch, w, t, threads)
+        cgbs, cdt, creps = cpu_baseline_decode(torch, w, t, threads, min_seconds=10.0, max_reps=200)
         log(f"bench: CPU baseline single-threaded on the first 8 sequences")
         sgbs, sdt, sreps = cpu_baseline_decode(torch, w, t, 1, batch=8)
         cpu = {"value": round(cgbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
