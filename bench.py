@@ -279,7 +279,8 @@ def run_trace_c5(torch, api, steps=200, seed=0x5EED0005):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         res = dict(admitted=admitted, completed=inf.completed_count, preemptions=inf.preemptions,
-                   prefill=inf.prefill_tokens, decoded=inf.decoded_tokens, wall=wall, gpu=sum(gpu_ms) * 1e-3)
+                   prefill=inf.prefill_tokens, decoded=inf.decoded_tokens, wall=wall, gpu=sum(gpu_ms) * 1e-3,
+                   flops=4 * d * H * inf.attended_pairs)
         inf = None
         cache.close()
         eng.close()
@@ -298,7 +299,10 @@ def run_trace_c5(torch, api, steps=200, seed=0x5EED0005):
             "prefill_tokens": b["prefill"], "decoded_tokens": b["decoded"],
             "wall_s": round(b["wall"], 4), "tokens_per_s_wall": round(tokens / b["wall"], 1),
             "wall_s_synchronous": round(a["wall"], 4),
-            "gpu_s": round(a["gpu"], 4), "tokens_per_s_gpu": round(tokens / a["gpu"], 1) if a["gpu"] > 0 else None}
+            "gpu_s": round(a["gpu"], 4), "tokens_per_s_gpu": round(tokens / a["gpu"], 1) if a["gpu"] > 0 else None,
+            # 4 d H flops per unmasked (row, key) pair over all the steps' kernels (append and decode included)
+            "attention_flops": a["flops"],
+            "attention_tflops_gpu": round(a["flops"] / a["gpu"] / 1e12, 1) if a["gpu"] > 0 else None}
 
 
 def main():

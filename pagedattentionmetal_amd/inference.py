@@ -58,6 +58,7 @@ class PagedAttentionInference:
         self._buf_rows = 0
         self._max_new: dict[int, int] = {}
         self.last_launch = None  # (context lengths, query lengths) of the last mixed_step, rows in that order
+        self.attended_pairs = 0  # unmasked (query row, key) pairs per head launched so far
 
     # --- requests (PagedAttentionInference.swift:100-113)
     def add_request(self, prompt_token_count: int, max_new_tokens: int) -> int:
@@ -157,6 +158,19 @@ class PagedAttentionInference:
             raise OutOfBlocks(f"{needed} blocks needed, {self.cache.available_blocks} available")
         return set(victims)
 
+    def _pairs(self, ctx, ql) -> int:
+        """Unmasked (query row, key) pairs per head of a mixed step: a chunk's rows
+        see keys from its one window start max(0, ctx + T - W) up to their own
+        position; a decode row sees its last min(L + 1, W) keys."""
+        W = self.layer.window_size
+        n = 0
+        for c, q in zip(ctx.tolist(), ql.tolist()):
+            kv = c + q
+            ws = max(0, kv - W) if W > 0 else 0
+            for_rows = (max(0, kv - ws) * (max(0, kv - ws) + 1) - max(0, c - ws) * (max(0, c - ws) + 1)) // 2
+            n += for_rows
+        return n
+
     def _buffers(self, rows):
         import torch
         L = self.layer
@@ -184,6 +198,7 @@ class PagedAttentionInference:
         self.cache.batch_view(ids, bt, sl, width)
         rows = int(ql.sum())
         self.last_launch = (ctx, ql)
+        self.attended_pairs += self._pairs(ctx, ql)
         q, out, nk, nv = self._buffers(rows)
         c = self.cache
         self.engine.mixed_step(q, out, c.k_pool(), c.v_pool(), bt, ctx, ql, self.layer, new_keys=nk, new_values=nv,

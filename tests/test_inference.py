@@ -95,3 +95,21 @@ def test_poisson_trace_on_the_gpu():
     assert inf.decoded_tokens > 0 and inf.prefill_tokens > 0 and inf.completed_count > 0
     assert len(checked) > 30
     assert inf.preemptions > 0  # the pool was sized to force it
+
+
+def test_attended_pairs_match_brute_force():
+    """The pair count of a mixed step equals an enumeration of the masks: a chunk's
+    rows see keys from its one window start max(0, ctx + T - W) up to their own
+    position (causal), a decode row its last min(L + 1, W) keys."""
+    rng = np.random.default_rng(5)
+    for W in (0, 1, 7, 64):
+        inf, _, _ = _driver(max_blocks=8, layer_kw=dict(window=W))
+        ctx = rng.integers(0, 100, 12).astype(np.int32)
+        ql = rng.integers(1, 90, 12).astype(np.int32)
+        ql[::3] = 1
+        want = 0
+        for c, q in zip(ctx.tolist(), ql.tolist()):
+            kv = c + q
+            ws = max(0, kv - W) if W else 0
+            want += sum(1 for p in range(c, kv) for j in range(kv) if ws <= j <= p)
+        assert inf._pairs(ctx, ql) == want
