@@ -182,7 +182,8 @@ class PagedAttentionInference:
             self._out = torch.empty_like(self._q)
             self._nk = torch.randn((n, L.num_kv_heads, L.head_dim), generator=g, device="cuda",
                                    dtype=torch.float16).mul_(0.5)
-            self._nv = torch.randn_like(self._nk).mul_(0.5)
+            self._nv = torch.randn((n, L.num_kv_heads, L.head_dim), generator=g, device="cuda",
+                                   dtype=torch.float16).mul_(0.5)
             self._buf_rows = n
         return self._q[:rows], self._out[:rows], self._nk[:rows], self._nv[:rows]
 

@@ -113,3 +113,27 @@ def test_attended_pairs_match_brute_force():
             ws = max(0, kv - W) if W else 0
             want += sum(1 for p in range(c, kv) for j in range(kv) if ws <= j <= p)
         assert inf._pairs(ctx, ql) == want
+
+
+@pytest.mark.gpu
+def test_asynchronous_serving_loop_matches_synchronous():
+    """The serving loop with the engine asynchronous and untimed (as bench.py's
+    wall-clock pass runs it) gives the same bookkeeping and the same outputs of
+    its last step as the synchronous, timed default."""
+    import torch
+    from pagedattentionmetal_amd.inference import poisson_trace
+    res = []
+    for asynchronous in (False, True):
+        inf, cache, sched = _driver(max_blocks=600, max_batch=16, max_sequences=256, attend=True,
+                                    layer_kw=dict(num_heads=32, num_kv_heads=8, window=0))
+        if asynchronous:
+            inf.engine.synchronous = False
+            inf.engine.set_gpu_timing(False)
+        poisson_trace(inf, steps=25, rate=2.0, prompt_range=(16, 500), output_range=(4, 16), seed=11)
+        torch.cuda.synchronize()
+        rows = int(inf.last_launch[1].sum())
+        res.append((inf.prefill_tokens, inf.decoded_tokens, inf.preemptions, inf.completed_count,
+                    inf._out[:rows].float().cpu()))
+        inf.engine.synchronize()
+    assert res[0][:4] == res[1][:4]
+    assert torch.isfinite(res[0][4]).all() and torch.equal(res[0][4], res[1][4])
