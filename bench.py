@@ -318,6 +318,8 @@ def main():
     ap.add_argument("--trace-only", action="store_true",
                     help="run only the c5 scheduler trace and print its JSON object (for profiling it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=("c1", "c2", "c3", "c4", "c5"),
+                    help="time one configuration alone and print its JSON object (for profiling it)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the 1 GiB read and copy calibration streams (achievable HBM rate; "
                          "the byte counters of a profiling run are scaled by what they read on these)")
@@ -334,6 +336,19 @@ def main():
     torch.cuda.set_device(0)
     if args.trace_only:
         print(json.dumps({"trace_c5": run_trace_c5(torch, api)}), flush=True)
+        return
+    if args.only == "c3":
+        w3, e3, t3 = mixed_setup(torch, api, workloads)
+        ms3, pk_ms = time_mixed(torch, e3, w3, t3, args.steps, args.warmup)
+        print(json.dumps({"c3": {"mixed_step_ms": round(ms3, 5), "prefill_kernel_ms": round(pk_ms, 5),
+                                 "tflops": round(w3.prefill_flops() / (pk_ms * 1e-3) / 1e12, 2)}}), flush=True)
+        return
+    if args.only:
+        k = int(args.only[1])
+        wk, ek, tk = decode_setup(k, torch, api, workloads)
+        msk, kk, rk = time_decode(torch, ek, wk, tk, args.steps, args.warmup)
+        print(json.dumps({args.only: {"ms_per_step": round(msk, 5), "kernel_ms": round(kk, 5),
+                                      "kv_GBps": round(wk.kv_bytes() / (msk * 1e-3) / 1e9, 2)}}), flush=True)
         return
     log("bench: c2 decode setup")
     w, eng, t = decode_setup(2, torch, api, workloads)

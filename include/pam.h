@@ -341,6 +341,11 @@ typedef struct pam_mixed_request {
     const int32_t *context_lens;
     const int32_t *query_lens;
     pam_layer_spec layer;
+    /* buffer lengths in bytes (0 skips that buffer's check): q and output need
+     * total_rows rows, new K/V total_rows token rows, block_tables num_seqs rows of
+     * bt_stride entries, each pool at least as many blocks as the longest
+     * sequence spans (the decode request's check) */
+    size_t q_bytes, output_bytes, new_keys_bytes, new_values_bytes, k_pool_bytes, v_pool_bytes, block_tables_bytes;
 } pam_mixed_request;
 int32_t pam_engine_mixed_step(void *context, const pam_mixed_request *request);
 

@@ -65,7 +65,9 @@ class AppendRequest(C.Structure):
 class MixedRequest(C.Structure):
     _fields_ = [("q", P), ("output", P), ("new_keys", P), ("new_values", P), ("k_pool", P), ("v_pool", P),
                 ("k_scale", P), ("v_scale", P), ("block_tables", P), ("bt_stride", I32), ("num_seqs", I32),
-                ("context_lens", P), ("query_lens", P), ("layer", LayerSpec)]
+                ("context_lens", P), ("query_lens", P), ("layer", LayerSpec), ("q_bytes", SZ), ("output_bytes", SZ),
+                ("new_keys_bytes", SZ), ("new_values_bytes", SZ), ("k_pool_bytes", SZ), ("v_pool_bytes", SZ),
+                ("block_tables_bytes", SZ)]
 
 
 class MemoryStats(C.Structure):

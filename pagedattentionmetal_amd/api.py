@@ -239,12 +239,20 @@ class PagedAttentionEngine:
     def mixed_step(self, q, output, k_pool, v_pool, block_tables, context_lens, query_lens, layer: PagedLayerSpec,
                    new_keys=None, new_values=None, k_scale=None, v_scale=None):
         import numpy as np
-        cl = np.ascontiguousarray(context_lens, dtype=np.int32)
-        ql = np.ascontiguousarray(query_lens, dtype=np.int32)
+        cl = np.ascontiguousarray(context_lens, dtype=np.int32).reshape(-1)
+        ql = np.ascontiguousarray(query_lens, dtype=np.int32).reshape(-1)
+        if len(cl) != len(ql):
+            raise PagedAttentionError("Invalid paged attention configuration: context_lens and query_lens must "
+                                      f"have one entry per sequence ({len(cl)} != {len(ql)}).")
+        if block_tables.dim() != 2 or block_tables.shape[0] < len(cl):
+            raise PagedAttentionError("Invalid paged attention configuration: block_tables needs one row per "
+                                      f"sequence ({len(cl)}).")
+        # the library checks every buffer's byte length against the step's rows
         r = _lib.MixedRequest(
             _ptr(q), _ptr(output), _ptr(new_keys), _ptr(new_values), _ptr(k_pool), _ptr(v_pool), _ptr(k_scale),
             _ptr(v_scale), _ptr(block_tables), int(block_tables.shape[1]), len(cl),
-            cl.ctypes.data_as(C.c_void_p), ql.ctypes.data_as(C.c_void_p), layer.c())
+            cl.ctypes.data_as(C.c_void_p), ql.ctypes.data_as(C.c_void_p), layer.c(), _nbytes(q), _nbytes(output),
+            _nbytes(new_keys), _nbytes(new_values), _nbytes(k_pool), _nbytes(v_pool), _nbytes(block_tables))
         self._check(lib().pam_engine_mixed_step(self._ctx, C.byref(r)))
 
     # --- calibration streams (achievable HBM rates, counter scaling)
@@ -439,8 +447,14 @@ class ContinuousBatchingScheduler:
         lib().pam_scheduler_preempt(self._s, int(sid))
 
     def handle_memory_pressure(self, required_blocks: int, cache: KVCacheManager):
-        buf = (C.c_int32 * 4096)()
-        n = lib().pam_scheduler_handle_memory_pressure(self._s, int(required_blocks), cache.handle, buf, 4096)
+        # every victim was running, and at most max_sequences sequences exist, so
+        # the buffer holds all of them (a second call could not return them:
+        # they are already paused)
+        cap = max(1, self.max_sequences)
+        buf = (C.c_int32 * cap)()
+        n = lib().pam_scheduler_handle_memory_pressure(self._s, int(required_blocks), cache.handle, buf, cap)
+        if n > cap:
+            raise PagedAttentionError(f"memory pressure preempted {n} sequences, more than max_sequences ({cap})")
         return list(buf[:n])
 
     def count(self, status: SequenceStatus) -> int:

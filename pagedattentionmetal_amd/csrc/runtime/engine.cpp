@@ -197,11 +197,15 @@ void Context::with_retry(const char *op, F &&fn) {
     throw PamError(last);
 }
 
-void Context::check_launch(hipError_t e, const char *what) {
+// An injected failure (pam_debug_fail_next_launches) stands in for a launch the
+// runtime refused: it is reported before the launch, so nothing is enqueued.
+template <class F>
+void Context::check_launch(F &&launch, const char *what) {
     if (fail_next_launches > 0) {
         fail_next_launches--;
         throw PamError(std::string("GPU command encoding failed: injected launch failure in ") + what);
     }
+    const hipError_t e = launch();
     if (e != hipSuccess) throw PamError(std::string("GPU command encoding failed: ") + what + ": " + hipGetErrorString(e));
 }
 
@@ -428,7 +432,7 @@ void Context::decode_gpu(const pam_decode_request &r) {
     const int64_t tmp = plan_split(p, l.data_type, use_mfma, max_tiles, waves);
     with_retry("decodeFlat", [&] {
         mark(ev0_);
-        check_launch(launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "decode");
+        check_launch([&] { return launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr); }, "decode");
         mark(ev1_);
         finish("decode");
     });
@@ -514,9 +518,9 @@ Context::PrefillPlan Context::plan_prefill(const pam_prefill_request &r) {
 
 void Context::launch_prefill_plan(const PrefillPlan &pl, int32_t dtype) {
     if (pl.dense)
-        check_launch(launch_prefill_mfma(pl.p, dtype, stream()), "prefill");
+        check_launch([&] { return launch_prefill_mfma(pl.p, dtype, stream()); }, "prefill");
     else
-        check_launch(launch_attention(pl.p, dtype, pl.use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "prefill");
+        check_launch([&] { return launch_attention(pl.p, dtype, pl.use_mfma, stream(), gpu_timing ? evmid_ : nullptr); }, "prefill");
 }
 
 void Context::prefill_gpu(const pam_prefill_request &r) {
@@ -596,7 +600,7 @@ void Context::fused_prefill_gpu(const pam_fused_prefill_request &r) {
     }
     with_retry("fusedPrefill", [&] {
         mark(ev0_);
-        if (!one_kernel) check_launch(launch_append(ap, l.data_type, stream()), "fused prefill append");
+        if (!one_kernel) check_launch([&] { return launch_append(ap, l.data_type, stream()); }, "fused prefill append");
         launch_prefill_plan(pl, l.data_type);
         mark(ev1_);
         finish("fusedPrefill");
@@ -643,7 +647,7 @@ void Context::backward(const pam_backward_request &r) {
     p.row_d = static_cast<float *>(workspace_.ptr);
     with_retry("backward", [&] {
         mark(ev0_);
-        check_launch(launch_backward(p, l.data_type, stream()), "backward");
+        check_launch([&] { return launch_backward(p, l.data_type, stream()); }, "backward");
         mark(ev1_);
         finish("backward");
     });
@@ -708,7 +712,7 @@ void Context::append_gpu(const pam_append_request &r) {
     const AppendParams p = append_params(r);
     with_retry(l.data_type == kFP8 ? "appendToCacheCheckedFP8" : "appendToCacheFlat", [&] {
         mark(ev0_);
-        check_launch(launch_append(p, l.data_type, stream()), "append");
+        check_launch([&] { return launch_append(p, l.data_type, stream()); }, "append");
         mark(ev1_);
         finish("append");
     });
@@ -726,6 +730,30 @@ void Context::mixed_step(const pam_mixed_request &r) {
         throw invalid_configuration("mixed step request has a null buffer.");
     if (l.data_type == kFP8 && (!r.k_scale || !r.v_scale))
         throw invalid_configuration("FP8 mixed step needs the K and V scale pools.");
+    if (r.bt_stride <= 0) throw invalid_configuration("btStride must be positive.");
+    // buffer sizes, before any launch (every kernel below indexes them by row)
+    {
+        int64_t total_rows = 0, max_blocks = 0;
+        for (int32_t s = 0; s < r.num_seqs; s++) {
+            if (r.context_lens[s] < 0 || r.query_lens[s] < 0)
+                throw invalid_configuration("negative context or query length");
+            total_rows += r.query_lens[s];
+            const int64_t nb = ceil_div((int64_t)r.context_lens[s] + r.query_lens[s], l.block_size);
+            if (nb > r.bt_stride) throw buffer_too_small("blockTables row", nb * 4, (int64_t)r.bt_stride * 4);
+            max_blocks = std::max<int64_t>(max_blocks, nb);
+        }
+        const int64_t in_row = (int64_t)l.num_kv_heads * l.head_dim * io_bytes(l.data_type);
+        require(r.q_bytes, "Q", total_rows * q_bytes_per_token(l));
+        require(r.output_bytes, "output", total_rows * q_bytes_per_token(l));
+        if (r.new_keys || r.new_values) {
+            if (!r.new_keys || !r.new_values) throw invalid_configuration("mixed step needs both new keys and new values.");
+            require(r.new_keys_bytes, "new keys", total_rows * in_row);
+            require(r.new_values_bytes, "new values", total_rows * in_row);
+        }
+        require(r.block_tables_bytes, "blockTables", (int64_t)r.num_seqs * r.bt_stride * 4);
+        require(r.k_pool_bytes, "K pool", pool_bytes_for(max_blocks, l));
+        require(r.v_pool_bytes, "V pool", pool_bytes_for(max_blocks, l));
+    }
     ensure_device();
     const int32_t bs = l.block_size, W = l.window_size;
     const int32_t G = l.num_heads / l.num_kv_heads;
@@ -854,10 +882,10 @@ void Context::mixed_step(const pam_mixed_request &r) {
     const int64_t tmp = ragged_rows > 0 ? plan_split(p, l.data_type, use_mfma, max_tiles + 1, waves) : 0;
     with_retry("mixedStep", [&] {
         mark(ev0_);
-        if (ab.keys) check_launch(launch_append_batch(ab, l.data_type, stream()), "mixed append");
-        if (!chunks.empty()) check_launch(launch_prefill_mfma(p, l.data_type, stream()), "mixed prefill");
+        if (ab.keys) check_launch([&] { return launch_append_batch(ab, l.data_type, stream()); }, "mixed append");
+        if (!chunks.empty()) check_launch([&] { return launch_prefill_mfma(p, l.data_type, stream()); }, "mixed prefill");
         if (ragged_rows > 0)
-            check_launch(launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr), "mixed attention");
+            check_launch([&] { return launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr); }, "mixed attention");
         else
             mark(evmid_);
         mark(ev1_);
@@ -870,13 +898,13 @@ void Context::mixed_step(const pam_mixed_request &r) {
 
 void Context::fp8_quantize(const uint16_t *v, const uint16_t *s, uint8_t *o, int64_t n) {
     ensure_device();
-    check_launch(launch_fp8_quantize(v, s, o, n, stream()), "fp8 quantize");
+    check_launch([&] { return launch_fp8_quantize(v, s, o, n, stream()); }, "fp8 quantize");
     finish("fp8 quantize");
 }
 
 void Context::fp8_dequant(const uint8_t *c, const uint16_t *s, uint16_t *o, int64_t n) {
     ensure_device();
-    check_launch(launch_fp8_dequant(c, s, o, n, stream()), "fp8 dequant");
+    check_launch([&] { return launch_fp8_dequant(c, s, o, n, stream()); }, "fp8 dequant");
     finish("fp8 dequant");
 }
 

@@ -131,7 +131,8 @@ class Context {
    private:
     template <class F>
     void with_retry(const char *op, F &&fn);
-    void check_launch(hipError_t e, const char *what);
+    template <class F>
+    void check_launch(F &&launch, const char *what);
     void zero_output(void *ptr, size_t bytes);
     void decode_gpu(const pam_decode_request &r);
     void prefill_gpu(const pam_prefill_request &r);

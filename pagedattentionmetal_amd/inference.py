@@ -99,6 +99,8 @@ class PagedAttentionInference:
         for sid in newcomers:  # handlePrefill's block work (:172-186)
             prompt = self.scheduler.sequence(sid)["prompt"]
             dropped |= self._ensure_blocks((prompt + bs - 1) // bs)
+            if sid in dropped:  # paused by this or an earlier newcomer's memory pressure: no blocks for it
+                continue
             try:
                 self.cache.allocate_sequence(sid)
             except PagedAttentionError:

@@ -354,3 +354,67 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(root, "bench.py")], capture_output=True, text=True, timeout=120,
                        env=env)
     assert r.returncode == 2 and "single GPU" in r.stderr
+
+
+def test_mixed_step_validation(pam, ctx):
+    """The mixed step checks every buffer against the step's rows before any
+    launch: q / output / new K,V rows, block-table rows and the pools."""
+    from pagedattentionmetal_amd import _lib
+    lay = _lib.LayerSpec(64, 4, 2, 16, 1, 0)
+    fake = 0x10000  # never dereferenced: validation fails first
+    cl = (C.c_int32 * 3)(10, 0, 40)
+    ql = (C.c_int32 * 3)(1, 20, 1)  # 22 rows; longest sequence 41 tokens = 3 blocks
+    row_q = 4 * 64 * 2
+    row_kv = 2 * 64 * 2
+    good = dict(q_bytes=22 * row_q, output_bytes=22 * row_q, new_keys_bytes=22 * row_kv,
+                new_values_bytes=22 * row_kv, k_pool_bytes=3 * 16 * row_kv, v_pool_bytes=3 * 16 * row_kv,
+                block_tables_bytes=3 * 4 * 4)
+
+    def req(**kw):
+        b = dict(good, **kw)
+        return _lib.MixedRequest(fake, fake, fake, fake, fake, fake, None, None, fake, 4, 3,
+                                 C.cast(cl, C.c_void_p), C.cast(ql, C.c_void_p), lay, b["q_bytes"],
+                                 b["output_bytes"], b["new_keys_bytes"], b["new_values_bytes"], b["k_pool_bytes"],
+                                 b["v_pool_bytes"], b["block_tables_bytes"])
+    for field, name in (("q_bytes", b"Q"), ("output_bytes", b"output"), ("new_keys_bytes", b"new keys"),
+                        ("new_values_bytes", b"new values"), ("k_pool_bytes", b"K pool"),
+                        ("v_pool_bytes", b"V pool"), ("block_tables_bytes", b"blockTables")):
+        r = req(**{field: good[field] - 1})
+        assert pam.pam_engine_mixed_step(ctx, C.byref(r)) == -1, field
+        err = pam.pam_last_error(ctx)
+        assert name in err and b"too small" in err, (field, err)
+    # a table row narrower than a sequence's blocks
+    r = req()
+    r.bt_stride = 2
+    assert pam.pam_engine_mixed_step(ctx, C.byref(r)) == -1
+    assert b"blockTables" in pam.pam_last_error(ctx)
+
+
+def test_mixed_step_python_checks():
+    """api.mixed_step refuses mismatched length arrays and short block tables
+    before calling the library."""
+    import torch
+    from pagedattentionmetal_amd import api
+    eng = api.PagedAttentionEngine()
+    lay = api.PagedLayerSpec(64, 4, 2, 16, 1)
+    q = torch.zeros((3, 4, 64), dtype=torch.float16)
+    kp = torch.zeros((4, 16, 2, 64), dtype=torch.float16)
+    bt = torch.zeros((2, 4), dtype=torch.int32)
+    with pytest.raises(api.PagedAttentionError, match="one entry per sequence"):
+        eng.mixed_step(q, q, kp, kp, bt, [1, 2], [1, 1, 1], lay)
+    with pytest.raises(api.PagedAttentionError, match="one row per"):
+        eng.mixed_step(q, q, kp, kp, bt, [1, 2, 3], [1, 1, 1], lay)
+    with pytest.raises(api.PagedAttentionError, match="Q buffer is too small"):
+        eng.mixed_step(q[:2], q, kp, kp, torch.zeros((3, 4), dtype=torch.int32), [1, 2, 3], [1, 1, 1], lay)
+    eng.close()
+
+
+def test_injected_launch_failure_enqueues_nothing(pam, ctx):
+    """pam_debug_fail_next_launches reports the failure in place of the launch,
+    like a launch the runtime refuses: the retry path then launches once."""
+    src = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                            "pagedattentionmetal_amd", "csrc", "runtime", "engine.cpp")).read()
+    i = src.index("void Context::check_launch(F &&launch")
+    body = src[i:src.index("\n}\n", i)]
+    # the injected failure throws before launch() is called
+    assert body.index("fail_next_launches--") < body.index("launch()")

@@ -67,6 +67,23 @@ def test_driver_out_of_blocks_for_a_prompt_that_cannot_fit():
         inf.step()
 
 
+def test_preempted_newcomers_hold_no_blocks():
+    """A newcomer that memory pressure pauses in its own step (the handler pauses
+    every running sequence, Scheduler.swift:135-152) is not allocated: after the
+    step no paused sequence holds blocks."""
+    inf, cache, sched = _driver(max_blocks=30)
+    inf.add_request(300, 4)  # 19 blocks each: the first fits, the second's pressure pauses both
+    inf.add_request(300, 4)
+    inf.step()
+    assert inf.preemptions == 2
+    assert sched.count(SequenceStatus.paused) == 2
+    assert cache.available_blocks == 30
+    for _ in range(200):
+        if not inf.step():
+            break
+    assert cache.available_blocks == 30
+
+
 @pytest.mark.gpu
 def test_poisson_trace_on_the_gpu():
     W = 256
