@@ -364,6 +364,11 @@ int32_t pam_calib_stream_copy(void *context, const void *src, void *dst, size_t 
  * (host-side; no GPU work is faulted). */
 int32_t pam_debug_fail_next_launches(void *context, int32_t n);
 
+/* Test hook: every split-merge counter of this context is set to `arrivals`
+ * arrivals of a launch that was abandoned part-way (an epoch no later launch
+ * uses).  Later launches must be unaffected. */
+int32_t pam_debug_dirty_counters(void *context, int32_t arrivals);
+
 /* Library version string. */
 const char *pam_version(void);
 

@@ -145,6 +145,7 @@ SIGNATURES = {
     "pam_calib_stream_read": (I32, [P, P, SZ, I32, P]),
     "pam_calib_stream_copy": (I32, [P, P, P, SZ, I32, P]),
     "pam_debug_fail_next_launches": (I32, [P, I32]),
+    "pam_debug_dirty_counters": (I32, [P, I32]),
     "pam_version": (C.c_char_p, []),
 }
 

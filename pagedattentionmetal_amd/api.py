@@ -184,6 +184,10 @@ class PagedAttentionEngine:
     def debug_fail_next_launches(self, n: int):
         self._check(lib().pam_debug_fail_next_launches(self._ctx, int(n)))
 
+    def debug_dirty_counters(self, arrivals: int):
+        """Test hook: leave every split-merge counter as an abandoned launch would."""
+        self._check(lib().pam_debug_dirty_counters(self._ctx, int(arrivals)))
+
     @property
     def last_stats(self) -> dict:
         s = _lib.Stats()

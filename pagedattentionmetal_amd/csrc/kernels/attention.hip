@@ -520,9 +520,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const AttnParams &p)
 // A unit that covers part of a row leaves a partial softmax state per head.
 // It is written with write-through stores, then the (row, kv head) counter is
 // incremented; the wave that brings it to the number of units covering the row
-// merges all partials with the whole wave (write-through loads), writes the
-// output and resets the counter to 0.  A row inside one unit is finished in
-// registers.  No reduce kernel runs.  The partials of (unit u, row r) sit in slot
+// merges all partials with the whole wave (write-through loads) and writes the
+// output.  Counters carry the launch's epoch (arrive_count), so none is ever
+// reset.  A row inside one unit is finished in registers.  No reduce kernel runs.  The partials of (unit u, row r) sit in slot
 // block u + r, unique because a row's units start where the previous row's end:
 // floats [((u + r) * Hkv + kvh) * G + g] * d for query head g of kv head kvh.
 template <typename KV, int HD, int BLK>
@@ -599,7 +599,6 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
     f16 *kt = tiles + wave * WT;
     const __amdgpu_buffer_rsrc_t prs = part_rsrc(p);
     const int ml_off = (int)((const char *)p.part_ml - (const char *)p.part_o);  // bytes
-    using gint = __attribute__((address_space(1))) int32_t;
 
     const int64_t x1 = (u + 1) * T / U;
     for (int64_t x = u * T / U; x < x1;) {
@@ -659,11 +658,10 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        gint *cnt = (gint *)(p.seg_count + (int64_t)lo * Hkv + kvh);
-        int32_t old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __builtin_amdgcn_readfirstlane(old);
-        if (old != nseg - 1) continue;
+        uint32_t before = 0;
+        if (lane == 0) before = arrive_count(p.seg_count + (int64_t)lo * Hkv + kvh, p.epoch);
+        before = __builtin_amdgcn_readfirstlane(before);
+        if (before != (uint32_t)(nseg - 1)) continue;
 
         // Last unit of this (row, kv head): merge all partials, the whole wave at
         // once.  The G * HD floats of one unit are contiguous; the lane owns the
@@ -706,7 +704,6 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
                 *reinterpret_cast<f16x4 *>(orow + 4 * v) = h;
             }
         }
-        if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1056,9 +1053,11 @@ static hipError_t launch_valu(const AttnParams &p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_attention(const AttnParams &p, int32_t dtype, bool use_mfma, hipStream_t stream,
+hipError_t launch_attention(const AttnParams &p_in, int32_t dtype, bool use_mfma, hipStream_t stream,
                             hipEvent_t after_main) {
-    if (p.rows <= 0) return hipSuccess;
+    if (p_in.rows <= 0) return hipSuccess;
+    AttnParams p = p_in;
+    p.epoch = next_launch_epoch();
     // masked lanes of the MFMA kernel read a lane-group slice of one token row
     // from the zero page: it must exist and cover head_dim elements
     if (p.zero_page == nullptr || (size_t)p.head_dim * 4 > kZeroPageBytes) return hipErrorInvalidValue;

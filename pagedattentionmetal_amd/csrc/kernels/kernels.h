@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <vector>
 
 namespace pam {
@@ -36,7 +37,7 @@ struct AttnParams {
     float *part_o;             // [rows][H][max_parts][d] split-context partial outputs
     float *part_ml;            // [rows][H][max_parts][2] (max in log2 units, sum)
                                // (stream-K: [part_slots][d] and [part_slots][2])
-    int32_t *seg_count;        // stream-K MFMA form: [rows][Hkv] counters, all 0 between launches
+    uint64_t *seg_count;       // stream-K MFMA form: [rows][Hkv] merge counters (epoch-tagged)
     uint32_t part_bytes;       // stream-K: bytes of part_o + part_ml (< 2^31)
     const void *zero_page;     // >= 1 KiB of zeros: the source of masked lanes' loads
     int32_t rows;
@@ -56,7 +57,7 @@ struct AttnParams {
     const int4 *pf_work;
     const int2 *pf_range;
     float *pf_part;
-    int32_t *pf_count;         // one per slot, all 0 between launches
+    uint64_t *pf_count;        // one merge counter per slot (epoch-tagged)
     uint32_t pf_part_bytes;
     int32_t pf_groups;         // workgroups of the launch
     // dense prefill, fused append (f16): the chunks' new keys and values
@@ -64,6 +65,10 @@ struct AttnParams {
     // chunk's q_offset are read from here, and the kernel writes them into the
     // pools.  Null: all keys come from the pools.
     const void *fuse_k, *fuse_v;
+    // tag of this launch for the merge counters: a counter holding another epoch
+    // counts as zero arrivals, so counters need no reset.  The launchers set a
+    // fresh nonzero epoch for every launch (a retried launch gets a new one).
+    uint32_t epoch;
 };
 
 // Paged attention over rows (decode / prefill-as-rows / ragged).  Chooses the
@@ -72,10 +77,21 @@ struct AttnParams {
 hipError_t launch_attention(const AttnParams &p, int32_t dtype, bool use_mfma, hipStream_t stream,
                             hipEvent_t after_main = nullptr);
 bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size);
+// A fresh launch epoch for the merge counters: process-wide (one counter for the
+// whole library, an inline function's static), so launches of any context that
+// share counters never repeat one; 0 (zeroed memory) is skipped.
+inline uint32_t next_launch_epoch() {
+    static std::atomic<uint32_t> epoch{0};
+    uint32_t e;
+    do e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+    while (e == 0);
+    return e;
+}
 // Stream-K form of the MFMA kernel (rows <= 2048): one launch, no reduce kernel.
-// Gives the partial slots (floats per slot: d + 2) and the counters it needs; the
-// counters must be zero before the first launch and every launch leaves them
-// zero.  Launches that share counters must not overlap.  False: not applicable.
+// Gives the partial slots (floats per slot: d + 2) and the 64-bit merge counters
+// it needs.  Counters start as any value an earlier launch left (or zero) and
+// are never reset; launches that share counters must not overlap.  False: not
+// applicable.
 bool mfma_streamk_plan(const AttnParams &p, int32_t dtype, int64_t *part_slots, int64_t *counters);
 
 // KV append into the paged pools.

@@ -124,4 +124,30 @@ __device__ __forceinline__ f16x8 e4m3x8_to_f16x8(uint32_t w0, uint32_t w1) {
     return (f16x8){(f16)a[0], (f16)a[1], (f16)b[0], (f16)b[1], (f16)c[0], (f16)c[1], (f16)d[0], (f16)d[1]};
 }
 
+// Cross-workgroup merge counters.  A counter is 64 bits: the launch's epoch in
+// the high word, the arrivals of that launch in the low word.  Every launch
+// carries a fresh nonzero epoch, so a counter left behind by an earlier launch
+// (one abandoned part-way, or zeroed memory: epoch 0) reads as zero arrivals and
+// nothing ever resets a counter.  Launches that share counters never overlap,
+// so a counter's epoch never exceeds the running launch's.
+//
+// arrive_count returns how many arrivals of this launch came before the
+// caller's.  The caller must have completed (s_waitcnt vmcnt(0)) the sc1
+// (agent-scope, L2 write-through) stores of whatever it publishes; the one
+// that sees count - 1 reads the published data with sc1 loads issued after this
+// returns.  Called by one lane.
+__device__ __forceinline__ uint32_t arrive_count(uint64_t *counter, uint32_t epoch) {
+    using g64 = __attribute__((address_space(1))) uint64_t;
+    g64 *c = (g64 *)counter;
+    const uint64_t tag = (uint64_t)epoch << 32;
+    // raise a stale counter to (epoch, 0); a current one is already above tag
+    const uint64_t seen = __hip_atomic_fetch_max(c, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the maximum has returned (it is applied) before the add is issued
+    asm volatile("s_waitcnt vmcnt(0)" ::"v"(seen) : "memory");
+    const uint64_t old = __hip_atomic_fetch_add(c, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // no load of the published data may be moved above the count
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return (uint32_t)old;
+}
+
 }  // namespace pam

@@ -503,8 +503,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
         // A piece of a split item publishes its state (O^T, reference max and row
         // sums, per lane) in its slot with write-through stores and counts it;
         // the workgroup that brings the count to the number of pieces merges all
-        // of them in piece order (the same result whichever workgroup merges),
-        // writes the rows and resets the counter.
+        // of them in piece order (the same result whichever workgroup merges)
+        // and writes the rows.  The counter carries the launch's epoch
+        // (arrive_count), so it is never reset.
         if (wb.z > 1) {
             static_assert(kPrefillSlotBytes == (int64_t)kPrefillWaves * 64 * RB * (16 * DT + 2) * 4, "slot size");
             const __amdgpu_buffer_rsrc_t prs =
@@ -533,9 +534,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
             __builtin_amdgcn_s_waitcnt(0);
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __syncthreads();
-            if (tid == 0)
-                merge_flag = __hip_atomic_fetch_add(p.pf_count + wb.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                             wb.z - 1;
+            if (tid == 0) merge_flag = arrive_count(p.pf_count + wb.x, p.epoch) == (uint32_t)(wb.z - 1);
             __syncthreads();
             if (!merge_flag) continue;
 #pragma unroll
@@ -564,7 +563,6 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
                 }
                 l_run[b] = den;
             }
-            if (tid == 0) __hip_atomic_store(p.pf_count + wb.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
 
         // finish: l summed over the two lane halves, O / l, rows in range only
@@ -593,7 +591,9 @@ bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int3
            (kPrefillRows % group) == 0 && block_size > 0 && (block_size & (block_size - 1)) == 0;
 }
 
-hipError_t launch_prefill_mfma(const AttnParams &p, int32_t dtype, hipStream_t stream) {
+hipError_t launch_prefill_mfma(const AttnParams &p_in, int32_t dtype, hipStream_t stream) {
+    AttnParams p = p_in;
+    p.epoch = next_launch_epoch();
     if (p.pf_work == nullptr || p.pf_range == nullptr || p.pf_groups <= 0) return hipErrorInvalidValue;
     const int G = p.num_heads / p.num_kv_heads;
     if (!prefill_mfma_supported(dtype, p.head_dim, G, p.block_size)) return hipErrorInvalidValue;

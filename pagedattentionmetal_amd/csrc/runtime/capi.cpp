@@ -635,4 +635,8 @@ PAM_API int32_t pam_debug_fail_next_launches(void *context, int32_t n) {
     return guarded(context, [&](Context *ctx) { ctx->fail_next_launches = n < 0 ? 0 : n; });
 }
 
+PAM_API int32_t pam_debug_dirty_counters(void *context, int32_t arrivals) {
+    return guarded(context, [&](Context *ctx) { ctx->dirty_counters(arrivals); });
+}
+
 PAM_API const char *pam_version(void) { return "pam-mi355x 0.1.0 (gfx950)"; }

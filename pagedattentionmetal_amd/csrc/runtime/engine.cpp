@@ -294,8 +294,8 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
         p.part_o = static_cast<float *>(workspace_.ptr);
         p.part_ml = p.part_o + slots * p.head_dim;
         p.part_bytes = (uint32_t)bytes;
-        reserve_counters(seg_count_, (size_t)counters * 4);
-        p.seg_count = static_cast<int32_t *>(seg_count_.ptr);
+        reserve_counters(seg_count_, (size_t)counters * 8);
+        p.seg_count = static_cast<uint64_t *>(seg_count_.ptr);
         return bytes;
     }
     p.part_tokens = choose_part_tokens(waves, max_tiles, use_mfma);
@@ -321,6 +321,17 @@ void Context::reserve_counters(DeviceBuffer &b, size_t bytes) {
     b.bytes = bytes;
 }
 
+void Context::dirty_counters(int32_t arrivals) {
+    ensure_device();
+    const uint64_t v = ((uint64_t)next_launch_epoch() << 32) | (uint32_t)arrivals;
+    for (DeviceBuffer *b : {&seg_count_, &pf_count_}) {
+        if (!b->ptr) continue;
+        std::vector<uint64_t> h(b->bytes / 8, v);
+        hip_check(hipStreamSynchronize(stream()), "dirty counters");
+        hip_check(hipMemcpy(b->ptr, h.data(), h.size() * 8, hipMemcpyHostToDevice), "dirty counters");
+    }
+}
+
 Context::DensePlan Context::plan_dense_prefill(AttnParams &p, const int4 *chunks, int32_t n, StageList &sl) {
     PrefillSplit ps;
     prefill_split_plan(chunks, n, p, cus_, ps);
@@ -341,9 +352,9 @@ Context::DensePlan Context::plan_dense_prefill(AttnParams &p, const int4 *chunks
             hip_check(hipMalloc(&pf_part_.ptr, (size_t)bytes), "hipMalloc prefill workspace");
             pf_part_.bytes = (size_t)bytes;
         }
-        reserve_counters(pf_count_, (size_t)ps.slots * 4);
+        reserve_counters(pf_count_, (size_t)ps.slots * 8);
         p.pf_part = static_cast<float *>(pf_part_.ptr);
-        p.pf_count = static_cast<int32_t *>(pf_count_.ptr);
+        p.pf_count = static_cast<uint64_t *>(pf_count_.ptr);
         p.pf_part_bytes = (uint32_t)bytes;
         d.tmp = bytes;
     }
@@ -533,8 +544,10 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
         finish("prefill");
     });
     const int32_t op = (pl.dense || pl.use_mfma) ? PAM_OP_PREFILL_MMA : PAM_OP_PREFILL_TILED_PASS;
-    record_stats(op, 1, r.seq_len, (int32_t)ceil_div(pl.kv_len, l.block_size), pl.tmp,
-                 pl.p.max_parts > 1 || pl.p.seg_count != nullptr, !pl.dense);
+    // split: the dense kernel cut items into pieces merged in the kernel, or the
+    // row kernels used split-context partitions
+    const bool split = pl.dense ? pl.p.pf_part != nullptr : (pl.p.max_parts > 1 || pl.p.seg_count != nullptr);
+    record_stats(op, 1, r.seq_len, (int32_t)ceil_div(pl.kv_len, l.block_size), pl.tmp, split, !pl.dense);
 }
 
 // fusedPrefill (PagedAttentionEngine.swift:633-710).  The reference runs one kernel

@@ -120,6 +120,10 @@ class Context {
         if (gpu_timing) (void)hipEventRecord(e, stream());
     }
 
+    // Test hook: every merge counter the context owns is set to `arrivals`
+    // arrivals of an abandoned launch (a consumed epoch).
+    void dirty_counters(int32_t arrivals);
+
     // --- scratch
     void reserve_workspace(size_t bytes);
     // stage host bytes into a context-owned device region (slot selects one of
@@ -171,9 +175,9 @@ class Context {
     bool stats_pending_ = false;
     bool stats_has_mid_ = false;
     DeviceBuffer workspace_;
-    DeviceBuffer seg_count_;  // stream-K counters: zero between launches
+    DeviceBuffer seg_count_;  // stream-K merge counters (epoch-tagged, never reset)
     DeviceBuffer pf_part_;    // dense prefill: partial slots of split items
-    DeviceBuffer pf_count_;   // dense prefill: counters, zero between launches
+    DeviceBuffer pf_count_;   // dense prefill: merge counters (epoch-tagged, never reset)
     void reserve_counters(DeviceBuffer &b, size_t bytes);
     DeviceBuffer scratch_[6];
     void *pinned_ = nullptr;

@@ -336,8 +336,7 @@ def test_prefill_parity(engine, case):
 def test_dense_prefill_split_repeatable(engine):
     """The dense prefill kernel cuts long items into pieces merged in the kernel
     (partial slots and counters): the merge order is fixed, so repeated calls give
-    the same bits, and the counters are back at zero after every call (a call
-    of another shape in between changes nothing)."""
+    the same bits, and a call of another shape in between changes nothing."""
     import torch
     rng = np.random.default_rng(77)
     H, hkv, d, bs, T, off = 32, 8, 128, 16, 700, 2500
@@ -354,6 +353,48 @@ def test_dense_prefill_split_repeatable(engine):
     assert row_rel_err(outs[0].astype(np.float64), ref) <= TOL[1]
     ref90 = oracle.prefill(1, q[:90], k, v, bt[0], off, causal=True, n_threads=8)
     assert row_rel_err(outs[1].astype(np.float64), ref90) <= TOL[1]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["decode_streamk", "prefill_split"])
+def test_split_merges_after_abandoned_launch(engine, path):
+    """The split-merge counters carry each launch's epoch: counters left as an
+    abandoned launch would leave them (any arrival count, an older epoch), or a
+    launch that failed and was retried, change neither the result nor its bits."""
+    import torch
+    rng = np.random.default_rng(505)
+    H, hkv, d, bs = 32, 8, 128, 16
+    if path == "decode_streamk":
+        q, k, v, bt, lens = make_case(rng, 3, H, hkv, d, bs, 1, [9000, 40, 5000])
+        args = (to_dev(q), to_dev(k), to_dev(v), to_dev(bt), to_dev(lens))
+        ref = oracle.decode(1, q, k, v, bt, lens, H, n_threads=8)
+
+        def run():
+            out = torch.zeros((3, H, d), dtype=torch.float16, device="cuda")
+            engine.decode(*args, out, 3, bt.shape[1], layer(H, hkv, d, bs, 1))
+            return to_host(out)
+    else:
+        T, off = 700, 2500
+        q, k, v, bt, _ = make_case(rng, 1, H, hkv, d, bs, 1, [off + T])
+        q = rng.standard_normal((T, H, d)).astype(np.float16)
+        kd, vd, qd, btd = to_dev(k), to_dev(v), to_dev(q), to_dev(bt[0])
+        ref = oracle.prefill(1, q, k, v, bt[0], off, causal=True, n_threads=8)
+
+        def run():
+            out = torch.zeros((T, H, d), dtype=torch.float16, device="cuda")
+            engine.prefill(qd, kd, vd, btd, out, T, layer(H, hkv, d, bs, 1), causal=True, q_offset=off)
+            return to_host(out)
+    first = run()
+    assert engine.last_stats["used_split_pass"] == 1, "the case must take the split path"
+    assert row_rel_err(first.astype(np.float64), ref) <= TOL[1]
+    for arrivals in (1, 3, 1000, 0x7FFFFFFF):
+        engine.debug_dirty_counters(arrivals)
+        again = run()
+        assert np.array_equal(again.view(np.uint16), first.view(np.uint16)), f"dirty counters ({arrivals})"
+    engine.set_max_retries(3)
+    engine.debug_fail_next_launches(1)  # refused once, then retried
+    again = run()
+    assert np.array_equal(again.view(np.uint16), first.view(np.uint16)), "after a retried launch"
 
 
 # ---------------------------------------------------------------- mixed step
