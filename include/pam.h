@@ -349,6 +349,21 @@ typedef struct pam_mixed_request {
 } pam_mixed_request;
 int32_t pam_engine_mixed_step(void *context, const pam_mixed_request *request);
 
+/* Allocation-free decode.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  pam_engine_decode_noalloc
+ * takes the same request and gives the same results as pam_engine_decode, but
+ * its kernels keep their split-context partials, merge counters and zero page
+ * in one fixed per-GPU array of the library (32 MiB, held until the process
+ * ends) and it calls no hipMalloc / hipFree; a request whose workspace does not
+ * fit (stream-K partials above 31 MiB - 4 KiB, or more than 131072 merge
+ * counters) fails with an error.  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (other contexts or streams) race.
+ * pam_engine_setup_noalloc prepares the context and the array (it may
+ * allocate; call it once, outside the no-allocation region). */
+int32_t pam_engine_setup_noalloc(void *context);
+int32_t pam_engine_decode_noalloc(void *context, const pam_decode_request *request);
+
 /* FP8 e4m3 codec over n elements (device buffers): the quantize_fp8 / dequant_fp8
  * pair of kernels.metal:553-601 with a per-element half scale. */
 int32_t pam_fp8_quantize(void *context, const uint16_t *values, const uint16_t *scales, uint8_t *out, int64_t n);

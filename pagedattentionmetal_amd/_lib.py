@@ -140,6 +140,8 @@ SIGNATURES = {
     "pam_set_decode_kernel": (I32, [P, I32]),
     "pam_set_gpu_timing": (I32, [P, C.c_bool]),
     "pam_engine_mixed_step": (I32, [P, C.POINTER(MixedRequest)]),
+    "pam_engine_setup_noalloc": (I32, [P]),
+    "pam_engine_decode_noalloc": (I32, [P, C.POINTER(DecodeRequest)]),
     "pam_fp8_quantize": (I32, [P, P, P, P, I64]),
     "pam_fp8_dequant": (I32, [P, P, P, P, I64]),
     "pam_calib_stream_read": (I32, [P, P, SZ, I32, P]),

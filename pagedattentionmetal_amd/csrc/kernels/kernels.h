@@ -94,6 +94,17 @@ inline uint32_t next_launch_epoch() {
 // applicable.
 bool mfma_streamk_plan(const AttnParams &p, int32_t dtype, int64_t *part_slots, int64_t *counters);
 
+// Allocation-free decode: a fixed device array per GPU (noalloc.hip) laid out as
+// [zero page | merge counters | split-context partials].
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+constexpr size_t kNoAllocZeroBytes = 4096;
+constexpr size_t kNoAllocCounterBytes = (size_t)1 << 20;
+// Looks up (once per device, with `device` current) the array's device address,
+// clears its zero page on `stream` and returns the address.
+hipError_t noalloc_scratch_setup(int device, hipStream_t stream, void **out);
+// The address set up for `device`, or null before noalloc_scratch_setup.
+void *noalloc_scratch(int device);
+
 // KV append into the paged pools.
 struct AppendParams {
     const void *keys;          // [n][Hkv][d] (f32 for f32 caches, f16 for f16 and fp8)

@@ -255,6 +255,15 @@ PAM_API int32_t pam_engine_decode(void *context, const pam_decode_request *reque
     return guarded(context, [&](Context *ctx) { ctx->decode(*request); });
 }
 
+PAM_API int32_t pam_engine_setup_noalloc(void *context) {
+    return guarded(context, [&](Context *ctx) { ctx->setup_noalloc(); });
+}
+
+PAM_API int32_t pam_engine_decode_noalloc(void *context, const pam_decode_request *request) {
+    if (!request) return -1;
+    return guarded(context, [&](Context *ctx) { ctx->decode_noalloc(*request); });
+}
+
 PAM_API int32_t pam_engine_prefill(void *context, const pam_prefill_request *request) {
     if (!request) return -1;
     return guarded(context, [&](Context *ctx) { ctx->prefill(*request); });

@@ -280,9 +280,18 @@ int32_t Context::choose_part_tokens(int64_t items_per_part, int64_t max_tiles, b
 // in the workspace plus the counters, no reduce kernel.  Otherwise rows are cut
 // into fixed partitions merged by the reduce kernel.  Returns the workspace
 // bytes used (0: none).
-int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves) {
+int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves,
+                            char *fixed) {
     p.seg_count = nullptr;
     int64_t slots = 0, counters = 0;
+    // `fixed`: the allocation-free scratch (kNoAllocScratchBytes, laid out as
+    // zero page | counters | partials); requests that do not fit it are refused
+    const int64_t fixed_parts = (int64_t)(kNoAllocScratchBytes - kNoAllocZeroBytes - kNoAllocCounterBytes);
+    auto too_big = [](const char *what, int64_t need, int64_t have) {
+        return PamError(std::string("Unsupported paged attention path: the allocation-free decode's ") + what +
+                        " needs " + std::to_string(need) + " bytes of its fixed " + std::to_string(have) +
+                        "-byte scratch.");
+    };
     // a partition length set through pam_set_partition_tokens selects the
     // partitioned form
     if (use_mfma && part_tokens_override == 0 && mfma_streamk_plan(p, dtype, &slots, &counters)) {
@@ -290,12 +299,20 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
         p.max_parts = 1;
         const int64_t bytes = slots * ((int64_t)p.head_dim + 2) * 4;
         if (bytes >= ((int64_t)1 << 31)) throw PamError("stream-K workspace exceeds 2 GiB");
-        reserve_workspace((size_t)bytes);
-        p.part_o = static_cast<float *>(workspace_.ptr);
+        if (fixed) {
+            if (bytes > fixed_parts) throw too_big("split-context partials", bytes, fixed_parts);
+            if (counters * 8 > (int64_t)kNoAllocCounterBytes)
+                throw too_big("merge counters", counters * 8, (int64_t)kNoAllocCounterBytes);
+            p.part_o = reinterpret_cast<float *>(fixed + kNoAllocZeroBytes + kNoAllocCounterBytes);
+            p.seg_count = reinterpret_cast<uint64_t *>(fixed + kNoAllocZeroBytes);
+        } else {
+            reserve_workspace((size_t)bytes);
+            p.part_o = static_cast<float *>(workspace_.ptr);
+            reserve_counters(seg_count_, (size_t)counters * 8);
+            p.seg_count = static_cast<uint64_t *>(seg_count_.ptr);
+        }
         p.part_ml = p.part_o + slots * p.head_dim;
         p.part_bytes = (uint32_t)bytes;
-        reserve_counters(seg_count_, (size_t)counters * 8);
-        p.seg_count = static_cast<uint64_t *>(seg_count_.ptr);
         return bytes;
     }
     p.part_tokens = choose_part_tokens(waves, max_tiles, use_mfma);
@@ -303,8 +320,13 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
     if (p.max_parts <= 1) return 0;
     const int64_t slots_p = (int64_t)p.rows * p.num_heads * p.max_parts;
     const int64_t bytes = slots_p * ((int64_t)p.head_dim + 2) * 4;
-    reserve_workspace((size_t)bytes);
-    p.part_o = static_cast<float *>(workspace_.ptr);
+    if (fixed) {
+        if (bytes > fixed_parts) throw too_big("split-context partials", bytes, fixed_parts);
+        p.part_o = reinterpret_cast<float *>(fixed + kNoAllocZeroBytes + kNoAllocCounterBytes);
+    } else {
+        reserve_workspace((size_t)bytes);
+        p.part_o = static_cast<float *>(workspace_.ptr);
+    }
     p.part_ml = p.part_o + slots_p * p.head_dim;
     return bytes;
 }
@@ -374,7 +396,17 @@ static int32_t heads_per_wave(int32_t group) {
 
 // ------------------------------------------------------------------ decode
 
-void Context::decode(const pam_decode_request &r) {
+void Context::setup_noalloc() {
+    ensure_device();
+    void *ptr = nullptr;
+    hip_check(noalloc_scratch_setup(device_, stream(), &ptr), "allocation-free scratch set-up");
+}
+
+void Context::decode(const pam_decode_request &r) { decode_checked(r, false); }
+
+void Context::decode_noalloc(const pam_decode_request &r) { decode_checked(r, true); }
+
+void Context::decode_checked(const pam_decode_request &r, bool noalloc) {
     validate_layer(r.layer);
     // validateDecode (PagedAttentionEngine.swift:1916-1934)
     if (r.batch_size <= 0) throw invalid_configuration("batchSize must be positive.");
@@ -393,20 +425,26 @@ void Context::decode(const pam_decode_request &r) {
         throw invalid_configuration("FP8 decode needs the K and V scale pools.");
     if (!r.q || !r.k_pool || !r.v_pool || !r.block_tables || !r.seq_lengths || !r.output)
         throw invalid_configuration("decode request has a null buffer.");
+    char *fixed = nullptr;
+    if (noalloc) {
+        // set up by pam_engine_setup_noalloc: this path creates nothing itself
+        if (!device_ready_ || (fixed = static_cast<char *>(noalloc_scratch(device_))) == nullptr)
+            throw PamError("GPU device or stream could not be initialized: call pam_engine_setup_noalloc first.");
+    }
     ensure_device();
     if (graceful_degradation) {
         try {
-            decode_gpu(r);
+            decode_gpu(r, fixed);
         } catch (const PamError &e) {
             std::fprintf(stderr, "[pam] decode failed: %s\n", e.what());
             zero_output(r.output, (size_t)(r.batch_size * q_bytes_per_token(l)));
         }
     } else {
-        decode_gpu(r);
+        decode_gpu(r, fixed);
     }
 }
 
-void Context::decode_gpu(const pam_decode_request &r) {
+void Context::decode_gpu(const pam_decode_request &r, char *fixed) {
     const pam_layer_spec &l = r.layer;
     const int32_t G = l.num_heads / l.num_kv_heads;
     bool use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size) && G >= 4;
@@ -434,13 +472,13 @@ void Context::decode_gpu(const pam_decode_request &r) {
     p.mode = kRowDecode;
     p.heads_per_wave = nh;
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
-    p.zero_page = zero_page_;
+    p.zero_page = fixed ? static_cast<const void *>(fixed) : zero_page_;
 
     const int64_t cap_tokens = (int64_t)r.max_num_blocks * l.block_size;
     int64_t max_tiles = ceil_div(cap_tokens, 16);
     if (l.window_size > 0) max_tiles = std::min<int64_t>(max_tiles, l.window_size / 16 + 2);
     const int64_t waves = (int64_t)r.batch_size * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-    const int64_t tmp = plan_split(p, l.data_type, use_mfma, max_tiles, waves);
+    const int64_t tmp = plan_split(p, l.data_type, use_mfma, max_tiles, waves, fixed);
     with_retry("decodeFlat", [&] {
         mark(ev0_);
         check_launch([&] { return launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr); }, "decode");

@@ -97,6 +97,10 @@ class Context {
 
     // --- engine (PagedAttentionEngine)
     void decode(const pam_decode_request &r);
+    // decode with the split-context workspace, counters and zero page in the
+    // library's fixed per-device scratch: no allocation (setup_noalloc first)
+    void decode_noalloc(const pam_decode_request &r);
+    void setup_noalloc();
     void prefill(const pam_prefill_request &r);
     void append(const pam_append_request &r);
     void mixed_step(const pam_mixed_request &r);
@@ -138,7 +142,8 @@ class Context {
     template <class F>
     void check_launch(F &&launch, const char *what);
     void zero_output(void *ptr, size_t bytes);
-    void decode_gpu(const pam_decode_request &r);
+    void decode_checked(const pam_decode_request &r, bool noalloc);
+    void decode_gpu(const pam_decode_request &r, char *fixed);
     void prefill_gpu(const pam_prefill_request &r);
     void append_gpu(const pam_append_request &r);
     void fused_prefill_gpu(const pam_fused_prefill_request &r);
@@ -152,7 +157,8 @@ class Context {
     void launch_prefill_plan(const PrefillPlan &pl, int32_t dtype);
     AppendParams append_params(const pam_append_request &r);
     int32_t choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma);
-    int64_t plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves);
+    int64_t plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves,
+                       char *fixed = nullptr);
     // dense prefill: work list of host chunks (the order staged as p.chunks) added
     // to `sl`, partial slots and counters reserved; after staging `sl` at `base`,
     // bind_dense_prefill points p at the list
