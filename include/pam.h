@@ -113,6 +113,7 @@ typedef struct pam_stats {
     double elapsed_ms;
     double kernel_ms; /* attention kernel alone (decode / prefill / mixed), -1 if not timed */
     double reduce_ms; /* split-context reduce kernel, 0 when not launched */
+    int32_t chunks;   /* prefill passes of the call (the chunk loop of the flat prefill), 0 for other ops */
 } pam_stats;
 
 /* PagedAttentionDecodeRequest (PagedAttentionTypes.swift:259-315).  *_bytes are the
@@ -223,6 +224,93 @@ int32_t pam_engine_append(void *context, const pam_append_request *request);
 int32_t pam_engine_fused_prefill(void *context, const pam_fused_prefill_request *request);
 /* PagedAttentionEngine.backward(q:kPool:...) (PagedAttentionEngine.swift:1340-1396) */
 int32_t pam_engine_backward(void *context, const pam_backward_request *request);
+/* Multi-layer calls over one shared pool, block table(s) and lengths; every
+ * layer has its own Q and output (and, for appends, its own keys, values and
+ * FP8 scale pools).  Arrays hold num_layers entries; *_bytes arrays may be
+ * NULL (no size check).  window_size > 0 overrides every layer's window. */
+typedef struct pam_decode_layers_request {
+    const void *const *q;       /* [num_layers] -> [batch_size][num_heads][head_dim] */
+    void *const *output;        /* [num_layers] */
+    const pam_layer_spec *layers;
+    int32_t num_layers;
+    const void *k_pool;
+    const void *v_pool;
+    const int32_t *block_tables; /* [batch_size][max_num_blocks] */
+    const uint32_t *seq_lengths;
+    int32_t batch_size;
+    int32_t max_num_blocks;
+    int32_t window_size;
+    const uint16_t *k_scale;
+    const uint16_t *v_scale;
+    const size_t *q_bytes, *output_bytes;
+    size_t k_pool_bytes, v_pool_bytes, block_tables_bytes, seq_lengths_bytes;
+} pam_decode_layers_request;
+typedef struct pam_prefill_layers_request {
+    const void *const *q;       /* [num_layers] -> [seq_len][num_heads][head_dim] */
+    void *const *output;
+    const pam_layer_spec *layers;
+    int32_t num_layers;
+    const void *k_pool;
+    const void *v_pool;
+    const int32_t *block_table;
+    int32_t seq_len;
+    bool causal;
+    int32_t window_size;
+    const uint16_t *k_scale;
+    const uint16_t *v_scale;
+    const size_t *q_bytes, *output_bytes;
+    size_t k_pool_bytes, v_pool_bytes, block_table_bytes;
+} pam_prefill_layers_request;
+typedef struct pam_append_layers_request {
+    const void *const *keys;    /* [num_layers] -> [num_new_tokens][num_kv_heads][head_dim] */
+    const void *const *values;
+    const pam_layer_spec *layers;
+    int32_t num_layers;
+    void *k_pool;
+    void *v_pool;
+    const int32_t *block_table;
+    int32_t token_offset;
+    int32_t num_new_tokens;
+    uint16_t *const *k_scale;   /* [num_layers] FP8 scale pools, or NULL */
+    uint16_t *const *v_scale;
+    const size_t *keys_bytes, *values_bytes;
+    size_t k_pool_bytes, v_pool_bytes, block_table_bytes;
+} pam_append_layers_request;
+/* PagedAttentionEngine.decodeLayers (PagedAttentionEngine.swift:1641-1741).
+ * Consecutive layers of one spec that the stream-K MFMA decode serves (G >= 4)
+ * share one launch, up to 16 query heads per kv head: each K/V tile is read
+ * once for all of their heads. */
+int32_t pam_engine_decode_layers(void *context, const pam_decode_layers_request *request);
+/* PagedAttentionEngine.prefillLayers (PagedAttentionEngine.swift:1433-1639) */
+int32_t pam_engine_prefill_layers(void *context, const pam_prefill_layers_request *request);
+/* PagedAttentionEngine.appendLayers (PagedAttentionEngine.swift:1744-1895): layers
+ * append in order at the same positions of the one pool. */
+int32_t pam_engine_append_layers(void *context, const pam_append_layers_request *request);
+
+/* PagedAttentionEngine.splitThreshold / defaultWindowSize / defaultChunkSize
+ * (PagedAttentionEngine.swift:116-121).  split_threshold (tokens, default 1024):
+ * only prefills whose longest key range exceeds it may run the multi-pass form
+ * (items cut over workgroups, partial states merged in the kernel).  The
+ * defaults apply to the flat overloads below when their argument is 0. */
+typedef struct pam_engine_config {
+    int32_t split_threshold;
+    int32_t default_window_size;
+    int32_t default_chunk_size;
+} pam_engine_config;
+int32_t pam_engine_set_config(void *context, const pam_engine_config *config);
+int32_t pam_engine_get_config(void *context, pam_engine_config *out);
+/* The flat overloads: the request's layer window is replaced by window_size,
+ * or defaultWindowSize when window_size is 0.
+ * prefill(q:kPool:...:windowSize:chunkSize:) (PagedAttentionEngine.swift:713-760):
+ * chunk_size (or defaultChunkSize) > 0 below seq_len runs the chunk loop, whose
+ * result equals the unchunked prefill; pam_stats.chunks counts its passes. */
+int32_t pam_engine_prefill_flat(void *context, const pam_prefill_request *request, int32_t window_size,
+                                int32_t chunk_size);
+/* decode(q:kPool:...:windowSize:) (PagedAttentionEngine.swift:1012-1046) */
+int32_t pam_engine_decode_flat(void *context, const pam_decode_request *request, int32_t window_size);
+/* appendToCache(keys:values:...:windowSize:) (PagedAttentionEngine.swift:1167-1201) */
+int32_t pam_engine_append_flat(void *context, const pam_append_request *request, int32_t window_size);
+
 /* PagedAttentionEngine.lastStats (PagedAttentionEngine.swift:136-141) */
 int32_t pam_engine_last_stats(void *context, pam_stats *out);
 /* PagedAttentionEngine.enableGracefulDegradation / maxRetries (Engine.swift:126-129) */

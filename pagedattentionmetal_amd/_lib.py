@@ -26,7 +26,7 @@ class LayerSpec(C.Structure):
 class Stats(C.Structure):
     _fields_ = [("operation", I32), ("batch_size", I32), ("sequence_length", I32), ("num_blocks", I32),
                 ("temporary_bytes", I64), ("used_split_pass", I32), ("elapsed_ms", C.c_double),
-                ("kernel_ms", C.c_double), ("reduce_ms", C.c_double)]
+                ("kernel_ms", C.c_double), ("reduce_ms", C.c_double), ("chunks", I32)]
 
 
 class DecodeRequest(C.Structure):
@@ -68,6 +68,35 @@ class MixedRequest(C.Structure):
                 ("context_lens", P), ("query_lens", P), ("layer", LayerSpec), ("q_bytes", SZ), ("output_bytes", SZ),
                 ("new_keys_bytes", SZ), ("new_values_bytes", SZ), ("k_pool_bytes", SZ), ("v_pool_bytes", SZ),
                 ("block_tables_bytes", SZ)]
+
+
+class EngineConfig(C.Structure):
+    _fields_ = [("split_threshold", I32), ("default_window_size", I32), ("default_chunk_size", I32)]
+
+
+PP = C.POINTER(C.c_void_p)
+PSZ = C.POINTER(C.c_size_t)
+
+
+class DecodeLayersRequest(C.Structure):
+    _fields_ = [("q", PP), ("output", PP), ("layers", C.POINTER(LayerSpec)), ("num_layers", I32), ("k_pool", P),
+                ("v_pool", P), ("block_tables", P), ("seq_lengths", P), ("batch_size", I32), ("max_num_blocks", I32),
+                ("window_size", I32), ("k_scale", P), ("v_scale", P), ("q_bytes", PSZ), ("output_bytes", PSZ),
+                ("k_pool_bytes", SZ), ("v_pool_bytes", SZ), ("block_tables_bytes", SZ), ("seq_lengths_bytes", SZ)]
+
+
+class PrefillLayersRequest(C.Structure):
+    _fields_ = [("q", PP), ("output", PP), ("layers", C.POINTER(LayerSpec)), ("num_layers", I32), ("k_pool", P),
+                ("v_pool", P), ("block_table", P), ("seq_len", I32), ("causal", C.c_bool), ("window_size", I32),
+                ("k_scale", P), ("v_scale", P), ("q_bytes", PSZ), ("output_bytes", PSZ), ("k_pool_bytes", SZ),
+                ("v_pool_bytes", SZ), ("block_table_bytes", SZ)]
+
+
+class AppendLayersRequest(C.Structure):
+    _fields_ = [("keys", PP), ("values", PP), ("layers", C.POINTER(LayerSpec)), ("num_layers", I32), ("k_pool", P),
+                ("v_pool", P), ("block_table", P), ("token_offset", I32), ("num_new_tokens", I32), ("k_scale", PP),
+                ("v_scale", PP), ("keys_bytes", PSZ), ("values_bytes", PSZ), ("k_pool_bytes", SZ),
+                ("v_pool_bytes", SZ), ("block_table_bytes", SZ)]
 
 
 class MemoryStats(C.Structure):
@@ -140,6 +169,14 @@ SIGNATURES = {
     "pam_set_decode_kernel": (I32, [P, I32]),
     "pam_set_gpu_timing": (I32, [P, C.c_bool]),
     "pam_engine_mixed_step": (I32, [P, C.POINTER(MixedRequest)]),
+    "pam_engine_set_config": (I32, [P, C.POINTER(EngineConfig)]),
+    "pam_engine_get_config": (I32, [P, C.POINTER(EngineConfig)]),
+    "pam_engine_prefill_flat": (I32, [P, C.POINTER(PrefillRequest), I32, I32]),
+    "pam_engine_decode_flat": (I32, [P, C.POINTER(DecodeRequest), I32]),
+    "pam_engine_append_flat": (I32, [P, C.POINTER(AppendRequest), I32]),
+    "pam_engine_decode_layers": (I32, [P, C.POINTER(DecodeLayersRequest)]),
+    "pam_engine_prefill_layers": (I32, [P, C.POINTER(PrefillLayersRequest)]),
+    "pam_engine_append_layers": (I32, [P, C.POINTER(AppendLayersRequest)]),
     "pam_engine_setup_noalloc": (I32, [P]),
     "pam_engine_decode_noalloc": (I32, [P, C.POINTER(DecodeRequest)]),
     "pam_fp8_quantize": (I32, [P, P, P, P, I64]),

@@ -188,6 +188,43 @@ class PagedAttentionEngine:
         """Test hook: leave every split-merge counter as an abandoned launch would."""
         self._check(lib().pam_debug_dirty_counters(self._ctx, int(arrivals)))
 
+    # --- splitThreshold / defaultWindowSize / defaultChunkSize (PagedAttentionEngine.swift:116-121)
+    def _config(self) -> _lib.EngineConfig:
+        c = _lib.EngineConfig()
+        self._check(lib().pam_engine_get_config(self._ctx, C.byref(c)))
+        return c
+
+    def _set_config(self, **kw):
+        c = self._config()
+        for k, v in kw.items():
+            setattr(c, k, int(v))
+        self._check(lib().pam_engine_set_config(self._ctx, C.byref(c)))
+
+    @property
+    def split_threshold(self) -> int:
+        """Tokens above which a prefill may run the multi-pass (split) form."""
+        return self._config().split_threshold
+
+    @split_threshold.setter
+    def split_threshold(self, v: int):
+        self._set_config(split_threshold=v)
+
+    @property
+    def default_window_size(self) -> int:
+        return self._config().default_window_size
+
+    @default_window_size.setter
+    def default_window_size(self, v: int):
+        self._set_config(default_window_size=v)
+
+    @property
+    def default_chunk_size(self) -> int:
+        return self._config().default_chunk_size
+
+    @default_chunk_size.setter
+    def default_chunk_size(self, v: int):
+        self._set_config(default_chunk_size=v)
+
     @property
     def last_stats(self) -> dict:
         s = _lib.Stats()
@@ -238,6 +275,101 @@ class PagedAttentionEngine:
         r = _lib.BackwardRequest(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_table), _ptr(d_out), _ptr(m),
                                  _ptr(l), _ptr(d_q), _ptr(d_k_pool), _ptr(d_v_pool), int(seq_len), layer.c())
         self._check(lib().pam_engine_backward(self._ctx, C.byref(r)))
+
+    # --- the flat overloads (PagedAttentionEngine.swift:713-760, 1012-1046, 1167-1201):
+    # the layer is built from the arguments, its window is window_size or
+    # defaultWindowSize; prefill's chunk_size (or defaultChunkSize) runs the chunk loop
+    def prefill_flat(self, q, k_pool, v_pool, block_table, seq_len, head_dim, num_heads, num_kv_heads, block_size,
+                     output, causal=True, data_type=PagedAttentionDataType.float16, window_size=0, chunk_size=0,
+                     k_scale=None, v_scale=None):
+        layer = PagedLayerSpec(head_dim, num_heads, num_kv_heads, block_size, data_type)
+        r = _lib.PrefillRequest(
+            _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_table), _ptr(output), int(seq_len), 0, layer.c(),
+            bool(causal), _ptr(k_scale), _ptr(v_scale), _nbytes(q), _nbytes(k_pool), _nbytes(v_pool),
+            _nbytes(block_table), _nbytes(output))
+        self._check(lib().pam_engine_prefill_flat(self._ctx, C.byref(r), int(window_size), int(chunk_size)))
+
+    def decode_flat(self, q, k_pool, v_pool, block_tables, seq_lengths, batch_size, max_num_blocks, head_dim,
+                    num_heads, num_kv_heads, block_size, output, data_type=PagedAttentionDataType.float16,
+                    window_size=0, k_scale=None, v_scale=None):
+        layer = PagedLayerSpec(head_dim, num_heads, num_kv_heads, block_size, data_type)
+        r = _lib.DecodeRequest(
+            _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_tables), _ptr(seq_lengths), _ptr(output), int(batch_size),
+            int(max_num_blocks), layer.c(), _ptr(k_scale), _ptr(v_scale), _nbytes(q), _nbytes(k_pool),
+            _nbytes(v_pool), _nbytes(block_tables), _nbytes(seq_lengths), _nbytes(output))
+        self._check(lib().pam_engine_decode_flat(self._ctx, C.byref(r), int(window_size)))
+
+    def append_to_cache_flat(self, keys, values, k_pool, v_pool, block_table, token_offset, num_new_tokens,
+                             num_heads, num_kv_heads, head_dim, block_size, data_type=PagedAttentionDataType.float16,
+                             window_size=0, k_scale=None, v_scale=None):
+        layer = PagedLayerSpec(head_dim, num_heads, num_kv_heads, block_size, data_type)
+        r = _lib.AppendRequest(
+            _ptr(keys), _ptr(values), _ptr(k_pool), _ptr(v_pool), _ptr(block_table), int(token_offset),
+            int(num_new_tokens), layer.c(), _ptr(k_scale), _ptr(v_scale), None, _nbytes(keys), _nbytes(values),
+            _nbytes(k_pool), _nbytes(v_pool), _nbytes(block_table))
+        self._check(lib().pam_engine_append_flat(self._ctx, C.byref(r), int(window_size)))
+
+    # --- multi-layer calls over one shared pool (PagedAttentionEngine.swift:1433-1895)
+    @staticmethod
+    def _arrays(bufs, layers):
+        n = len(layers)
+        ptrs = (C.c_void_p * max(n, 1))(*[_ptr(b) for b in bufs])
+        sizes = (C.c_size_t * max(n, 1))(*[_nbytes(b) for b in bufs])
+        return ptrs, sizes
+
+    def decode_layers(self, q_buffers, k_pool, v_pool, block_tables, seq_lengths, output_buffers, batch_size,
+                      max_num_blocks, layers, window_size=0, k_scale=None, v_scale=None):
+        """decodeLayers: each layer's Q into its output over the one pool; layers of one
+        spec share K/V reads (one launch for up to 16 query heads per kv head)."""
+        if len(q_buffers) != len(layers) or len(output_buffers) != len(layers):
+            raise PagedAttentionError("Invalid paged attention configuration: buffer/layer count mismatch")
+        n = len(layers)
+        qp, qs = self._arrays(q_buffers, layers)
+        op, os_ = self._arrays(output_buffers, layers)
+        specs = (_lib.LayerSpec * max(n, 1))(*[l.c() for l in layers])
+        r = _lib.DecodeLayersRequest(
+            C.cast(qp, _lib.PP), C.cast(op, _lib.PP), specs, n, _ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
+            _ptr(seq_lengths), int(batch_size), int(max_num_blocks), int(window_size), _ptr(k_scale), _ptr(v_scale),
+            qs, os_, _nbytes(k_pool), _nbytes(v_pool), _nbytes(block_tables), _nbytes(seq_lengths))
+        self._check(lib().pam_engine_decode_layers(self._ctx, C.byref(r)))
+
+    def prefill_layers(self, q_buffers, k_pool, v_pool, block_table, output_buffers, seq_len, layers, causal=True,
+                       window_size=0, k_scale=None, v_scale=None):
+        """prefillLayers: rows 0 .. seq_len-1 of every layer over the one pool."""
+        if len(q_buffers) != len(layers) or len(output_buffers) != len(layers):
+            raise PagedAttentionError("Invalid paged attention configuration: buffer/layer count mismatch")
+        n = len(layers)
+        qp, qs = self._arrays(q_buffers, layers)
+        op, os_ = self._arrays(output_buffers, layers)
+        specs = (_lib.LayerSpec * max(n, 1))(*[l.c() for l in layers])
+        r = _lib.PrefillLayersRequest(
+            C.cast(qp, _lib.PP), C.cast(op, _lib.PP), specs, n, _ptr(k_pool), _ptr(v_pool), _ptr(block_table),
+            int(seq_len), bool(causal), int(window_size), _ptr(k_scale), _ptr(v_scale), qs, os_, _nbytes(k_pool),
+            _nbytes(v_pool), _nbytes(block_table))
+        self._check(lib().pam_engine_prefill_layers(self._ctx, C.byref(r)))
+
+    def append_layers(self, keys, values, k_pool, v_pool, block_table, token_offset, num_new_tokens, layers,
+                      k_scale_buffers=None, v_scale_buffers=None):
+        """appendLayers: every layer's keys/values at the same positions of the one pool, in order."""
+        if len(keys) != len(layers) or len(values) != len(layers):
+            raise PagedAttentionError("Invalid paged attention configuration: buffer/layer count mismatch")
+        if k_scale_buffers is not None and len(k_scale_buffers) != len(layers):
+            raise PagedAttentionError("Invalid paged attention configuration: kScaleBuffers count must match "
+                                      "layers count")
+        if v_scale_buffers is not None and len(v_scale_buffers) != len(layers):
+            raise PagedAttentionError("Invalid paged attention configuration: vScaleBuffers count must match "
+                                      "layers count")
+        n = len(layers)
+        kp, ks = self._arrays(keys, layers)
+        vp, vs = self._arrays(values, layers)
+        specs = (_lib.LayerSpec * max(n, 1))(*[l.c() for l in layers])
+        ksp = C.cast(self._arrays(k_scale_buffers, layers)[0], _lib.PP) if k_scale_buffers is not None else None
+        vsp = C.cast(self._arrays(v_scale_buffers, layers)[0], _lib.PP) if v_scale_buffers is not None else None
+        r = _lib.AppendLayersRequest(
+            C.cast(kp, _lib.PP), C.cast(vp, _lib.PP), specs, n, _ptr(k_pool), _ptr(v_pool), _ptr(block_table),
+            int(token_offset), int(num_new_tokens), ksp, vsp, ks, vs, _nbytes(k_pool), _nbytes(v_pool),
+            _nbytes(block_table))
+        self._check(lib().pam_engine_append_layers(self._ctx, C.byref(r)))
 
     # --- mixed continuous-batching step (no reference counterpart)
     def mixed_step(self, q, output, k_pool, v_pool, block_tables, context_lens, query_lens, layer: PagedLayerSpec,

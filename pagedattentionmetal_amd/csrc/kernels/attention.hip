@@ -80,6 +80,36 @@ __device__ __forceinline__ PartRange part_range(const RowCtx &c, int part, int p
     return pr;
 }
 
+// Query-head slot v of kv head kvh in row out_row.  One layer (FL false): head
+// kvh * G + v of p.q / p.out.  Fused layers (FL, decodeLayers): slots run over
+// G * fused_layers heads, slot v being head kvh * G + v % G of layer v / G.
+__device__ __forceinline__ int64_t head_elem(const AttnParams &p, int out_row, int kvh, int g) {
+    return ((int64_t)out_row * p.num_heads + kvh * (p.num_heads / p.num_kv_heads) + g) * p.head_dim;
+}
+template <bool FL, typename T>
+__device__ __forceinline__ const T *q_head(const AttnParams &p, int out_row, int kvh, int v) {
+    if constexpr (!FL) {
+        return static_cast<const T *>(p.q) + head_elem(p, out_row, kvh, v);
+    } else {
+        const int G = p.num_heads / p.num_kv_heads, layer = v / G;
+        return static_cast<const T *>(p.layer_q[layer]) + head_elem(p, out_row, kvh, v - layer * G);
+    }
+}
+template <bool FL, typename T>
+__device__ __forceinline__ T *out_head(const AttnParams &p, int out_row, int kvh, int v) {
+    if constexpr (!FL) {
+        return static_cast<T *>(p.out) + head_elem(p, out_row, kvh, v);
+    } else {
+        const int G = p.num_heads / p.num_kv_heads, layer = v / G;
+        return static_cast<T *>(p.layer_out[layer]) + head_elem(p, out_row, kvh, v - layer * G);
+    }
+}
+// query-head slots per kv head
+template <bool FL>
+__device__ __forceinline__ int slot_group(const AttnParams &p) {
+    return (p.num_heads / p.num_kv_heads) * (FL ? p.fused_layers : 1);
+}
+
 // ------------------------------------------------------------------ KV slices
 
 template <typename KV>
@@ -163,7 +193,7 @@ struct MfmaShape {
 // the N side) and V with the transposing ds_read_b64_tr_b16 as the A operand of
 // O^T = V^T P^T (v_mfma_f32_16x16x16_f16), whose B operand is the S^T
 // accumulator layout itself (lane%16 = head, lane/16 = token quad).
-template <typename KV, int HD, int BLK>
+template <typename KV, int HD, int BLK, bool FL>
 __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, int kvh, const PartRange pr, f16 *kt,
                                           float &m_run, float &l_run, f32x4 (&o)[MfmaShape<KV, HD>::NO]) {
     using S = MfmaShape<KV, HD>;
@@ -172,16 +202,15 @@ __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, 
     constexpr bool kFp8 = sizeof(KV) == 1;
     constexpr bool kTileScale = kFp8 && BLK == kBlkTile;  // one block (one scale pair) per tile
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
-    const int H = p.num_heads;
-    const int G = H / p.num_kv_heads;
-    const int h = kvh * G + row;  // this lane's query head (N column)
-    const bool head_ok = row < G;
+    // this lane's query-head slot (N column): a head of kv head kvh, of one of
+    // the fused layers
+    const bool head_ok = row < slot_group<FL>(p);
     f16 *vt = kt + 16 * KL;
 
     // Q^T B operand: lane holds Q[h][32c + 8g .. +8] for chunk c
     f16x8 qv[NC];
     {
-        const f16 *qp = static_cast<const f16 *>(p.q) + ((int64_t)c.out_row * H + (head_ok ? h : 0)) * HD + 8 * grp;
+        const f16 *qp = q_head<FL, f16>(p, c.out_row, kvh, head_ok ? row : 0) + 8 * grp;
 #pragma unroll
         for (int i = 0; i < NC; i++) {
             f16x8 v = *reinterpret_cast<const f16x8 *>(qp + 32 * i);
@@ -444,7 +473,7 @@ __device__ __forceinline__ void mfma_item(const AttnParams &p, int r, int part, 
     }
     float m_run, l_run;
     f32x4 o[NO];
-    mfma_core<KV, HD, BLK>(p, c, kvh, pr, reinterpret_cast<f16 *>(smem) + wave * WT, m_run, l_run, o);
+    mfma_core<KV, HD, BLK, false>(p, c, kvh, pr, reinterpret_cast<f16 *>(smem) + wave * WT, m_run, l_run, o);
     float l_tot = l_run + shfl_xor(l_run, 16);
     l_tot += shfl_xor(l_tot, 32);
 
@@ -525,7 +554,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const AttnParams &p)
 // reset.  A row inside one unit is finished in registers.  No reduce kernel runs.  The partials of (unit u, row r) sit in slot
 // block u + r, unique because a row's units start where the previous row's end:
 // floats [((u + r) * Hkv + kvh) * G + g] * d for query head g of kv head kvh.
-template <typename KV, int HD, int BLK>
+template <typename KV, int HD, int BLK, bool FL>
 __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void attn_mfma_streamk(AttnParams p) {
     using S = MfmaShape<KV, HD>;
     constexpr int NO = S::NO, WT = S::WT;
@@ -574,13 +603,17 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
         return c;
     };
 
-    const int H = p.num_heads, Hkv = p.num_kv_heads, G = H / Hkv;
-    f16 *out = static_cast<f16 *>(p.out);
+    const int H = p.num_heads, Hkv = p.num_kv_heads;
+    const int G = slot_group<FL>(p);  // query-head slots per kv head (all fused layers)
+    const int nl = FL ? p.fused_layers : 1;
     // rows without keys: 0/0 as in the reference's m/l bookkeeping
     for (int rr = blockIdx.x; rr < rows; rr += gridDim.x)
         if (prefix[rr + 1] == prefix[rr]) {
             const int orow = ctx_of(rr).out_row;
-            for (int idx = tid; idx < H * HD; idx += NT) out[(int64_t)orow * H * HD + idx] = (f16)__builtin_nanf("");
+            for (int l = 0; l < nl; l++) {
+                f16 *ob = out_head<FL, f16>(p, orow, 0, l * (H / Hkv));
+                for (int idx = tid; idx < H * HD; idx += NT) ob[idx] = (f16)__builtin_nanf("");
+            }
         }
 
     const int NH = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
@@ -625,20 +658,19 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
 
         float m_run, l_run;
         f32x4 o[NO];
-        mfma_core<KV, HD, BLK>(p, c, kvh, pr, kt, m_run, l_run, o);
+        mfma_core<KV, HD, BLK, FL>(p, c, kvh, pr, kt, m_run, l_run, o);
         float l_tot = l_run + shfl_xor(l_run, 16);
         l_tot += shfl_xor(l_tot, 32);
-        f16 *orow = out + ((int64_t)c.out_row * H + kvh * G) * HD;  // this kv head's G heads
-
         if (nseg == 1) {
             if (head_ok) {
+                f16 *oh = out_head<FL, f16>(p, c.out_row, kvh, row);
                 const float inv = 1.0f / l_tot;
 #pragma unroll
                 for (int i = 0; i < NO; i++) {
                     f16x4 v;
 #pragma unroll
                     for (int q = 0; q < 4; q++) v[q] = (f16)(o[i][q] * inv);
-                    *reinterpret_cast<f16x4 *>(orow + row * HD + 16 * i + 4 * grp) = v;
+                    *reinterpret_cast<f16x4 *>(oh + 16 * i + 4 * grp) = v;
                 }
             }
             continue;
@@ -701,7 +733,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
                 f16x4 h;
 #pragma unroll
                 for (int q = 0; q < 4; q++) h[q] = (f16)(acc[q] * inv);
-                *reinterpret_cast<f16x4 *>(orow + 4 * v) = h;
+                *reinterpret_cast<f16x4 *>(out_head<FL, f16>(p, c.out_row, kvh, g) + (4 * v - g * HD)) = h;
             }
         }
     }
@@ -963,7 +995,8 @@ static hipError_t streamk_grid(int *grid) {
         hipError_t e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e == hipSuccess)
-            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_streamk<KV, HD, BLK>, 64 * kMfmaWaves, 0);
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_streamk<KV, HD, BLK, false>,
+                                                             64 * kMfmaWaves, 0);
         if (e != hipSuccess) return e;
         resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
     }
@@ -979,7 +1012,12 @@ static hipError_t launch_mfma_blk(const AttnParams &p, hipStream_t stream) {
         int grid = 0;
         const hipError_t e = streamk_grid<KV, HD, BLK>(&grid);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((attn_mfma_streamk<KV, HD, BLK>), dim3(grid), block, 0, stream, p);
+        // fused layers run on the same grid (the partial slots are planned for it;
+        // no wave waits on another, so residency is a matter of speed only)
+        if (p.fused_layers > 1)
+            hipLaunchKernelGGL((attn_mfma_streamk<KV, HD, BLK, true>), dim3(grid), block, 0, stream, p);
+        else
+            hipLaunchKernelGGL((attn_mfma_streamk<KV, HD, BLK, false>), dim3(grid), block, 0, stream, p);
         return hipGetLastError();
     }
     const dim3 grid(p.max_parts, p.num_kv_heads, p.rows);
@@ -1028,7 +1066,8 @@ bool mfma_streamk_plan(const AttnParams &p, int32_t dtype, int64_t *part_slots, 
     const hipError_t e = dtype == kF16 ? streamk_grid_kv<f16>(p.head_dim, p.block_size, &grid)
                                        : streamk_grid_kv<uint8_t>(p.head_dim, p.block_size, &grid);
     if (e != hipSuccess) return false;
-    const int64_t Hkv = p.num_kv_heads, G = p.num_heads / p.num_kv_heads;
+    const int64_t Hkv = p.num_kv_heads;
+    const int64_t G = (int64_t)(p.num_heads / p.num_kv_heads) * (p.fused_layers > 1 ? p.fused_layers : 1);
     const int64_t NH = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
     const int64_t units = (int64_t)grid * (kMfmaWaves / NH) / (Hkv / NH);
     *part_slots = (units + (int64_t)p.rows) * Hkv * G;

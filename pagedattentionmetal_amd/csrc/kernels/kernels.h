@@ -24,6 +24,10 @@ enum RowMode : int32_t {
     kRowRagged = 2,   // row r described by row_info[r] = {bt_row, k_lo, k_hi, q/out row}
 };
 
+// Layers whose query heads one decode launch can serve from each K/V tile (the
+// MFMA decode holds up to 16 query heads per kv head; G >= 4).
+constexpr int kMaxFusedLayers = 4;
+
 struct AttnParams {
     const void *q;             // [rows][H][d] (f32 for f32 caches, f16 otherwise)
     void *out;                 // [rows][H][d] same type as q
@@ -65,6 +69,14 @@ struct AttnParams {
     // chunk's q_offset are read from here, and the kernel writes them into the
     // pools.  Null: all keys come from the pools.
     const void *fuse_k, *fuse_v;
+    // decode over layers sharing one pool (decodeLayers): the heads of
+    // fused_layers layers share every K/V tile, so query-head slot v of a kv
+    // head is head v % G of layer v / G, read from layer_q[v / G] and written to
+    // layer_out[v / G].  fused_layers <= 1: p.q / p.out only.  Stream-K MFMA
+    // decode only (G * fused_layers <= 16).
+    int32_t fused_layers;
+    const void *layer_q[kMaxFusedLayers];
+    void *layer_out[kMaxFusedLayers];
     // tag of this launch for the merge counters: a counter holding another epoch
     // counts as zero arrivals, so counters need no reset.  The launchers set a
     // fresh nonzero epoch for every launch (a retried launch gets a new one).
@@ -188,7 +200,9 @@ struct PrefillSplit {
     int64_t slots = 0;
 };
 constexpr int64_t kPrefillSlotBytes = 8 * 64 * (64 + 2) * 4;  // one workgroup's O^T, m, l
-void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t groups, PrefillSplit &out);
+// allow_split false: grid order only (no item is cut into pieces).
+void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t groups, PrefillSplit &out,
+                        bool allow_split = true);
 bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size);
 
 }  // namespace pam

@@ -693,7 +693,8 @@ int32_t pf_fill(const std::vector<PfItem> &items, int64_t cap, int32_t groups, P
 }
 }  // namespace
 
-void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t groups, PrefillSplit &out) {
+void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t groups, PrefillSplit &out,
+                        bool allow_split) {
     constexpr int KT = kPrefillKT;
     const int32_t G = p.num_heads / p.num_kv_heads, tpw = kPrefillRows / G;
     std::vector<PfItem> items;
@@ -765,7 +766,7 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
     // The balanced split pays for its partials and, with many items per
     // workgroup, loses the side-by-side L2 sharing of the grid order: it is
     // taken only when it clearly shortens the estimated makespan.
-    if (grid_ids <= INT32_MAX && (double)lo > 0.95 * (double)grid_makespan) {
+    if (grid_ids <= INT32_MAX && (!allow_split || (double)lo > 0.95 * (double)grid_makespan)) {
         out.range.assign(grid_ids, make_int2(0, 0));
         for (int64_t b = 0; b < grid_ids; b++) {
             if (grid_item[b] < 0) continue;

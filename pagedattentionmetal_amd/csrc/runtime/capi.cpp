@@ -255,6 +255,57 @@ PAM_API int32_t pam_engine_decode(void *context, const pam_decode_request *reque
     return guarded(context, [&](Context *ctx) { ctx->decode(*request); });
 }
 
+PAM_API int32_t pam_engine_set_config(void *context, const pam_engine_config *config) {
+    if (!config) return -1;
+    return guarded(context, [&](Context *ctx) {
+        if (config->split_threshold < 0 || config->default_window_size < 0 || config->default_chunk_size < 0)
+            throw invalid_configuration("engine settings must be non-negative.");
+        ctx->split_threshold = config->split_threshold;
+        ctx->default_window_size = config->default_window_size;
+        ctx->default_chunk_size = config->default_chunk_size;
+    });
+}
+
+PAM_API int32_t pam_engine_get_config(void *context, pam_engine_config *out) {
+    if (!out) return -1;
+    return guarded(context, [&](Context *ctx) {
+        out->split_threshold = ctx->split_threshold;
+        out->default_window_size = ctx->default_window_size;
+        out->default_chunk_size = ctx->default_chunk_size;
+    });
+}
+
+PAM_API int32_t pam_engine_prefill_flat(void *context, const pam_prefill_request *request, int32_t window_size,
+                                        int32_t chunk_size) {
+    if (!request) return -1;
+    return guarded(context, [&](Context *ctx) { ctx->prefill_flat(*request, window_size, chunk_size); });
+}
+
+PAM_API int32_t pam_engine_decode_flat(void *context, const pam_decode_request *request, int32_t window_size) {
+    if (!request) return -1;
+    return guarded(context, [&](Context *ctx) { ctx->decode_flat(*request, window_size); });
+}
+
+PAM_API int32_t pam_engine_append_flat(void *context, const pam_append_request *request, int32_t window_size) {
+    if (!request) return -1;
+    return guarded(context, [&](Context *ctx) { ctx->append_flat(*request, window_size); });
+}
+
+PAM_API int32_t pam_engine_decode_layers(void *context, const pam_decode_layers_request *request) {
+    if (!request) return -1;
+    return guarded(context, [&](Context *ctx) { ctx->decode_layers(*request); });
+}
+
+PAM_API int32_t pam_engine_prefill_layers(void *context, const pam_prefill_layers_request *request) {
+    if (!request) return -1;
+    return guarded(context, [&](Context *ctx) { ctx->prefill_layers(*request); });
+}
+
+PAM_API int32_t pam_engine_append_layers(void *context, const pam_append_layers_request *request) {
+    if (!request) return -1;
+    return guarded(context, [&](Context *ctx) { ctx->append_layers(*request); });
+}
+
 PAM_API int32_t pam_engine_setup_noalloc(void *context) {
     return guarded(context, [&](Context *ctx) { ctx->setup_noalloc(); });
 }

@@ -223,6 +223,7 @@ void Context::record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t b
     last_stats.num_blocks = blocks;
     last_stats.temporary_bytes = tmp;
     last_stats.used_split_pass = split ? 1 : 0;
+    last_stats.chunks = (op >= PAM_OP_PREFILL_SINGLE_PASS && op <= PAM_OP_PREFILL_TILED_PASS) ? 1 : 0;
     last_stats.elapsed_ms = last_stats.kernel_ms = last_stats.reduce_ms = -1.0;
     stats_pending_ = gpu_timing;
     stats_has_mid_ = has_mid;
@@ -355,8 +356,13 @@ void Context::dirty_counters(int32_t arrivals) {
 }
 
 Context::DensePlan Context::plan_dense_prefill(AttnParams &p, const int4 *chunks, int32_t n, StageList &sl) {
+    // splitThreshold (PagedAttentionEngine.swift:116-117, :1952-1958): only
+    // prefills past it may use the multi-pass form, here items cut into pieces
+    // whose partial states are merged in the kernel
+    int64_t longest = 0;
+    for (int32_t c = 0; c < n; c++) longest = std::max<int64_t>(longest, (int64_t)chunks[c].y + chunks[c].z);
     PrefillSplit ps;
-    prefill_split_plan(chunks, n, p, cus_, ps);
+    prefill_split_plan(chunks, n, p, cus_, ps, longest > split_threshold);
     DensePlan d;
     d.o_work = sl.add(ps.work.data(), ps.work.size() * sizeof(int4));
     d.o_range = sl.add(ps.range.data(), ps.range.size() * sizeof(int2));
@@ -406,9 +412,9 @@ void Context::decode(const pam_decode_request &r) { decode_checked(r, false); }
 
 void Context::decode_noalloc(const pam_decode_request &r) { decode_checked(r, true); }
 
-void Context::decode_checked(const pam_decode_request &r, bool noalloc) {
+// validateDecode (PagedAttentionEngine.swift:1916-1934)
+static void validate_decode(const pam_decode_request &r) {
     validate_layer(r.layer);
-    // validateDecode (PagedAttentionEngine.swift:1916-1934)
     if (r.batch_size <= 0) throw invalid_configuration("batchSize must be positive.");
     if (r.max_num_blocks <= 0) throw invalid_configuration("maxNumBlocks must be positive.");
     if (r.block_tables_bytes != 0 &&
@@ -425,6 +431,10 @@ void Context::decode_checked(const pam_decode_request &r, bool noalloc) {
         throw invalid_configuration("FP8 decode needs the K and V scale pools.");
     if (!r.q || !r.k_pool || !r.v_pool || !r.block_tables || !r.seq_lengths || !r.output)
         throw invalid_configuration("decode request has a null buffer.");
+}
+
+void Context::decode_checked(const pam_decode_request &r, bool noalloc) {
+    validate_decode(r);
     char *fixed = nullptr;
     if (noalloc) {
         // set up by pam_engine_setup_noalloc: this path creates nothing itself
@@ -437,22 +447,28 @@ void Context::decode_checked(const pam_decode_request &r, bool noalloc) {
             decode_gpu(r, fixed);
         } catch (const PamError &e) {
             std::fprintf(stderr, "[pam] decode failed: %s\n", e.what());
-            zero_output(r.output, (size_t)(r.batch_size * q_bytes_per_token(l)));
+            zero_output(r.output, (size_t)(r.batch_size * q_bytes_per_token(r.layer)));
         }
     } else {
         decode_gpu(r, fixed);
     }
 }
 
-void Context::decode_gpu(const pam_decode_request &r, char *fixed) {
+// Kernel choice, parameters and split workspace of one decode launch.  With
+// `fused` > 1 the launch serves that many consecutive layers of `layers_q` /
+// `layers_out` (same spec, shared pool): the stream-K MFMA kernel reads each K/V
+// tile once for all of their heads.
+Context::DecodePlan Context::plan_decode(const pam_decode_request &r, char *fixed, int32_t fused,
+                                         const void *const *layers_q, void *const *layers_out) {
     const pam_layer_spec &l = r.layer;
     const int32_t G = l.num_heads / l.num_kv_heads;
+    DecodePlan d{};
     bool use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size) && G >= 4;
     if (decode_kernel_choice == 1) use_mfma = false;
     if (decode_kernel_choice == 2) use_mfma = mfma_supported(l.data_type, l.head_dim, G, l.block_size);
     const int32_t nh = heads_per_wave(G);
 
-    AttnParams p{};
+    AttnParams &p = d.p;
     p.q = r.q;
     p.out = r.output;
     p.k_pool = r.k_pool;
@@ -473,26 +489,331 @@ void Context::decode_gpu(const pam_decode_request &r, char *fixed) {
     p.heads_per_wave = nh;
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
     p.zero_page = fixed ? static_cast<const void *>(fixed) : zero_page_;
+    if (fused > 1) {
+        if (!use_mfma || fused > kMaxFusedLayers || G * fused > 16) throw PamError("decode layers cannot be fused");
+        p.fused_layers = fused;
+        for (int32_t i = 0; i < fused; i++) {
+            p.layer_q[i] = layers_q[i];
+            p.layer_out[i] = layers_out[i];
+        }
+    }
 
     const int64_t cap_tokens = (int64_t)r.max_num_blocks * l.block_size;
     int64_t max_tiles = ceil_div(cap_tokens, 16);
     if (l.window_size > 0) max_tiles = std::min<int64_t>(max_tiles, l.window_size / 16 + 2);
     const int64_t waves = (int64_t)r.batch_size * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-    const int64_t tmp = plan_split(p, l.data_type, use_mfma, max_tiles, waves, fixed);
+    d.tmp = plan_split(p, l.data_type, use_mfma, max_tiles, waves, fixed);
+    if (fused > 1 && p.seg_count == nullptr) throw PamError("decode layers cannot be fused");
+    d.use_mfma = use_mfma;
+    return d;
+}
+
+// Layers that one stream-K launch can serve together (0: this layer cannot be
+// fused with others).
+int32_t Context::fusable_layers(const pam_decode_request &r) {
+    const pam_layer_spec &l = r.layer;
+    const int32_t G = l.num_heads / l.num_kv_heads;
+    if (decode_kernel_choice == 1 || part_tokens_override != 0 || G < 4) return 0;
+    if (!mfma_supported(l.data_type, l.head_dim, G, l.block_size)) return 0;
+    AttnParams p{};
+    p.rows = r.batch_size;
+    p.num_heads = l.num_heads;
+    p.num_kv_heads = l.num_kv_heads;
+    p.head_dim = l.head_dim;
+    p.block_size = l.block_size;
+    int64_t slots = 0, counters = 0;
+    if (!mfma_streamk_plan(p, l.data_type, &slots, &counters)) return 0;
+    return std::min<int32_t>(kMaxFusedLayers, 16 / G);
+}
+
+void Context::decode_gpu(const pam_decode_request &r, char *fixed) {
+    const DecodePlan d = plan_decode(r, fixed, 1, nullptr, nullptr);
+    const pam_layer_spec &l = r.layer;
     with_retry("decodeFlat", [&] {
         mark(ev0_);
-        check_launch([&] { return launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr); }, "decode");
+        check_launch([&] { return launch_attention(d.p, l.data_type, d.use_mfma, stream(), gpu_timing ? evmid_ : nullptr); }, "decode");
         mark(ev1_);
         finish("decode");
     });
-    record_stats(PAM_OP_DECODE, r.batch_size, 0, r.max_num_blocks, tmp, p.max_parts > 1 || p.seg_count != nullptr, true);
+    record_stats(PAM_OP_DECODE, r.batch_size, 0, r.max_num_blocks, d.tmp, d.p.max_parts > 1 || d.p.seg_count != nullptr,
+                 true);
+}
+
+// decodeLayers (PagedAttentionEngine.swift:1641-1741): every layer decodes its
+// own Q into its own output over the one pool, table and lengths; a window
+// argument > 0 overrides each layer's window.  Consecutive layers of one spec
+// that the stream-K kernel serves run as one launch per group (each K/V tile
+// read once for all of their heads); the others run one launch per layer.  All
+// launches of the call are one retried unit on the context's stream.
+void Context::decode_layers(const pam_decode_layers_request &r) {
+    if (r.num_layers < 0 || (r.num_layers > 0 && (!r.q || !r.output || !r.layers)))
+        throw invalid_configuration("buffer/layer count mismatch");
+    const int32_t n = r.num_layers;
+    if (n == 0) return;
+    std::vector<pam_decode_request> reqs((size_t)n);
+    for (int32_t i = 0; i < n; i++) {
+        pam_decode_request &q = reqs[i];
+        q = pam_decode_request{};
+        q.q = r.q[i];
+        q.output = r.output[i];
+        q.k_pool = r.k_pool;
+        q.v_pool = r.v_pool;
+        q.block_tables = r.block_tables;
+        q.seq_lengths = r.seq_lengths;
+        q.batch_size = r.batch_size;
+        q.max_num_blocks = r.max_num_blocks;
+        q.layer = r.layers[i];
+        if (r.window_size > 0) q.layer.window_size = r.window_size;
+        q.k_scale = r.k_scale;
+        q.v_scale = r.v_scale;
+        q.q_bytes = r.q_bytes ? r.q_bytes[i] : 0;
+        q.output_bytes = r.output_bytes ? r.output_bytes[i] : 0;
+        q.k_pool_bytes = r.k_pool_bytes;
+        q.v_pool_bytes = r.v_pool_bytes;
+        q.block_tables_bytes = r.block_tables_bytes;
+        q.seq_lengths_bytes = r.seq_lengths_bytes;
+        validate_decode(q);
+    }
+    ensure_device();
+    if (graceful_degradation) {
+        try {
+            decode_layers_gpu(reqs);
+        } catch (const PamError &e) {
+            std::fprintf(stderr, "[pam] decodeLayers failed: %s\n", e.what());
+            for (const auto &q : reqs) zero_output(q.output, (size_t)(q.batch_size * q_bytes_per_token(q.layer)));
+        }
+    } else {
+        decode_layers_gpu(reqs);
+    }
+}
+
+static bool same_spec(const pam_layer_spec &a, const pam_layer_spec &b) {
+    return a.head_dim == b.head_dim && a.num_heads == b.num_heads && a.num_kv_heads == b.num_kv_heads &&
+           a.block_size == b.block_size && a.data_type == b.data_type && a.window_size == b.window_size;
+}
+
+void Context::decode_layers_gpu(const std::vector<pam_decode_request> &reqs) {
+    // groups of consecutive layers: [first, first + count)
+    std::vector<std::pair<int32_t, int32_t>> groups;
+    for (int32_t i = 0; i < (int32_t)reqs.size();) {
+        const int32_t cap = std::max<int32_t>(1, fusable_layers(reqs[i]));
+        int32_t j = i + 1;
+        while (j < (int32_t)reqs.size() && j - i < cap && same_spec(reqs[j].layer, reqs[i].layer)) j++;
+        groups.emplace_back(i, j - i);
+        i = j;
+    }
+    int64_t tmp = 0;
+    bool split = false;
+    with_retry("decodeLayers", [&] {
+        mark(ev0_);
+        for (const auto &g : groups) {
+            std::vector<const void *> qs;
+            std::vector<void *> outs;
+            for (int32_t k = 0; k < g.second; k++) {
+                qs.push_back(reqs[g.first + k].q);
+                outs.push_back(reqs[g.first + k].output);
+            }
+            // launches of the call run in stream order, so they share the workspace
+            const DecodePlan d = plan_decode(reqs[g.first], nullptr, g.second, qs.data(), outs.data());
+            tmp = std::max(tmp, d.tmp);
+            split = split || d.p.max_parts > 1 || d.p.seg_count != nullptr;
+            check_launch([&] { return launch_attention(d.p, reqs[g.first].layer.data_type, d.use_mfma, stream()); },
+                         "decodeLayers");
+        }
+        mark(ev1_);
+        finish("decodeLayers");
+    });
+    last_fused_groups = (int32_t)groups.size();
+    record_stats(PAM_OP_DECODE, reqs[0].batch_size, 0, reqs[0].max_num_blocks, tmp, split, false);
+}
+
+// prefillLayers (PagedAttentionEngine.swift:1433-1639): causal (or full)
+// prefill of rows 0 .. seq_len-1 of every layer over the one pool and table; a
+// window argument > 0 overrides each layer's window.  One launch per layer (the
+// prefill is MFMA-bound: sharing K/V reads across layers would save little),
+// all in one retried unit on the context's stream.
+void Context::prefill_layers(const pam_prefill_layers_request &r) {
+    if (r.num_layers < 0 || (r.num_layers > 0 && (!r.q || !r.output || !r.layers)))
+        throw invalid_configuration("buffer/layer count mismatch");
+    const int32_t n = r.num_layers;
+    if (n == 0) return;
+    std::vector<pam_prefill_request> reqs((size_t)n);
+    for (int32_t i = 0; i < n; i++) {
+        pam_prefill_request &q = reqs[i];
+        q = pam_prefill_request{};
+        q.q = r.q[i];
+        q.output = r.output[i];
+        q.k_pool = r.k_pool;
+        q.v_pool = r.v_pool;
+        q.block_table = r.block_table;
+        q.seq_len = r.seq_len;
+        q.q_offset = 0;
+        q.layer = r.layers[i];
+        if (r.window_size > 0) q.layer.window_size = r.window_size;
+        q.causal = r.causal;
+        q.k_scale = r.k_scale;
+        q.v_scale = r.v_scale;
+        q.q_bytes = r.q_bytes ? r.q_bytes[i] : 0;
+        q.output_bytes = r.output_bytes ? r.output_bytes[i] : 0;
+        q.k_pool_bytes = r.k_pool_bytes;
+        q.v_pool_bytes = r.v_pool_bytes;
+        q.block_table_bytes = r.block_table_bytes;
+        validate_prefill(q);
+    }
+    ensure_device();
+    auto run = [&] {
+        int64_t tmp = 0;
+        bool split = false;
+        with_retry("prefillLayers", [&] {
+            mark(ev0_);
+            for (const auto &q : reqs) {
+                // a layer's work list is staged on the stream ahead of its launch
+                const PrefillPlan pl = plan_prefill(q);
+                tmp = std::max(tmp, pl.tmp);
+                split = split || (pl.dense ? pl.p.pf_part != nullptr : (pl.p.max_parts > 1 || pl.p.seg_count != nullptr));
+                launch_prefill_plan(pl, q.layer.data_type, false);
+            }
+            mark(ev1_);
+            finish("prefillLayers");
+        });
+        record_stats(PAM_OP_PREFILL_MMA, 1, r.seq_len, (int32_t)ceil_div(r.seq_len, reqs[0].layer.block_size), tmp,
+                     split, false);
+    };
+    if (graceful_degradation) {
+        try {
+            run();
+        } catch (const PamError &e) {
+            std::fprintf(stderr, "[pam] prefillLayers failed: %s\n", e.what());
+            for (const auto &q : reqs) zero_output(q.output, (size_t)(q.seq_len * q_bytes_per_token(q.layer)));
+        }
+    } else {
+        run();
+    }
+}
+
+// appendLayers (PagedAttentionEngine.swift:1744-1895): every layer's new keys and
+// values are appended, in layer order, at the same positions of the one pool
+// (FP8: with that layer's scale pools), so a later layer's rows replace an
+// earlier one's, as in the reference.  One retried unit on the stream.
+void Context::append_layers(const pam_append_layers_request &r) {
+    if (r.num_layers < 0 || (r.num_layers > 0 && (!r.keys || !r.values || !r.layers)))
+        throw invalid_configuration("buffer/layer count mismatch");
+    const int32_t n = r.num_layers;
+    if (n == 0) return;
+    std::vector<pam_append_request> reqs((size_t)n);
+    for (int32_t i = 0; i < n; i++) {
+        pam_append_request &a = reqs[i];
+        a = pam_append_request{};
+        a.keys = r.keys[i];
+        a.values = r.values[i];
+        a.k_pool = r.k_pool;
+        a.v_pool = r.v_pool;
+        a.block_table = r.block_table;
+        a.token_offset = r.token_offset;
+        a.num_new_tokens = r.num_new_tokens;
+        a.layer = r.layers[i];
+        a.k_scale = r.k_scale ? r.k_scale[i] : nullptr;
+        a.v_scale = r.v_scale ? r.v_scale[i] : nullptr;
+        a.keys_bytes = r.keys_bytes ? r.keys_bytes[i] : 0;
+        a.values_bytes = r.values_bytes ? r.values_bytes[i] : 0;
+        a.k_pool_bytes = r.k_pool_bytes;
+        a.v_pool_bytes = r.v_pool_bytes;
+        a.block_table_bytes = r.block_table_bytes;
+        validate_append(a);
+    }
+    ensure_device();
+    auto run = [&] {
+        with_retry("appendLayers", [&] {
+            mark(ev0_);
+            for (const auto &a : reqs) {
+                const AppendParams ap = append_params(a);
+                check_launch([&] { return launch_append(ap, a.layer.data_type, stream()); }, "appendLayers");
+            }
+            mark(ev1_);
+            finish("appendLayers");
+        });
+        record_stats(PAM_OP_APPEND, 1, r.num_new_tokens, 0, 0, false, false);
+    };
+    if (graceful_degradation) {
+        try {
+            run();
+        } catch (const PamError &e) {
+            std::fprintf(stderr, "[pam] appendLayers failed: %s\n", e.what());
+        }
+    } else {
+        run();
+    }
+}
+
+// ------------------------------------------------------------------ flat overloads
+
+static int32_t effective(int32_t arg, int32_t dflt) { return arg > 0 ? arg : dflt; }
+
+void Context::decode_flat(const pam_decode_request &r, int32_t window_size) {
+    pam_decode_request q = r;
+    q.layer.window_size = effective(window_size, default_window_size);
+    decode(q);
+}
+
+void Context::append_flat(const pam_append_request &r, int32_t window_size) {
+    pam_append_request a = r;
+    a.layer.window_size = effective(window_size, default_window_size);
+    append(a);
+}
+
+// The reference's chunk loop (:740-756) prefills rows [0, end) for every chunk
+// end in turn; each pass overwrites the rows of the one before, so its result is
+// the last pass, the unchunked prefill.  Here a causal prefill without window
+// runs its chunks as query-offset pieces [start, end) - one launch per chunk,
+// every row computed once, each exactly as the unchunked prefill computes it
+// (a causal row reads only keys up to itself).  A full or windowed prefill, whose
+// rows depend on the final length, runs as the one pass that decides the result.
+void Context::prefill_flat(const pam_prefill_request &r, int32_t window_size, int32_t chunk_size) {
+    pam_prefill_request q = r;
+    q.layer.window_size = effective(window_size, default_window_size);
+    const int32_t chunk = effective(chunk_size, default_chunk_size);
+    if (chunk <= 0 || r.seq_len <= chunk || !r.causal || q.layer.window_size > 0 || r.q_offset != 0) {
+        prefill(q);
+        last_stats.chunks = chunk > 0 && r.seq_len > chunk ? (int32_t)ceil_div(r.seq_len, chunk) : 1;
+        return;
+    }
+    validate_prefill(q);
+    const int64_t qrow = q_bytes_per_token(q.layer);
+    int32_t n = 0;
+    for (int32_t start = 0; start < r.seq_len; start += chunk, n++) {
+        pam_prefill_request c = q;
+        c.seq_len = std::min(chunk, r.seq_len - start);
+        c.q_offset = start;
+        c.q = static_cast<const char *>(r.q) + start * qrow;
+        c.output = static_cast<char *>(r.output) + start * qrow;
+        c.q_bytes = r.q_bytes ? r.q_bytes - (size_t)(start * qrow) : 0;
+        c.output_bytes = r.output_bytes ? r.output_bytes - (size_t)(start * qrow) : 0;
+        prefill(c);
+    }
+    last_stats.chunks = n;
 }
 
 // ------------------------------------------------------------------ prefill
 
 void Context::prefill(const pam_prefill_request &r) {
+    validate_prefill(r);
+    const pam_layer_spec &l = r.layer;
+    ensure_device();
+    if (graceful_degradation) {
+        try {
+            prefill_gpu(r);
+        } catch (const PamError &e) {
+            std::fprintf(stderr, "[pam] prefill failed: %s\n", e.what());
+            zero_output(r.output, (size_t)(r.seq_len * q_bytes_per_token(l)));
+        }
+    } else {
+        prefill_gpu(r);
+    }
+}
+
+// validatePrefill (PagedAttentionEngine.swift:1897-1914)
+void Context::validate_prefill(const pam_prefill_request &r) {
     validate_layer(r.layer);
-    // validatePrefill (PagedAttentionEngine.swift:1897-1914)
     if (r.seq_len <= 0) throw invalid_configuration("seqLen must be positive.");
     if (r.q_offset < 0) throw invalid_configuration("qOffset must be non-negative.");
     const pam_layer_spec &l = r.layer;
@@ -507,17 +828,6 @@ void Context::prefill(const pam_prefill_request &r) {
         throw invalid_configuration("FP8 prefill needs the K and V scale pools.");
     if (!r.q || !r.k_pool || !r.v_pool || !r.block_table || !r.output)
         throw invalid_configuration("prefill request has a null buffer.");
-    ensure_device();
-    if (graceful_degradation) {
-        try {
-            prefill_gpu(r);
-        } catch (const PamError &e) {
-            std::fprintf(stderr, "[pam] prefill failed: %s\n", e.what());
-            zero_output(r.output, (size_t)(r.seq_len * q_bytes_per_token(l)));
-        }
-    } else {
-        prefill_gpu(r);
-    }
 }
 
 Context::PrefillPlan Context::plan_prefill(const pam_prefill_request &r) {
@@ -565,11 +875,12 @@ Context::PrefillPlan Context::plan_prefill(const pam_prefill_request &r) {
     return pl;
 }
 
-void Context::launch_prefill_plan(const PrefillPlan &pl, int32_t dtype) {
+void Context::launch_prefill_plan(const PrefillPlan &pl, int32_t dtype, bool mark_mid) {
+    hipEvent_t mid = gpu_timing && mark_mid ? evmid_ : nullptr;
     if (pl.dense)
         check_launch([&] { return launch_prefill_mfma(pl.p, dtype, stream()); }, "prefill");
     else
-        check_launch([&] { return launch_attention(pl.p, dtype, pl.use_mfma, stream(), gpu_timing ? evmid_ : nullptr); }, "prefill");
+        check_launch([&] { return launch_attention(pl.p, dtype, pl.use_mfma, stream(), mid); }, "prefill");
 }
 
 void Context::prefill_gpu(const pam_prefill_request &r) {
@@ -708,8 +1019,22 @@ void Context::backward(const pam_backward_request &r) {
 // ------------------------------------------------------------------ append
 
 void Context::append(const pam_append_request &r) {
+    validate_append(r);
+    ensure_device();
+    if (graceful_degradation) {
+        try {
+            append_gpu(r);
+        } catch (const PamError &e) {
+            std::fprintf(stderr, "[pam] appendToCache failed: %s\n", e.what());
+        }
+    } else {
+        append_gpu(r);
+    }
+}
+
+// validateAppend (PagedAttentionEngine.swift:1936-1950)
+void Context::validate_append(const pam_append_request &r) {
     validate_layer(r.layer);
-    // validateAppend (PagedAttentionEngine.swift:1936-1950)
     if (r.token_offset < 0) throw invalid_configuration("tokenOffset must be non-negative.");
     if (r.num_new_tokens <= 0) throw invalid_configuration("numNewTokens must be positive.");
     const pam_layer_spec &l = r.layer;
@@ -727,16 +1052,6 @@ void Context::append(const pam_append_request &r) {
         throw PamError("Unsupported paged attention path: FP8 append takes a block table, not a slot mapping.");
     if (!r.keys || !r.values || !r.k_pool || !r.v_pool || (!r.block_table && !r.slot_mapping))
         throw invalid_configuration("append request has a null buffer.");
-    ensure_device();
-    if (graceful_degradation) {
-        try {
-            append_gpu(r);
-        } catch (const PamError &e) {
-            std::fprintf(stderr, "[pam] appendToCache failed: %s\n", e.what());
-        }
-    } else {
-        append_gpu(r);
-    }
 }
 
 AppendParams Context::append_params(const pam_append_request &r) {

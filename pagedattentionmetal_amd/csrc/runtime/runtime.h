@@ -100,6 +100,14 @@ class Context {
     // decode with the split-context workspace, counters and zero page in the
     // library's fixed per-device scratch: no allocation (setup_noalloc first)
     void decode_noalloc(const pam_decode_request &r);
+    // decodeLayers / prefillLayers / appendLayers: per-layer buffers over one
+    // shared pool
+    void decode_layers(const pam_decode_layers_request &r);
+    void prefill_layers(const pam_prefill_layers_request &r);
+    void append_layers(const pam_append_layers_request &r);
+    static void validate_prefill(const pam_prefill_request &r);
+    static void validate_append(const pam_append_request &r);
+    int32_t last_fused_groups = 0;  // launches the last decode_layers call made
     void setup_noalloc();
     void prefill(const pam_prefill_request &r);
     void append(const pam_append_request &r);
@@ -112,6 +120,17 @@ class Context {
     pam_stats last_stats{};
     pam_stats stats();  // last_stats with event timings resolved
     bool graceful_degradation = true;
+    // splitThreshold, defaultWindowSize, defaultChunkSize
+    // (PagedAttentionEngine.swift:116-121)
+    int32_t split_threshold = 1024;
+    int32_t default_window_size = 0;
+    int32_t default_chunk_size = 0;
+    // the flat overloads: prefill(q:...:windowSize:chunkSize:) (:713-760),
+    // decode(q:...:windowSize:) (:1012-1046), appendToCache(keys:...:windowSize:)
+    // (:1167-1201)
+    void prefill_flat(const pam_prefill_request &r, int32_t window_size, int32_t chunk_size);
+    void decode_flat(const pam_decode_request &r, int32_t window_size);
+    void append_flat(const pam_append_request &r, int32_t window_size);
     int32_t max_retries = 3;
     int32_t consecutive_failures = 0;
     int32_t fail_next_launches = 0;
@@ -144,6 +163,15 @@ class Context {
     void zero_output(void *ptr, size_t bytes);
     void decode_checked(const pam_decode_request &r, bool noalloc);
     void decode_gpu(const pam_decode_request &r, char *fixed);
+    struct DecodePlan {
+        AttnParams p;
+        bool use_mfma;
+        int64_t tmp;
+    };
+    DecodePlan plan_decode(const pam_decode_request &r, char *fixed, int32_t fused, const void *const *layers_q,
+                           void *const *layers_out);
+    int32_t fusable_layers(const pam_decode_request &r);
+    void decode_layers_gpu(const std::vector<pam_decode_request> &reqs);
     void prefill_gpu(const pam_prefill_request &r);
     void append_gpu(const pam_append_request &r);
     void fused_prefill_gpu(const pam_fused_prefill_request &r);
@@ -154,7 +182,7 @@ class Context {
         int64_t tmp, kv_len;
     };
     PrefillPlan plan_prefill(const pam_prefill_request &r);
-    void launch_prefill_plan(const PrefillPlan &pl, int32_t dtype);
+    void launch_prefill_plan(const PrefillPlan &pl, int32_t dtype, bool mark_mid = true);
     AppendParams append_params(const pam_append_request &r);
     int32_t choose_part_tokens(int64_t items_per_part, int64_t max_tiles, bool mfma);
     int64_t plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves,

@@ -15,11 +15,18 @@ newcomers and sequences already prefilled:
   pauses running sequences, newest first, until enough blocks are free, then
   their blocks are released and they must be prefilled again later.
 
-The attention of a step runs as ONE ``mixed_step`` launch set: the newcomers'
-prompts as causal prefill chunks and the prefilled sequences as single-token
-decode rows, with synthetic new K/V appended at their positions (the
-reference issues a prefill per newcomer and then one batched decode, on
-uninitialised Q buffers and without writing K/V).  Sequences the step
+With one layer, the attention of a step runs as ONE ``mixed_step`` launch
+set: the newcomers' prompts as causal prefill chunks and the prefilled
+sequences as single-token decode rows, with synthetic new K/V appended at their
+positions (the reference issues a prefill per newcomer and then one batched
+decode, on uninitialised Q buffers and without writing K/V).
+
+With several layers (``layer`` a list of specs over the one shared pool, the
+reference's ``layerSpecs``), the step makes the reference's calls: per
+newcomer, its prompt's synthetic K/V appended and ``prefill_layers`` over its
+rows (handlePrefill, :172-219); then, for the prefilled sequences, their new
+tokens' K/V appended (one slot-mapped append) and one ``decode_layers`` over
+the batch (handleDecode, :221-278), every layer with its own Q and output.  Sequences the step
 preempts are left out of its launch (the reference would still decode them
 from freed blocks).  Q and the new K/V are synthetic: there is no model.
 
@@ -46,7 +53,8 @@ class PagedAttentionInference:
         self.engine = engine
         self.cache = cache
         self.scheduler = scheduler
-        self.layer = layer
+        self.layers = list(layer) if isinstance(layer, (list, tuple)) else [layer]
+        self.layer = self.layers[0]
         self.attend = attend
         self.prefilled: set[int] = set()
         self.step_count = 0
@@ -120,7 +128,10 @@ class PagedAttentionInference:
             self.cache.append_tokens(sid, 1)  # the new token's slot, written by the step
 
         if self.attend and (newcomers or decoding):
-            self._launch(newcomers, decoding, prompts, lens)
+            if len(self.layers) > 1:
+                self._launch_layers(newcomers, decoding, prompts, lens)
+            else:
+                self._launch(newcomers, decoding, prompts, lens)
 
         for sid in newcomers:  # :205-217
             self.scheduler.mark_prefilled(sid)
@@ -206,6 +217,65 @@ class PagedAttentionInference:
         c = self.cache
         self.engine.mixed_step(q, out, c.k_pool(), c.v_pool(), bt, ctx, ql, self.layer, new_keys=nk, new_values=nv,
                                k_scale=c.k_scale(), v_scale=c.v_scale())
+
+
+    def _layer_buffers(self, rows):
+        """Per-layer synthetic Q and outputs (rows x H x d), and the step's new K/V."""
+        import torch
+        if rows > getattr(self, "_lbuf_rows", 0):
+            n = max(rows, 2 * getattr(self, "_lbuf_rows", 0), 1024)
+            g = torch.Generator(device="cuda")
+            g.manual_seed(int(self._rng.integers(1 << 31)))
+            dt = torch.float32 if self.layer.data_type == 0 else torch.float16
+            self._lq = [torch.randn((n, l.num_heads, l.head_dim), generator=g, device="cuda", dtype=dt)
+                        for l in self.layers]
+            self._lout = [torch.empty_like(q) for q in self._lq]
+            L = self.layer
+            self._lk = torch.randn((n, L.num_kv_heads, L.head_dim), generator=g, device="cuda", dtype=dt).mul_(0.5)
+            self._lv = torch.randn((n, L.num_kv_heads, L.head_dim), generator=g, device="cuda", dtype=dt).mul_(0.5)
+            self._lbuf_rows = n
+        return ([q[:rows] for q in self._lq], [o[:rows] for o in self._lout], self._lk[:rows], self._lv[:rows])
+
+    def _launch_layers(self, newcomers, decoding, prompts, lens):
+        """The reference's per-step calls over all layers (PagedAttentionInference.swift:172-278)."""
+        import torch
+        c, eng, L = self.cache, self.engine, self.layer
+        bs = c.block_size
+        fp8 = L.data_type == 2
+        scales = dict(k_scale=c.k_scale(), v_scale=c.v_scale()) if fp8 else {}
+        self.last_launch = None
+        for sid in newcomers:  # handlePrefill: one prefillLayers per newcomer
+            T = prompts[sid]
+            bt = torch.tensor(c.get_block_table(sid), dtype=torch.int32, device="cuda")
+            qs, outs, nk, nv = self._layer_buffers(T)
+            eng.append_to_cache(nk, nv, c.k_pool(), c.v_pool(), bt, 0, T, L, **scales)
+            eng.prefill_layers(qs, c.k_pool(), c.v_pool(), bt, outs, T, self.layers, causal=True, **scales)
+            self.attended_pairs += self._pairs(np.array([0]), np.array([T])) * len(self.layers)
+        if not decoding:
+            return
+        # handleDecode: the new tokens' K/V at their positions, then one decodeLayers
+        B = len(decoding)
+        qs, outs, nk, nv = self._layer_buffers(B)
+        if fp8:  # FP8 appends take a block table (per-block scale rule)
+            for i, sid in enumerate(decoding):
+                bt = torch.tensor(c.get_block_table(sid), dtype=torch.int32, device="cuda")
+                eng.append_to_cache(nk[i:i + 1], nv[i:i + 1], c.k_pool(), c.v_pool(), bt, lens[sid], 1, L, **scales)
+        else:
+            slots = []
+            for sid in decoding:
+                t = c.get_block_table(sid)
+                pos = lens[sid]
+                slots.append(t[pos // bs] * bs + pos % bs)
+            sm = torch.tensor(slots, dtype=torch.int64, device="cuda")
+            eng.append_to_cache(nk, nv, c.k_pool(), c.v_pool(), None, 0, B, L, slot_mapping=sm)
+        width = max((lens[s] + 1 + bs - 1) // bs for s in decoding)
+        bt = torch.zeros((B, width), dtype=torch.int32, device="cuda")
+        sl = torch.zeros(B, dtype=torch.int32, device="cuda")
+        c.batch_view(decoding, bt, sl, width)
+        eng.decode_layers(qs, c.k_pool(), c.v_pool(), bt, sl, outs, B, width, self.layers, **scales)
+        ctx = np.array([lens[s] for s in decoding], np.int32)
+        self.attended_pairs += self._pairs(ctx, np.ones(B, np.int32)) * len(self.layers)
+        self.last_launch = (ctx, np.ones(B, np.int32))
 
 
 def poisson_trace(inference: PagedAttentionInference, steps: int, rate: float, prompt_range, output_range,

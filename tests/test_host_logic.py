@@ -418,3 +418,40 @@ def test_injected_launch_failure_enqueues_nothing(pam, ctx):
     body = src[i:src.index("\n}\n", i)]
     # the injected failure throws before launch() is called
     assert body.index("fail_next_launches--") < body.index("launch()")
+
+
+def test_engine_config_surface():
+    """splitThreshold / defaultWindowSize / defaultChunkSize (PagedAttentionEngine.swift:116-121):
+    reference defaults, settable, negative values refused."""
+    from pagedattentionmetal_amd import api
+    eng = api.PagedAttentionEngine()
+    assert (eng.split_threshold, eng.default_window_size, eng.default_chunk_size) == (1024, 0, 0)
+    eng.split_threshold = 4096
+    eng.default_window_size = 256
+    eng.default_chunk_size = 512
+    assert (eng.split_threshold, eng.default_window_size, eng.default_chunk_size) == (4096, 256, 512)
+    with pytest.raises(api.PagedAttentionError, match="non-negative"):
+        eng.default_chunk_size = -1
+    assert eng.default_chunk_size == 512
+    eng.close()
+
+
+def test_layers_calls_validate_before_any_launch(pam, ctx):
+    """decodeLayers / prefillLayers / appendLayers: count mismatches raise the
+    reference's error; zero layers is a no-op; a bad layer fails validation
+    before any device work."""
+    from pagedattentionmetal_amd import _lib, api
+    eng = api.PagedAttentionEngine()
+    lay = api.PagedLayerSpec(64, 4, 2, 16, 1)
+    with pytest.raises(api.PagedAttentionError, match="buffer/layer count mismatch"):
+        eng.decode_layers([0x1000], 0x1000, 0x1000, 0x1000, 0x1000, [], 1, 1, [lay])
+    with pytest.raises(api.PagedAttentionError, match="buffer/layer count mismatch"):
+        eng.prefill_layers([0x1000, 0x1000], 0x1000, 0x1000, 0x1000, [0x1000], 4, [lay, lay])
+    with pytest.raises(api.PagedAttentionError, match="kScaleBuffers count"):
+        eng.append_layers([0x1000], [0x1000], 0x1000, 0x1000, 0x1000, 0, 4, [lay], k_scale_buffers=[])
+    r = _lib.DecodeLayersRequest()
+    assert pam.pam_engine_decode_layers(ctx, C.byref(r)) == 0  # zero layers
+    bad = api.PagedLayerSpec(64, 3, 2, 16, 1)  # H % Hkv != 0
+    with pytest.raises(api.PagedAttentionError, match="divisible"):
+        eng.decode_layers([0x1000], 0x1000, 0x1000, 0x1000, 0x1000, [0x1000], 1, 1, [bad])
+    eng.close()
