@@ -67,6 +67,28 @@ def decode_setup(k, torch, api, workloads):
     return w, eng, (q, kp, vp, bt, lens, out, layer, ks, vs)
 
 
+def event_steps(torch, stream, step, n, depth=2):
+    """Per-step GPU times (ms) from HIP events recorded on `stream` around each
+    step, with at most `depth` steps in flight (a serving loop waits for each
+    step's output; a queue thousands of launches deep is not a serving loop and
+    measured unsteady).  Returns the list of n durations."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i in range(n):
+        if i >= depth:
+            ev[i - depth][1].synchronize()
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in ev]
+
+
+def median(xs):
+    xs = sorted(xs)
+    n = len(xs)
+    return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+
+
 def time_decode(torch, eng, w, t, steps, warmup):
     q, kp, vp, bt, lens, out, layer, ks, vs = t
     stream = torch.cuda.current_stream()
@@ -88,6 +110,8 @@ def time_decode(torch, eng, w, t, steps, warmup):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    # BASELINE's timing rule: HIP events around each step, median of the steps
+    med = median(event_steps(torch, stream, step, max(steps, 100)))
     eng.set_gpu_timing(True)
     # per-kernel durations: HIP events recorded by the engine around each launch
     kern, red = [], []
@@ -99,7 +123,7 @@ def time_decode(torch, eng, w, t, steps, warmup):
     torch.cuda.synchronize()
     kern_ms = sum(kern) / len(kern)
     red_ms = sum(red) / len(red)
-    return ms, kern_ms, red_ms
+    return ms, kern_ms, red_ms, med
 
 
 def mixed_setup(torch, api, workloads):
@@ -124,7 +148,8 @@ def mixed_setup(torch, api, workloads):
 
 def time_mixed(torch, eng, w, t, steps, warmup):
     """Whole mixed step (append + prefill chunks + decode rows), then the prefill
-    chunks alone (the dense prefill kernel, timed by the engine's HIP events)."""
+    chunks alone (the dense prefill kernel, timed by the engine's HIP events);
+    both the median over the timed steps."""
     q, kp, vp, bt, nk, nv, out, layer = t
     stream = torch.cuda.current_stream()
     eng.set_stream(stream)
@@ -140,18 +165,13 @@ def time_mixed(torch, eng, w, t, steps, warmup):
         eng.mixed_step(q[:rows_ch], out[:rows_ch], kp, vp, bt[:nch], ctx[:nch], ql[:nch], layer)
 
     assert (ql[:nch] > 1).all() and (ql[nch:] == 1).all()
-    # the timed steps run as a serving loop would: no per-call timing events
+    # the timed steps run as a serving loop would: no per-call timing events,
+    # each step's output awaited before the step after next is issued (event_steps)
     eng.set_gpu_timing(False)
     for _ in range(max(warmup, 1)):
         step()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    ms = median(event_steps(torch, stream, step, max(steps, 100)))
     eng.set_gpu_timing(True)
     for _ in range(max(warmup, 1)):
         prefill_only()
@@ -160,7 +180,7 @@ def time_mixed(torch, eng, w, t, steps, warmup):
         prefill_only()
         kern.append(eng.last_stats["kernel_ms"])
     torch.cuda.synchronize()
-    return ms, sum(kern) / len(kern)
+    return ms, median(kern)
 
 
 def compact_rows(torch, w, t, B):
@@ -346,13 +366,14 @@ def main():
     if args.only:
         k = int(args.only[1])
         wk, ek, tk = decode_setup(k, torch, api, workloads)
-        msk, kk, rk = time_decode(torch, ek, wk, tk, args.steps, args.warmup)
+        msk, kk, rk, mk = time_decode(torch, ek, wk, tk, args.steps, args.warmup)
         print(json.dumps({args.only: {"ms_per_step": round(msk, 5), "kernel_ms": round(kk, 5),
+                                      "kernel_ms_median": round(mk, 5),
                                       "kv_GBps": round(wk.kv_bytes() / (msk * 1e-3) / 1e9, 2)}}), flush=True)
         return
     log("bench: c2 decode setup")
     w, eng, t = decode_setup(2, torch, api, workloads)
-    ms, kern_ms, red_ms = time_decode(torch, eng, w, t, args.steps, args.warmup)
+    ms, kern_ms, red_ms, med_ms = time_decode(torch, eng, w, t, args.steps, args.warmup)
     kv = w.kv_bytes()
     gbs = kv / (ms * 1e-3) / 1e9
     # A c2 step is exactly one launch of the decode kernel (stream-K: no reduce,
@@ -421,6 +442,7 @@ def main():
                      "kernel": "attn_mfma_streamk<f16,128,bs16> (stream-K split, partials merged in the "
                                "kernel; no reduce launch)",
                      "kernel_ms": round(ms, 5),
+                     "kernel_ms_median": round(med_ms, 5),
                      "kernel_ms_per_launch_events": round(kern_ms, 5)},
         "cpu_baseline": cpu,
         "prefill": {"workload": "c3: mixed continuous-batching step, 8 chunks x 512 new tokens (context "
@@ -453,11 +475,14 @@ def main():
         for k, sample in ((1, None), (4, 16), (5, 4)):
             log(f"bench: c{k} decode")
             wk, ek, tk = decode_setup(k, torch, api, workloads)
-            msk, kk, rk = time_decode(torch, ek, wk, tk, args.steps, args.warmup)
+            msk, kk, rk, mk = time_decode(torch, ek, wk, tk, args.steps, args.warmup)
             b = wk.kv_bytes()
+            # c4 and c5 are one launch per step (stream-K, no reduce): the loop's
+            # time per step is the kernel's; c1 adds the reduce kernel
             cfgs[f"c{k}"] = {"ms_per_step": round(msk, 5), "kv_GBps": round(b / (msk * 1e-3) / 1e9, 2),
                              "kernel_ms": round(kk, 5), "reduce_ms": round(rk, 5),
-                             "kernel_frac_hbm": round(b / (kk * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "kernel_ms_median": round(mk, 5),
+                             "kernel_frac_hbm": round(b / (msk * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                              "tokens_per_s": round(wk.batch / (msk * 1e-3), 1)}
             if not args.no_cpu:
                 threads = max(1, min(16, os.cpu_count() or 1))

@@ -70,7 +70,8 @@ Context::~Context() {
     if (evmid_) (void)hipEventDestroy(evmid_);
     if (handoff_) (void)hipEventDestroy(handoff_);
     if (zero_page_) (void)hipFree(zero_page_);
-    if (staged_) (void)hipEventDestroy(staged_);
+    for (auto &e : seg_event_)
+        if (e) (void)hipEventDestroy(e);
     if (own_stream_) (void)hipStreamDestroy(own_stream_);
 }
 
@@ -88,7 +89,7 @@ void Context::ensure_device() {
     hip_check(hipEventCreate(&ev1_), "hipEventCreate");
     hip_check(hipEventCreate(&evmid_), "hipEventCreate");
     hip_check(hipEventCreateWithFlags(&handoff_, hipEventDisableTiming), "hipEventCreate");
-    hip_check(hipEventCreateWithFlags(&staged_, hipEventDisableTiming), "hipEventCreate");
+    for (auto &e : seg_event_) hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
     // zeros that masked lanes of the attention kernels load instead of pool rows
     hip_check(hipMalloc(&zero_page_, kZeroPageBytes), "hipMalloc zero page");
     hip_check(hipMemset(zero_page_, 0, kZeroPageBytes), "hipMemset zero page");
@@ -138,34 +139,47 @@ void *Context::device_scratch(int slot, size_t bytes) {
 }
 
 // Host bytes -> pinned staging -> device memory, ordered on the stream.  The
-// pinned arena is reused once the copies staged from it have completed.
+// pinned arena is a ring of kStageSegs segments; each segment's last copy
+// records an event, and a segment is refilled only after the event it recorded
+// on its previous use, so the host waits for copies several calls old (already
+// done in a steady serving loop) instead of draining the stream when the arena
+// wraps.
 void *Context::stage_into(void *dst, const void *host, size_t bytes) {
     if (bytes == 0) return dst;
     const size_t need = (bytes + 255) & ~(size_t)255;
-    if (pinned_used_ + need > pinned_bytes_) {
-        hip_check(hipEventSynchronize(staged_), "staging wait");
+    const size_t seg = pinned_bytes_ / kStageSegs;
+    if (need > seg) {
+        // grow: every staged copy must be done with the old arena
+        for (int i = 0; i < kStageSegs; i++)
+            if (seg_used_[i]) hip_check(hipEventSynchronize(seg_event_[i]), "staging wait");
+        if (pinned_) hip_check(hipHostFree(pinned_), "hipHostFree");
+        pinned_ = nullptr;
+        pinned_bytes_ = 0;
+        const size_t want = std::max<size_t>(need * kStageSegs, (size_t)4 << 20);
+        hip_check(hipHostMalloc(&pinned_, want, hipHostMallocMapped), "hipHostMalloc");
+        hip_check(hipHostGetDevicePointer(&pinned_dev_, pinned_, 0), "hipHostGetDevicePointer");
+        pinned_bytes_ = want;
+        for (int i = 0; i < kStageSegs; i++) seg_used_[i] = false;
+        cur_seg_ = 0;
         pinned_used_ = 0;
-        if (need > pinned_bytes_) {
-            if (pinned_) hip_check(hipHostFree(pinned_), "hipHostFree");
-            pinned_ = nullptr;
-            pinned_bytes_ = 0;
-            size_t want = std::max<size_t>(need, 1 << 20);
-            hip_check(hipHostMalloc(&pinned_, want, hipHostMallocMapped), "hipHostMalloc");
-            hip_check(hipHostGetDevicePointer(&pinned_dev_, pinned_, 0), "hipHostGetDevicePointer");
-            pinned_bytes_ = want;
-        }
+    } else if (pinned_used_ + need > seg) {
+        cur_seg_ = (cur_seg_ + 1) % kStageSegs;
+        pinned_used_ = 0;
+        if (seg_used_[cur_seg_]) hip_check(hipEventSynchronize(seg_event_[cur_seg_]), "staging wait");
     }
-    char *src = static_cast<char *>(pinned_) + pinned_used_;
+    const size_t off = (size_t)cur_seg_ * (pinned_bytes_ / kStageSegs) + pinned_used_;
+    char *src = static_cast<char *>(pinned_) + off;
     std::memcpy(src, host, bytes);
     // a copy kernel on this stream (a DMA-engine copy would cost an engine
     // hand-off around the call); destinations are 256-byte aligned allocations
-    const char *src_dev = static_cast<const char *>(pinned_dev_) + pinned_used_;
+    const char *src_dev = static_cast<const char *>(pinned_dev_) + off;
     pinned_used_ += need;
     if (((uintptr_t)dst & 15) == 0)
         hip_check(launch_stage_copy(src_dev, dst, bytes, stream()), "staging copy");
     else
         hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream()), "hipMemcpyAsync staging");
-    hip_check(hipEventRecord(staged_, stream()), "hipEventRecord");
+    hip_check(hipEventRecord(seg_event_[cur_seg_], stream()), "hipEventRecord");
+    seg_used_[cur_seg_] = true;
     return dst;
 }
 

@@ -204,7 +204,12 @@ class Context {
     int cus_ = 256;  // compute units of the device (set in ensure_device)
     hipStream_t own_stream_ = nullptr, ext_stream_ = nullptr;
     bool use_ext_stream_ = false;
-    hipEvent_t ev0_ = nullptr, ev1_ = nullptr, evmid_ = nullptr, staged_ = nullptr, handoff_ = nullptr;
+    hipEvent_t ev0_ = nullptr, ev1_ = nullptr, evmid_ = nullptr, handoff_ = nullptr;
+    // pinned staging ring: kStageSegs segments, each with the event of its last copy
+    static constexpr int kStageSegs = 4;
+    hipEvent_t seg_event_[kStageSegs] = {};
+    bool seg_used_[kStageSegs] = {};
+    int cur_seg_ = 0;
     void *zero_page_ = nullptr;
     bool stats_pending_ = false;
     bool stats_has_mid_ = false;
