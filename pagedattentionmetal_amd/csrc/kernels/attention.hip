@@ -138,6 +138,11 @@ constexpr int kStreamKMaxRows = 2048;
 // Decode rows whose key ranges the stream-K form keeps in LDS (8 KiB: three
 // workgroups of the e4m3 kernel still fit a CU).
 constexpr int kStreamKRangeCache = 1024;
+// Rounds of 64 pieces (256 floats) of a (row, kv head)'s partials that the
+// stream-K merge folds together (its loads in flight per batch: 4 units x this);
+// d = 64 runs three workgroups per CU and has registers for two.
+template <int HD>
+constexpr int kMergeRounds = 2;
 // Fewest tiles per stream-K unit: shorter units would only add partials.
 constexpr int kStreamKMinTiles = 8;
 
@@ -697,43 +702,76 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
 
         // Last unit of this (row, kv head): merge all partials, the whole wave at
         // once.  The G * HD floats of one unit are contiguous; the lane owns the
-        // 4-float pieces v = lane + 64 k (head 4v / HD), four units in flight.
-        const int nv = G * HD / 4;
-        for (int k = 0; k * 64 < nv; k++) {
-            const int v = lane + 64 * k < nv ? lane + 64 * k : lane;  // inactive lanes re-read piece `lane`
-            const int g = (4 * v) / HD;
-            float M = -INFINITY, den = 0.0f;
-            f32x4 acc = (f32x4)0.0f;
-            auto fold = [&](const f32x2 ml, const f32x4 ov) {
-                const float Mn = fmaxf(M, ml[0]);
-                const float a = M == -INFINITY ? 0.0f : exp2f(M - Mn);
+        // 4-float pieces v = lane + 64 k (head 4v / HD).  Up to kMergeRounds
+        // rounds k are merged together, four units at a time, so every batch of
+        // loads covers 4 * kMergeRounds partials (the merge's dependent load
+        // batches, not its arithmetic, set its time).  Each piece folds the
+        // units in ascending order: the result does not depend on the batching.
+        constexpr int R = kMergeRounds<HD>;
+        const int nv = G * HD / 4, rounds = (nv + 63) / 64;
+        for (int k0 = 0; k0 < rounds; k0 += R) {
+            int v[R], g[R];
+            float M[R], den[R];
+            f32x4 acc[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int kv = lane + 64 * (k0 + r);
+                v[r] = kv < nv ? kv : lane;  // inactive lanes (and rounds) re-read piece `lane`
+                g[r] = (4 * v[r]) / HD;
+                M[r] = -INFINITY;
+                den[r] = 0.0f;
+                acc[r] = (f32x4)0.0f;
+            }
+            auto fold = [&](int r, const f32x2 ml, const f32x4 ov) {
+                const float Mn = fmaxf(M[r], ml[0]);
+                const float a = M[r] == -INFINITY ? 0.0f : exp2f(M[r] - Mn);
                 const float b = ml[0] == -INFINITY ? 0.0f : exp2f(ml[0] - Mn);
-                den = den * a + ml[1] * b;
-                acc = acc * a + ov * b;
-                M = Mn;
+                den[r] = den[r] * a + ml[1] * b;
+                acc[r] = acc[r] * a + ov * b;
+                M[r] = Mn;
             };
-            auto ld_ml = [&](int64_t uu) {
-                return __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)((slot0(uu) + g) * 8), 0, kSc1);
+            auto ld_ml = [&](int64_t uu, int r) {
+                return __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)((slot0(uu) + g[r]) * 8), 0, kSc1);
             };
-            auto ld_o = [&](int64_t uu) {
-                return __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(slot0(uu) * HD * 4) + 16 * v, 0, kSc1);
+            auto ld_o = [&](int64_t uu, int r) {
+                return __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(slot0(uu) * HD * 4) + 16 * v[r], 0, kSc1);
             };
             int64_t uu = first;
             for (; uu + 3 <= last; uu += 4) {
-                const f32x2 m0 = ld_ml(uu), m1 = ld_ml(uu + 1), m2 = ld_ml(uu + 2), m3 = ld_ml(uu + 3);
-                const f32x4 o0 = ld_o(uu), o1 = ld_o(uu + 1), o2 = ld_o(uu + 2), o3 = ld_o(uu + 3);
-                fold(m0, o0);
-                fold(m1, o1);
-                fold(m2, o2);
-                fold(m3, o3);
-            }
-            for (; uu <= last; uu++) fold(ld_ml(uu), ld_o(uu));
-            if (lane + 64 * k < nv) {
-                const float inv = 1.0f / den;
-                f16x4 h;
+                f32x2 m[4][R];
+                f32x4 o[4][R];
 #pragma unroll
-                for (int q = 0; q < 4; q++) h[q] = (f16)(acc[q] * inv);
-                *reinterpret_cast<f16x4 *>(out_head<FL, f16>(p, c.out_row, kvh, g) + (4 * v - g * HD)) = h;
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        m[j][r] = ld_ml(uu + j, r);
+                        o[j][r] = ld_o(uu + j, r);
+                    }
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) fold(r, m[j][r], o[j][r]);
+            }
+            for (; uu <= last; uu++) {
+                f32x2 m[R];
+                f32x4 o[R];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    m[r] = ld_ml(uu, r);
+                    o[r] = ld_o(uu, r);
+                }
+#pragma unroll
+                for (int r = 0; r < R; r++) fold(r, m[r], o[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                if (lane + 64 * (k0 + r) < nv) {
+                    const float inv = 1.0f / den[r];
+                    f16x4 h;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) h[q] = (f16)(acc[r][q] * inv);
+                    *reinterpret_cast<f16x4 *>(out_head<FL, f16>(p, c.out_row, kvh, g[r]) + (4 * v[r] - g[r] * HD)) = h;
+                }
             }
         }
     }
