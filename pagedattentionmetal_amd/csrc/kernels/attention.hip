@@ -139,9 +139,10 @@ constexpr int kStreamKMaxRows = 2048;
 // workgroups of the e4m3 kernel still fit a CU).
 constexpr int kStreamKRangeCache = 1024;
 // Rounds of 64 pieces (256 floats) of a (row, kv head)'s partials that the
-// stream-K merge folds together (its loads in flight per batch: 4 units x this);
-// d = 64 runs three workgroups per CU and has registers for two.
-template <int HD>
+// stream-K merge folds together (its loads in flight per batch: 4 units x this).
+// Measured on gfx950 against 1 and 4: 2 is best on c2, c4 and c5 (4 raises the
+// kernel's registers to 254 and slows c2; d = 64, three workgroups per CU,
+// spills at 4).
 constexpr int kMergeRounds = 2;
 // Fewest tiles per stream-K unit: shorter units would only add partials.
 constexpr int kStreamKMinTiles = 8;
@@ -707,7 +708,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
         // loads covers 4 * kMergeRounds partials (the merge's dependent load
         // batches, not its arithmetic, set its time).  Each piece folds the
         // units in ascending order: the result does not depend on the batching.
-        constexpr int R = kMergeRounds<HD>;
+        constexpr int R = kMergeRounds;
         const int nv = G * HD / 4, rounds = (nv + 63) / 64;
         for (int k0 = 0; k0 < rounds; k0 += R) {
             int v[R], g[R];
