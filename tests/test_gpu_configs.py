@@ -139,14 +139,22 @@ def test_mixed_step_c3_full_size(torch):
             # prefill restates a chunk at [q_offset, q_offset + 16): its keys end at q_offset + 16 <= total
             e = row_rel_err(got[rows_], ref)
             assert e <= TOL[1], f"chunk {s} rows {i0}..{i0 + 16}: rel err {e:.3e}"
+    # every row of the chunks with the longest and the shortest cached context
+    chunks = np.nonzero(ql > 1)[0]
+    for s in (chunks[np.argmax(ctx[chunks])], chunks[np.argmin(ctx[chunks])]):
+        rows_ = slice(cu[s], cu[s] + ql[s])
+        ref = oracle.prefill(1, qh[rows_], kh, vh, cbt[s], int(ctx[s]), causal=True, n_threads=16)
+        e = row_rel_err(got[rows_], ref)
+        assert e <= TOL[1], f"chunk {s} (context {ctx[s]}), all {ql[s]} rows: rel err {e:.3e}"
 
 
 def test_mixed_step_c3_full_size_fp8(torch):
     """The c3 step over e4m3 pools: the cached context is quantised through the
     append kernel, the step appends the new tokens (FP8 rule) and attends with
     the dense prefill and the decode rows dequantising as they read.  Decode rows
-    all, prefill chunks on three 16-row slices each, against the oracle on the
-    pools the GPU wrote (compared after dequantisation)."""
+    all, prefill chunks on three 16-row slices each and every row of the chunk
+    with the longest context, against the oracle on the pools the GPU wrote
+    (compared after dequantisation)."""
     from pagedattentionmetal_amd import api, workloads
     w = workloads.mixed_config()
     g = torch.Generator(device="cuda")
@@ -202,3 +210,11 @@ def test_mixed_step_c3_full_size_fp8(torch):
                                  v_scale=vsh, n_threads=16)
             e = row_rel_err(got[rows_], ref)
             assert e <= TOL[2], f"chunk {s} rows {i0}..{i0 + 16}: rel err {e:.3e}"
+    # every row of the chunk with the longest cached context
+    chunks = np.nonzero(ql > 1)[0]
+    s = chunks[np.argmax(ctx[chunks])]
+    rows_ = slice(cu[s], cu[s] + ql[s])
+    ref = oracle.prefill(2, qh[rows_], kh, vh, cbt[s], int(ctx[s]), causal=True, k_scale=ksh, v_scale=vsh,
+                         n_threads=16)
+    e = row_rel_err(got[rows_], ref)
+    assert e <= TOL[2], f"chunk {s} (context {ctx[s]}), all {ql[s]} rows: rel err {e:.3e}"
