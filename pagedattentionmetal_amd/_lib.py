@@ -177,6 +177,12 @@ SIGNATURES = {
     "pam_engine_decode_layers": (I32, [P, C.POINTER(DecodeLayersRequest)]),
     "pam_engine_prefill_layers": (I32, [P, C.POINTER(PrefillLayersRequest)]),
     "pam_engine_append_layers": (I32, [P, C.POINTER(AppendLayersRequest)]),
+    "pam_module_load": (I32, [P, C.c_char_p]),
+    "pam_module_unload": (I32, [P]),
+    "pam_module_function": (I32, [P, C.c_char_p, C.POINTER(C.c_void_p)]),
+    "pam_module_launch": (I32, [P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                C.c_uint32, P, SZ]),
+    "pam_module_default_path": (C.c_char_p, []),
     "pam_engine_setup_noalloc": (I32, [P]),
     "pam_engine_decode_noalloc": (I32, [P, C.POINTER(DecodeRequest)]),
     "pam_fp8_quantize": (I32, [P, P, P, P, I64]),

@@ -181,6 +181,28 @@ class PagedAttentionEngine:
     def reserve_workspace(self, nbytes: int):
         self._check(lib().pam_reserve_workspace(self._ctx, int(nbytes)))
 
+    # --- code-object loading (the reference's pipeline manager, PagedAttentionEngine.swift:151-198)
+    def load_module(self, path: str = None):
+        """Launch the code object's entries (hipModuleLoad / hipModuleLaunchKernel);
+        default: libpam_kernels.hsaco beside libpam.so."""
+        path = path or lib().pam_module_default_path().decode()
+        self._check(lib().pam_module_load(self._ctx, path.encode()))
+
+    def unload_module(self):
+        self._check(lib().pam_module_unload(self._ctx))
+
+    def module_function(self, name: str) -> int:
+        f = C.c_void_p()
+        self._check(lib().pam_module_function(self._ctx, name.encode(), C.byref(f)))
+        return f.value
+
+    def module_launch(self, function: int, grid, block, args: bytes, shared_bytes: int = 0):
+        """Launch a code-object entry with its packed kernel arguments on the engine's stream."""
+        g = tuple(grid) + (1,) * (3 - len(grid))
+        b = tuple(block) + (1,) * (3 - len(block))
+        buf = C.create_string_buffer(bytes(args), len(args))
+        self._check(lib().pam_module_launch(self._ctx, function, *g, *b, int(shared_bytes), buf, len(args)))
+
     def debug_fail_next_launches(self, n: int):
         self._check(lib().pam_debug_fail_next_launches(self._ctx, int(n)))
 

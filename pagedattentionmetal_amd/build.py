@@ -57,12 +57,31 @@ def _compile(src: str) -> str:
     return obj
 
 
+MODULE_SRC = os.path.join(CSRC, "module", "module_entry.hip")
+MODULE = os.path.join(HERE, "libpam_kernels.hsaco")
+
+
+def _code_object() -> str:
+    """libpam_kernels.hsaco: the kernels' named entries as a gfx950 code object
+    (an ELF, not a bundle) for hipModuleLoad."""
+    tmp = MODULE + ".tmp"
+    cmd = [_hipcc(), "-O3", "-std=c++17", f"--offload-arch={ARCH}", "--cuda-device-only", "--no-gpu-bundle-output",
+           *DEVICE_FLAGS, MODULE_SRC, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {MODULE_SRC}:\n{r.stderr}")
+    os.replace(tmp, MODULE)
+    return MODULE
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
-    workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    workers = min(len(srcs) + 1, max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(workers) as ex:
+        module = ex.submit(_code_object)
         objs = list(ex.map(_compile, srcs))
+        module.result()
     tmp = LIB + ".tmp"
     cmd = [_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -70,7 +89,7 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {MODULE}")
     return LIB
 
 

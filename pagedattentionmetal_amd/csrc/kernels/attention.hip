@@ -154,14 +154,6 @@ enum BlockMode : int {
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
-// ds_read_b64_tr_b16: the 16 lanes of a group each address 4 consecutive halves
-// a[i][0..3]; lane o receives a[4j + o/4][o%4] for j = 0..3.
-__device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
-    const fp16x4_raw v =
-        __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) fp16x4_raw *)(p));
-    return __builtin_bit_cast(f16x4, v);
-}
 
 template <typename KV, int HD>
 struct MfmaShape {
@@ -561,7 +553,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const AttnParams &p)
 // block u + r, unique because a row's units start where the previous row's end:
 // floats [((u + r) * Hkv + kvh) * G + g] * d for query head g of kv head kvh.
 template <typename KV, int HD, int BLK, bool FL>
-__global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void attn_mfma_streamk(AttnParams p) {
+__device__ __forceinline__ void streamk_body(const AttnParams &p) {
     using S = MfmaShape<KV, HD>;
     constexpr int NO = S::NO, WT = S::WT;
     __shared__ __attribute__((aligned(16))) f16 tiles[kMfmaWaves * WT];
@@ -776,6 +768,13 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
             }
         }
     }
+}
+
+// The kernel (the fat binary's entry); streamk_body also backs the named
+// entries of the code object (module_entry.hip).
+template <typename KV, int HD, int BLK, bool FL>
+__global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void attn_mfma_streamk(AttnParams p) {
+    streamk_body<KV, HD, BLK, FL>(p);
 }
 
 // ------------------------------------------------------------------ VALU body
@@ -1043,14 +1042,31 @@ static hipError_t streamk_grid(int *grid) {
     return hipSuccess;
 }
 
+hipError_t streamk_occupancy(int32_t dtype, bool fused_layers, int *per_cu) {
+    const int t = 64 * kMfmaWaves;
+    if (dtype == kF16)
+        return fused_layers
+                   ? hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, attn_mfma_streamk<f16, 128, kBlkTile, true>, t, 0)
+                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, attn_mfma_streamk<f16, 128, kBlkTile, false>, t, 0);
+    if (dtype == kFP8)
+        return fused_layers
+                   ? hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, attn_mfma_streamk<uint8_t, 128, kBlkTile, true>, t, 0)
+                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, attn_mfma_streamk<uint8_t, 128, kBlkTile, false>, t, 0);
+    return hipErrorInvalidValue;
+}
+
 template <typename KV, int HD, int BLK>
-static hipError_t launch_mfma_blk(const AttnParams &p, hipStream_t stream) {
+static hipError_t launch_mfma_blk(const AttnParams &p, hipStream_t stream, const KernelTable *kt) {
     const dim3 block(64 * kMfmaWaves);
     if (p.seg_count != nullptr) {
         if (p.rows > kStreamKMaxRows) return hipErrorInvalidValue;
         int grid = 0;
         const hipError_t e = streamk_grid<KV, HD, BLK>(&grid);
         if (e != hipSuccess) return e;
+        if (kt && HD == 128 && BLK == kBlkTile) {
+            const hipFunction_t f = kt->streamk[sizeof(KV) == 1][p.fused_layers > 1];
+            if (f) return module_launch(f, dim3(grid), block, p, stream);
+        }
         // fused layers run on the same grid (the partial slots are planned for it;
         // no wave waits on another, so residency is a matter of speed only)
         if (p.fused_layers > 1)
@@ -1065,18 +1081,18 @@ static hipError_t launch_mfma_blk(const AttnParams &p, hipStream_t stream) {
 }
 
 template <typename KV, int HD>
-static hipError_t launch_mfma_hd(const AttnParams &p, hipStream_t stream) {
-    if (p.block_size % 16 == 0) return launch_mfma_blk<KV, HD, kBlkTile>(p, stream);
-    if (p.block_size == 8) return launch_mfma_blk<KV, HD, kBlkSmall>(p, stream);
+static hipError_t launch_mfma_hd(const AttnParams &p, hipStream_t stream, const KernelTable *kt) {
+    if (p.block_size % 16 == 0) return launch_mfma_blk<KV, HD, kBlkTile>(p, stream, kt);
+    if (p.block_size == 8) return launch_mfma_blk<KV, HD, kBlkSmall>(p, stream, kt);
     return hipErrorInvalidValue;
 }
 
 template <typename KV>
-static hipError_t launch_mfma(const AttnParams &p, hipStream_t stream) {
+static hipError_t launch_mfma(const AttnParams &p, hipStream_t stream, const KernelTable *kt) {
     switch (p.head_dim) {
-        case 64: return launch_mfma_hd<KV, 64>(p, stream);
-        case 128: return launch_mfma_hd<KV, 128>(p, stream);
-        case 256: return launch_mfma_hd<KV, 256>(p, stream);
+        case 64: return launch_mfma_hd<KV, 64>(p, stream, kt);
+        case 128: return launch_mfma_hd<KV, 128>(p, stream, kt);
+        case 256: return launch_mfma_hd<KV, 256>(p, stream, kt);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1132,7 +1148,7 @@ static hipError_t launch_valu(const AttnParams &p, hipStream_t stream) {
 }
 
 hipError_t launch_attention(const AttnParams &p_in, int32_t dtype, bool use_mfma, hipStream_t stream,
-                            hipEvent_t after_main) {
+                            hipEvent_t after_main, const KernelTable *kt) {
     if (p_in.rows <= 0) return hipSuccess;
     AttnParams p = p_in;
     p.epoch = next_launch_epoch();
@@ -1141,7 +1157,7 @@ hipError_t launch_attention(const AttnParams &p_in, int32_t dtype, bool use_mfma
     if (p.zero_page == nullptr || (size_t)p.head_dim * 4 > kZeroPageBytes) return hipErrorInvalidValue;
     hipError_t e;
     if (use_mfma) {
-        e = dtype == kF16 ? launch_mfma<f16>(p, stream) : launch_mfma<uint8_t>(p, stream);
+        e = dtype == kF16 ? launch_mfma<f16>(p, stream, kt) : launch_mfma<uint8_t>(p, stream, kt);
     } else {
         switch (dtype) {
             case kF32: e = launch_valu<float, float>(p, stream); break;

@@ -83,11 +83,31 @@ struct AttnParams {
     uint32_t epoch;
 };
 
+// Entry points of a loaded code object (libpam_kernels.hsaco, module_entry.hip).
+// A launcher given a table launches a configuration the table holds through
+// hipModuleLaunchKernel and any other through the library's own kernel; both
+// run the same kernel body.
+struct KernelTable {
+    hipFunction_t streamk[2][2];  // decode stream-K, d = 128, blocks >= 16: [f16, e4m3][one layer, fused layers]
+    hipFunction_t prefill[3];     // dense prefill, d = 128: f16, f16 with fused append, e4m3
+};
+// hipModuleLaunchKernel of `f` with the parameter block as its kernel arguments.
+inline hipError_t module_launch(hipFunction_t f, dim3 grid, dim3 block, const AttnParams &p, hipStream_t stream) {
+    size_t bytes = sizeof(AttnParams);
+    void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<AttnParams *>(&p), HIP_LAUNCH_PARAM_BUFFER_SIZE,
+                      &bytes, HIP_LAUNCH_PARAM_END};
+    return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, nullptr, config);
+}
+// Resident workgroups per CU of the library's stream-K kernel (dtype f16 / fp8,
+// d = 128, blocks >= 16, one layer or fused layers), for checking a code
+// object's entry against it.
+hipError_t streamk_occupancy(int32_t dtype, bool fused_layers, int *per_cu);
+
 // Paged attention over rows (decode / prefill-as-rows / ragged).  Chooses the
 // MFMA kernel for 4 <= H/Hkv <= 16 with f16/fp8 KV and d in {64,128,256},
 // otherwise the VALU kernel.  Launches the split-context reduce when max_parts > 1.
 hipError_t launch_attention(const AttnParams &p, int32_t dtype, bool use_mfma, hipStream_t stream,
-                            hipEvent_t after_main = nullptr);
+                            hipEvent_t after_main = nullptr, const KernelTable *kt = nullptr);
 bool mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size);
 // A fresh launch epoch for the merge counters: process-wide (one counter for the
 // whole library, an inline function's static), so launches of any context that
@@ -187,7 +207,8 @@ hipError_t launch_stream_copy(const void *src, void *dst, size_t bytes, int bloc
 
 // Dense chunked-prefill (MFMA, f16): rows [q_offset, q_offset + T) of one sequence.
 // Dense prefill (MFMA): f16 or e4m3 KV, d = 128; Q and O f16.
-hipError_t launch_prefill_mfma(const AttnParams &p, int32_t dtype, hipStream_t stream);
+hipError_t launch_prefill_mfma(const AttnParams &p, int32_t dtype, hipStream_t stream,
+                              const KernelTable *kt = nullptr);
 // Work list of the dense prefill kernel for chunks {bt_row, q_offset, len,
 // row_base} (host memory).  An item is (chunk, kv head, block of 256 / G query rows)
 // over its key tiles; items are cut into segments so that the `groups`

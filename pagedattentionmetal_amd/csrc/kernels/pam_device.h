@@ -24,6 +24,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 // whole-L2 writeback.
 constexpr int kSc1 = 16;
 
+typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
+// ds_read_b64_tr_b16: the 16 lanes of a group each address 4 consecutive halves
+// a[i][0..3]; lane o receives a[4j + o/4][o%4] for j = 0..3.
+__device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
+    const fp16x4_raw v =
+        __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) fp16x4_raw *)(p));
+    return __builtin_bit_cast(f16x4, v);
+}
+
 __device__ __forceinline__ f16 bits_to_f16(uint16_t b) { return __builtin_bit_cast(f16, b); }
 __device__ __forceinline__ uint16_t f16_to_bits(f16 h) { return __builtin_bit_cast(uint16_t, h); }
 

@@ -51,15 +51,6 @@ constexpr float kRescaleLog2 = 8.0f;           // lazy-rescale threshold (log2 u
 constexpr int kBtCache = 2048;                 // block-table entries a workgroup keeps in LDS
 constexpr int kXcds = 8;                       // accelerator dies (each with its own L2)
 
-typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
-
-// ds_read_b64_tr_b16: the 16 lanes of a group each address 4 consecutive halves
-// a[i][0..3]; lane o receives a[4j + o/4][o%4] for j = 0..3.
-__device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
-    const fp16x4_raw v =
-        __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) fp16x4_raw *)(p));
-    return __builtin_bit_cast(f16x4, v);
-}
 
 // LDS tiles (layouts checked against SQ_LDS_BANK_CONFLICT on gfx950).
 // K: rows of 128 + 8 halves, so the 16 consecutive rows one 16-lane pass of an
@@ -79,7 +70,7 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
 }
 
 template <int HD, int RB, bool FUSED, typename KV>
-__global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(AttnParams p) {
+__device__ __forceinline__ void prefill_body(const AttnParams &p) {
     // KV: f16 pools, or e4m3 codes (uint8_t) with a half scale per physical block
     constexpr bool FP8 = sizeof(KV) == 1;
     static_assert(!(FUSED && FP8), "the fused append is f16 only");
@@ -586,20 +577,32 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
     }
 }
 
+// The kernel (the fat binary's entry); prefill_body also backs the named
+// entries of the code object (module_entry.hip).
+template <int HD, int RB, bool FUSED, typename KV>
+__global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(AttnParams p) {
+    prefill_body<HD, RB, FUSED, KV>(p);
+}
+
 bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size) {
     return (dtype == kF16 || dtype == kFP8) && head_dim == 128 && group >= 1 && group <= 32 &&
            (kPrefillRows % group) == 0 && block_size > 0 && (block_size & (block_size - 1)) == 0;
 }
 
-hipError_t launch_prefill_mfma(const AttnParams &p_in, int32_t dtype, hipStream_t stream) {
+hipError_t launch_prefill_mfma(const AttnParams &p_in, int32_t dtype, hipStream_t stream, const KernelTable *kt) {
     AttnParams p = p_in;
     p.epoch = next_launch_epoch();
     if (p.pf_work == nullptr || p.pf_range == nullptr || p.pf_groups <= 0) return hipErrorInvalidValue;
     const int G = p.num_heads / p.num_kv_heads;
     if (!prefill_mfma_supported(dtype, p.head_dim, G, p.block_size)) return hipErrorInvalidValue;
     const dim3 grid(p.pf_groups), block(64 * kPrefillWaves);
+    if (dtype == kFP8 && (p.fuse_k != nullptr || p.k_scale == nullptr || p.v_scale == nullptr))
+        return hipErrorInvalidValue;
+    if (kt) {  // the code object's entry of this configuration, when it has one
+        const hipFunction_t f = kt->prefill[dtype == kFP8 ? 2 : (p.fuse_k != nullptr ? 1 : 0)];
+        if (f) return module_launch(f, grid, block, p, stream);
+    }
     if (dtype == kFP8) {
-        if (p.fuse_k != nullptr || p.k_scale == nullptr || p.v_scale == nullptr) return hipErrorInvalidValue;
         hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, false, uint8_t>), grid, block, 0, stream, p);
     } else if (p.fuse_k != nullptr) {
         hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, true, f16>), grid, block, 0, stream, p);

@@ -5,6 +5,9 @@
 // runs under the context mutex; cache state under the cache mutex (context
 // first, then cache).  Failures set the context's last error and return -1
 // (PagedAttentionCABI.swift:18-37); success clears it.
+#include <dlfcn.h>
+
+#include <mutex>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -304,6 +307,41 @@ PAM_API int32_t pam_engine_prefill_layers(void *context, const pam_prefill_layer
 PAM_API int32_t pam_engine_append_layers(void *context, const pam_append_layers_request *request) {
     if (!request) return -1;
     return guarded(context, [&](Context *ctx) { ctx->append_layers(*request); });
+}
+
+PAM_API int32_t pam_module_load(void *context, const char *path) {
+    return guarded(context, [&](Context *ctx) { ctx->module_load(path); });
+}
+
+PAM_API int32_t pam_module_unload(void *context) {
+    return guarded(context, [&](Context *ctx) { ctx->module_unload(); });
+}
+
+PAM_API int32_t pam_module_function(void *context, const char *name, void **function) {
+    if (!function) return -1;
+    return guarded(context, [&](Context *ctx) { *function = ctx->module_function(name); });
+}
+
+PAM_API int32_t pam_module_launch(void *context, void *function, uint32_t grid_x, uint32_t grid_y, uint32_t grid_z,
+                                  uint32_t block_x, uint32_t block_y, uint32_t block_z, uint32_t shared_bytes,
+                                  void *args, size_t args_bytes) {
+    const uint32_t g[3] = {grid_x, grid_y, grid_z}, b[3] = {block_x, block_y, block_z};
+    return guarded(context, [&](Context *ctx) { ctx->module_launch_raw(function, g, b, shared_bytes, args, args_bytes); });
+}
+
+PAM_API const char *pam_module_default_path(void) {
+    // libpam_kernels.hsaco beside this library
+    static std::string path;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        Dl_info info{};
+        if (dladdr((void *)&pam_module_default_path, &info) && info.dli_fname) {
+            path = info.dli_fname;
+            const size_t slash = path.rfind('/');
+            path = (slash == std::string::npos ? std::string() : path.substr(0, slash + 1)) + "libpam_kernels.hsaco";
+        }
+    });
+    return path.c_str();
 }
 
 PAM_API int32_t pam_engine_setup_noalloc(void *context) {

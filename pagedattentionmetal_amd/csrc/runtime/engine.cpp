@@ -59,6 +59,7 @@ Context::Context() {}
 Context::~Context() {
     if (!device_ready_) return;
     (void)hipSetDevice(device_);
+    module_unload();
     if (own_stream_) (void)hipStreamSynchronize(own_stream_);
     if (workspace_.ptr) (void)hipFree(workspace_.ptr);
     if (seg_count_.ptr) (void)hipFree(seg_count_.ptr);
@@ -414,6 +415,82 @@ static int32_t heads_per_wave(int32_t group) {
     return 1;
 }
 
+// ------------------------------------------------------------------ code object
+
+// The reference's pipeline manager (PagedAttentionEngine.swift:151-198, 248-333)
+// compiles its shader library at start-up and looks kernels up by name; here a
+// gfx950 code object is loaded with hipModuleLoad and its named entries are
+// bound for this context's launches.
+void Context::module_load(const char *path) {
+    ensure_device();
+    if (!path || !*path) throw invalid_configuration("code object path is empty.");
+    module_unload();
+    hipModule_t m = nullptr;
+    const hipError_t e = hipModuleLoad(&m, path);
+    if (e != hipSuccess)
+        throw PamError(std::string("GPU device or stream could not be initialized: hipModuleLoad(") + path +
+                       "): " + hipGetErrorString(e));
+    KernelTable t{};
+    auto get = [&](const char *name) {
+        hipFunction_t f = nullptr;
+        return hipModuleGetFunction(&f, m, name) == hipSuccess ? f : nullptr;
+    };
+    t.streamk[0][0] = get("pam_decode_streamk_f16_d128");
+    t.streamk[1][0] = get("pam_decode_streamk_e4m3_d128");
+    t.streamk[0][1] = get("pam_decode_layers_streamk_f16_d128");
+    t.streamk[1][1] = get("pam_decode_layers_streamk_e4m3_d128");
+    t.prefill[0] = get("pam_prefill_f16_d128");
+    t.prefill[1] = get("pam_prefill_fused_f16_d128");
+    t.prefill[2] = get("pam_prefill_e4m3_d128");
+    // a stream-K launch is planned for the library kernel's resident grid: an
+    // entry with another occupancy would not fit the plan's partial slots
+    for (int dt = 0; dt < 2; dt++)
+        for (int fl = 0; fl < 2; fl++) {
+            if (!t.streamk[dt][fl]) continue;
+            int lib = 0, mod = 0;
+            hip_check(streamk_occupancy(dt == 0 ? kF16 : kFP8, fl != 0, &lib), "stream-K occupancy");
+            hip_check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&mod, t.streamk[dt][fl], 256, 0),
+                      "code object occupancy");
+            if (mod != lib) {
+                (void)hipModuleUnload(m);
+                throw PamError("Unsupported paged attention path: the code object's stream-K entry runs " +
+                               std::to_string(mod) + " workgroups per CU, the library's kernel " +
+                               std::to_string(lib) + ".");
+            }
+        }
+    module_ = m;
+    ktab_ = t;
+}
+
+void Context::module_unload() {
+    if (!module_) return;
+    if (device_ready_) (void)hipStreamSynchronize(stream());
+    (void)hipModuleUnload(module_);
+    module_ = nullptr;
+    ktab_ = KernelTable{};
+}
+
+void *Context::module_function(const char *name) {
+    if (!module_) throw invalid_configuration("no code object is loaded.");
+    hipFunction_t f = nullptr;
+    if (!name || hipModuleGetFunction(&f, module_, name) != hipSuccess)
+        throw invalid_configuration(std::string("the code object has no entry '") + (name ? name : "") + "'.");
+    return (void *)f;
+}
+
+void Context::module_launch_raw(void *function, const uint32_t grid[3], const uint32_t block[3], uint32_t shared_bytes,
+                                void *args, size_t args_bytes) {
+    if (!module_ || !function) throw invalid_configuration("no code object entry to launch.");
+    ensure_device();
+    void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &args_bytes,
+                      HIP_LAUNCH_PARAM_END};
+    check_launch([&] {
+        return hipModuleLaunchKernel((hipFunction_t)function, grid[0], grid[1], grid[2], block[0], block[1], block[2],
+                                     shared_bytes, stream(), nullptr, args_bytes ? config : nullptr);
+    }, "module launch");
+    finish("module launch");
+}
+
 // ------------------------------------------------------------------ decode
 
 void Context::setup_noalloc() {
@@ -545,7 +622,7 @@ void Context::decode_gpu(const pam_decode_request &r, char *fixed) {
     const pam_layer_spec &l = r.layer;
     with_retry("decodeFlat", [&] {
         mark(ev0_);
-        check_launch([&] { return launch_attention(d.p, l.data_type, d.use_mfma, stream(), gpu_timing ? evmid_ : nullptr); }, "decode");
+        check_launch([&] { return launch_attention(d.p, l.data_type, d.use_mfma, stream(), gpu_timing ? evmid_ : nullptr, ktab()); }, "decode");
         mark(ev1_);
         finish("decode");
     });
@@ -631,7 +708,7 @@ void Context::decode_layers_gpu(const std::vector<pam_decode_request> &reqs) {
             const DecodePlan d = plan_decode(reqs[g.first], nullptr, g.second, qs.data(), outs.data());
             tmp = std::max(tmp, d.tmp);
             split = split || d.p.max_parts > 1 || d.p.seg_count != nullptr;
-            check_launch([&] { return launch_attention(d.p, reqs[g.first].layer.data_type, d.use_mfma, stream()); },
+            check_launch([&] { return launch_attention(d.p, reqs[g.first].layer.data_type, d.use_mfma, stream(), nullptr, ktab()); },
                          "decodeLayers");
         }
         mark(ev1_);
@@ -892,9 +969,9 @@ Context::PrefillPlan Context::plan_prefill(const pam_prefill_request &r) {
 void Context::launch_prefill_plan(const PrefillPlan &pl, int32_t dtype, bool mark_mid) {
     hipEvent_t mid = gpu_timing && mark_mid ? evmid_ : nullptr;
     if (pl.dense)
-        check_launch([&] { return launch_prefill_mfma(pl.p, dtype, stream()); }, "prefill");
+        check_launch([&] { return launch_prefill_mfma(pl.p, dtype, stream(), ktab()); }, "prefill");
     else
-        check_launch([&] { return launch_attention(pl.p, dtype, pl.use_mfma, stream(), mid); }, "prefill");
+        check_launch([&] { return launch_attention(pl.p, dtype, pl.use_mfma, stream(), mid, ktab()); }, "prefill");
 }
 
 void Context::prefill_gpu(const pam_prefill_request &r) {
@@ -1263,9 +1340,9 @@ void Context::mixed_step(const pam_mixed_request &r) {
     with_retry("mixedStep", [&] {
         mark(ev0_);
         if (ab.keys) check_launch([&] { return launch_append_batch(ab, l.data_type, stream()); }, "mixed append");
-        if (!chunks.empty()) check_launch([&] { return launch_prefill_mfma(p, l.data_type, stream()); }, "mixed prefill");
+        if (!chunks.empty()) check_launch([&] { return launch_prefill_mfma(p, l.data_type, stream(), ktab()); }, "mixed prefill");
         if (ragged_rows > 0)
-            check_launch([&] { return launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr); }, "mixed attention");
+            check_launch([&] { return launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr, ktab()); }, "mixed attention");
         else
             mark(evmid_);
         mark(ev1_);

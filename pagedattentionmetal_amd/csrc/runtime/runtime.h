@@ -147,6 +147,15 @@ class Context {
     // arrivals of an abandoned launch (a consumed epoch).
     void dirty_counters(int32_t arrivals);
 
+    // --- code object (libpam_kernels.hsaco): named entries loaded with
+    // hipModuleLoad and used for this context's launches while loaded
+    void module_load(const char *path);
+    void module_unload();
+    void *module_function(const char *name);
+    void module_launch_raw(void *function, const uint32_t grid[3], const uint32_t block[3], uint32_t shared_bytes,
+                           void *args, size_t args_bytes);
+    const KernelTable *ktab() const { return module_ ? &ktab_ : nullptr; }
+
     // --- scratch
     void reserve_workspace(size_t bytes);
     // stage host bytes into a context-owned device region (slot selects one of
@@ -211,6 +220,8 @@ class Context {
     bool seg_used_[kStageSegs] = {};
     int cur_seg_ = 0;
     void *zero_page_ = nullptr;
+    hipModule_t module_ = nullptr;
+    KernelTable ktab_{};
     bool stats_pending_ = false;
     bool stats_has_mid_ = false;
     DeviceBuffer workspace_;

@@ -455,3 +455,21 @@ def test_layers_calls_validate_before_any_launch(pam, ctx):
     with pytest.raises(api.PagedAttentionError, match="divisible"):
         eng.decode_layers([0x1000], 0x1000, 0x1000, 0x1000, 0x1000, [0x1000], 1, 1, [bad])
     eng.close()
+
+
+def test_code_object_is_built_beside_the_library(pam, ctx):
+    """libpam_kernels.hsaco is a gfx950 ELF code object beside libpam.so with the
+    named entries; loading it needs a GPU and fails cleanly without one."""
+    path = pam.pam_module_default_path().decode()
+    assert path.endswith("libpam_kernels.hsaco") and os.path.exists(path)
+    with open(path, "rb") as f:
+        head = f.read(4)
+        data = head + f.read()
+    assert head == b"\x7fELF"
+    for name in (b"pam_decode_streamk_f16_d128", b"pam_decode_streamk_e4m3_d128", b"pam_decode_layers_streamk_f16_d128",
+                 b"pam_prefill_f16_d128", b"pam_prefill_fused_f16_d128", b"pam_prefill_e4m3_d128", b"pam_fill_u32"):
+        assert name in data, name
+    import torch
+    if not torch.cuda.is_available():
+        assert pam.pam_module_load(ctx, path.encode()) == -1
+        assert pam.pam_last_error(ctx)
