@@ -17,9 +17,14 @@
 
 namespace pam {
 
+// Every HIP failure reaches the caller as this exception; the thread's last
+// error is cleared so that an unrelated later hipGetLastError does not report it
+// again (a device fault stays sticky in the runtime regardless).
 void hip_check(hipError_t e, const char *what) {
-    if (e != hipSuccess)
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
         throw ExecutionError(std::string("GPU command execution failed: ") + what + ": " + hipGetErrorString(e));
+    }
 }
 
 // ------------------------------------------------------------------ helpers
@@ -427,13 +432,19 @@ void Context::module_load(const char *path) {
     module_unload();
     hipModule_t m = nullptr;
     const hipError_t e = hipModuleLoad(&m, path);
-    if (e != hipSuccess)
+    if (e != hipSuccess) {
+        (void)hipGetLastError();  // the failure is reported here, not to the caller's next launch check
         throw PamError(std::string("GPU device or stream could not be initialized: hipModuleLoad(") + path +
                        "): " + hipGetErrorString(e));
+    }
     KernelTable t{};
     auto get = [&](const char *name) {
         hipFunction_t f = nullptr;
-        return hipModuleGetFunction(&f, m, name) == hipSuccess ? f : nullptr;
+        if (hipModuleGetFunction(&f, m, name) == hipSuccess) return f;
+        // an absent entry leaves hipErrorNotFound as the thread's last error,
+        // which a later hipGetLastError (torch's launch check) would report
+        (void)hipGetLastError();
+        return (hipFunction_t) nullptr;
     };
     t.streamk[0][0] = get("pam_decode_streamk_f16_d128");
     t.streamk[1][0] = get("pam_decode_streamk_e4m3_d128");
@@ -473,8 +484,10 @@ void Context::module_unload() {
 void *Context::module_function(const char *name) {
     if (!module_) throw invalid_configuration("no code object is loaded.");
     hipFunction_t f = nullptr;
-    if (!name || hipModuleGetFunction(&f, module_, name) != hipSuccess)
+    if (!name || hipModuleGetFunction(&f, module_, name) != hipSuccess) {
+        (void)hipGetLastError();  // reported by this exception, not by the caller's next launch check
         throw invalid_configuration(std::string("the code object has no entry '") + (name ? name : "") + "'.");
+    }
     return (void *)f;
 }
 

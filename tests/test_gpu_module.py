@@ -82,4 +82,7 @@ def test_module_launch_named_entry_with_packed_arguments():
     from pagedattentionmetal_amd.api import PagedAttentionError
     with pytest.raises(PagedAttentionError, match="no entry"):
         e.module_function("pam_no_such_kernel")
+    # the failed lookup is not left behind for torch's next launch check
+    torch.zeros(4, device="cuda").add_(1)
+    torch.cuda.synchronize()
     e.close()
