@@ -174,6 +174,12 @@ class PagedAttentionEngine:
     def set_decode_kernel(self, choice: int):
         self._check(lib().pam_set_decode_kernel(self._ctx, int(choice)))
 
+    def set_mixed_launch(self, mode: int, prefill_groups: int = 0, decode_groups: int = 0):
+        """mixed_step's attention: 0 automatic, 1 separate prefill and decode
+        launches, 2 one launch holding both; the one launch's workgroups per part
+        (0 = automatic)."""
+        self._check(lib().pam_set_mixed_launch(self._ctx, int(mode), int(prefill_groups), int(decode_groups)))
+
     def set_gpu_timing(self, enabled: bool):
         """HIP-event timing of every call (last_stats times); off: no events, times -1."""
         self._check(lib().pam_set_gpu_timing(self._ctx, bool(enabled)))

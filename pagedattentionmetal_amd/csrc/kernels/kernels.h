@@ -214,7 +214,8 @@ hipError_t launch_prefill_mfma(const AttnParams &p, int32_t dtype, hipStream_t s
 // over its key tiles; items are cut into segments so that the `groups`
 // workgroups get about the same number of tiles.  Fills p.pf_groups; the caller
 // stages `work` and `range` to the device and provides `slots` partial slots of
-// kPrefillSlotBytes and as many zeroed counters.
+// kPrefillSlotBytes and as many 64-bit merge counters (epoch-tagged: any
+// starting value).
 struct PrefillSplit {
     std::vector<int4> work;
     std::vector<int2> range;
@@ -225,5 +226,14 @@ constexpr int64_t kPrefillSlotBytes = 8 * 64 * (64 + 2) * 4;  // one workgroup's
 void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t groups, PrefillSplit &out,
                         bool allow_split = true);
 bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size);
+
+// One launch for a mixed step (mixed.hip): the dense prefill's work list (p.pf_*,
+// p.pf_groups workgroups first) and the stream-K decode of p.rows single-token
+// rows on `decode_groups` workgroups of 8 waves after them.
+constexpr int kMixedMaxRows = 1024;  // decode rows one mixed launch takes
+bool mixed_launch_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size, int32_t rows);
+// partial slots (d + 2 floats each) and merge counters of the decode part
+void mixed_decode_slots(const AttnParams &p, int32_t decode_groups, int64_t *part_slots, int64_t *counters);
+hipError_t launch_mixed_step(const AttnParams &p, int32_t dtype, int32_t decode_groups, hipStream_t stream);
 
 }  // namespace pam

@@ -8,15 +8,15 @@
 // configuration, with the same launch bounds, so a context bound to the module
 // gives the same results bit for bit.  Built by build.py with hipcc --genco; it
 // is not part of libpam.so.
-#include "../kernels/attention.hip"
-#include "../kernels/prefill.hip"
+#include "../kernels/attention_body.h"
+#include "../kernels/prefill_body.h"
 
 namespace pam {
 
 #define PAM_STREAMK_ENTRY(NAME, KV, HD, BLK, FL)                                                      \
     extern "C" __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void NAME( \
         AttnParams p) {                                                                                \
-        streamk_body<KV, HD, BLK, FL>(p);                                                              \
+        streamk_body<KV, HD, BLK, FL>(p, blockIdx.x, gridDim.x);                                     \
     }
 #define PAM_PREFILL_ENTRY(NAME, FUSED, KV)                                                   \
     extern "C" __global__ __launch_bounds__(64 * kPrefillWaves, 1) void NAME(AttnParams p) { \

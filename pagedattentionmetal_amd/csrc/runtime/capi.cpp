@@ -652,6 +652,16 @@ PAM_API int32_t pam_set_partition_tokens(void *context, int32_t tokens) {
     });
 }
 
+PAM_API int32_t pam_set_mixed_launch(void *context, int32_t mode, int32_t prefill_groups, int32_t decode_groups) {
+    return guarded(context, [&](Context *ctx) {
+        if (mode < 0 || mode > 2) throw invalid_configuration("mixed launch mode must be 0, 1 or 2");
+        if (prefill_groups < 0 || decode_groups < 0) throw invalid_configuration("workgroup counts must be >= 0");
+        ctx->mixed_launch_mode = mode;
+        ctx->mixed_prefill_groups = prefill_groups;
+        ctx->mixed_decode_groups = decode_groups;
+    });
+}
+
 PAM_API int32_t pam_set_decode_kernel(void *context, int32_t choice) {
     return guarded(context, [&](Context *ctx) {
         if (choice < 0 || choice > 2) throw invalid_configuration("decode kernel choice must be 0, 1 or 2");

@@ -375,14 +375,15 @@ void Context::dirty_counters(int32_t arrivals) {
     }
 }
 
-Context::DensePlan Context::plan_dense_prefill(AttnParams &p, const int4 *chunks, int32_t n, StageList &sl) {
+Context::DensePlan Context::plan_dense_prefill(AttnParams &p, const int4 *chunks, int32_t n, StageList &sl,
+                                              int32_t groups) {
     // splitThreshold (PagedAttentionEngine.swift:116-117, :1952-1958): only
     // prefills past it may use the multi-pass form, here items cut into pieces
     // whose partial states are merged in the kernel
     int64_t longest = 0;
     for (int32_t c = 0; c < n; c++) longest = std::max<int64_t>(longest, (int64_t)chunks[c].y + chunks[c].z);
     PrefillSplit ps;
-    prefill_split_plan(chunks, n, p, cus_, ps, longest > split_threshold);
+    prefill_split_plan(chunks, n, p, groups > 0 ? groups : cus_, ps, longest > split_threshold);
     DensePlan d;
     d.o_work = sl.add(ps.work.data(), ps.work.size() * sizeof(int4));
     d.o_range = sl.add(ps.range.data(), ps.range.size() * sizeof(int2));
@@ -1291,8 +1292,17 @@ void Context::mixed_step(const pam_mixed_request &r) {
     pf.num_kv_heads = l.num_kv_heads;
     pf.window = W;
     pf.causal = 1;
+    // One launch for the chunks and the decode rows (mixed.hip): the prefill's
+    // workgroups first, the decode's after them.  Automatic: the prefill is
+    // planned for every CU and the decode's resident grid follows it.
+    const bool one_launch = mixed_launch_mode != 1 && !chunks.empty() && ragged_rows > 0 && use_mfma &&
+                            part_tokens_override == 0 &&
+                            mixed_launch_supported(l.data_type, l.head_dim, G, bs, ragged_rows);
+    const int32_t mix_pf_groups = mixed_prefill_groups > 0 ? mixed_prefill_groups : cus_;
+    const int32_t mix_dec_groups = mixed_decode_groups > 0 ? mixed_decode_groups : cus_;
     DensePlan dense_plan;
-    if (!chunks.empty()) dense_plan = plan_dense_prefill(pf, chunks.data(), (int32_t)chunks.size(), sl);
+    if (!chunks.empty())
+        dense_plan = plan_dense_prefill(pf, chunks.data(), (int32_t)chunks.size(), sl, one_launch ? mix_pf_groups : 0);
     const char *sbase = static_cast<const char *>(stage(0, sl.blob.data(), sl.blob.size()));
     const int4 *d_rows = ragged_rows ? reinterpret_cast<const int4 *>(sbase + o_rows) : nullptr;
     if (appending) {
@@ -1349,10 +1359,34 @@ void Context::mixed_step(const pam_mixed_request &r) {
     p.scale_log2 = kLog2eHost / std::sqrt((float)l.head_dim);
     p.zero_page = zero_page_;
     const int64_t waves = (int64_t)ragged_rows * (use_mfma ? l.num_kv_heads : l.num_heads / nh);
-    const int64_t tmp = ragged_rows > 0 ? plan_split(p, l.data_type, use_mfma, max_tiles + 1, waves) : 0;
+    int64_t tmp = 0;
+    if (one_launch) {
+        int64_t slots = 0, counters = 0;
+        mixed_decode_slots(p, mix_dec_groups, &slots, &counters);
+        const int64_t bytes = slots * ((int64_t)l.head_dim + 2) * 4;
+        if (bytes >= ((int64_t)1 << 31)) throw PamError("stream-K workspace exceeds 2 GiB");
+        reserve_workspace((size_t)bytes);
+        reserve_counters(seg_count_, (size_t)counters * 8);
+        p.part_o = static_cast<float *>(workspace_.ptr);
+        p.part_ml = p.part_o + slots * l.head_dim;
+        p.part_bytes = (uint32_t)bytes;
+        p.seg_count = static_cast<uint64_t *>(seg_count_.ptr);
+        p.part_tokens = (int32_t)((max_tiles + 1) * 16);
+        p.max_parts = 1;
+        tmp = bytes;
+    } else if (ragged_rows > 0) {
+        tmp = plan_split(p, l.data_type, use_mfma, max_tiles + 1, waves);
+    }
     with_retry("mixedStep", [&] {
         mark(ev0_);
         if (ab.keys) check_launch([&] { return launch_append_batch(ab, l.data_type, stream()); }, "mixed append");
+        if (one_launch) {
+            check_launch([&] { return launch_mixed_step(p, l.data_type, mix_dec_groups, stream()); }, "mixed attention");
+            mark(evmid_);
+            mark(ev1_);
+            finish("mixed step");
+            return;
+        }
         if (!chunks.empty()) check_launch([&] { return launch_prefill_mfma(p, l.data_type, stream(), ktab()); }, "mixed prefill");
         if (ragged_rows > 0)
             check_launch([&] { return launch_attention(p, l.data_type, use_mfma, stream(), gpu_timing ? evmid_ : nullptr, ktab()); }, "mixed attention");

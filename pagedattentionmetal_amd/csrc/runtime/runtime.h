@@ -136,6 +136,8 @@ class Context {
     int32_t fail_next_launches = 0;
     int32_t part_tokens_override = 0;
     int32_t decode_kernel_choice = 0;
+    // mixed step: 0 automatic, 1 separate launches, 2 one launch; its groups (0: automatic)
+    int32_t mixed_launch_mode = 0, mixed_prefill_groups = 0, mixed_decode_groups = 0;
     // HIP events around each call's kernels (the timings of last_stats); off
     // saves their queue packets between back-to-back launches
     bool gpu_timing = true;
@@ -203,7 +205,7 @@ class Context {
         size_t o_work = 0, o_range = 0;
         int64_t tmp = 0;
     };
-    DensePlan plan_dense_prefill(AttnParams &p, const int4 *chunks, int32_t n, StageList &sl);
+    DensePlan plan_dense_prefill(AttnParams &p, const int4 *chunks, int32_t n, StageList &sl, int32_t groups = 0);
     static void bind_dense_prefill(AttnParams &p, const DensePlan &d, const char *base);
     void record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t blocks, int64_t tmp, bool split,
                       bool has_mid);

@@ -519,3 +519,70 @@ def test_mixed_step_random_ragged_chunks(engine, seed, H, hkv, bs, window):
         err = row_rel_err(got[r0:r0 + T][fin], ref[fin]) if fin.any() else 0.0
         assert err <= TOL[1], f"sequence {s} (context {ctx[s]}, {T} new): rel err {err:.3e}"
         r0 += T
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed,dtype,groups", [(1, 1, (0, 0)), (2, 1, (200, 40)), (3, 2, (0, 0)), (4, 1, (64, 384))])
+def test_mixed_step_one_launch(engine, seed, dtype, groups):
+    """pam_set_mixed_launch(2): the prefill chunks and the decode rows of a step in
+    one launch (prefill workgroups first, stream-K decode after them), for several
+    workgroup splits.  Every decode row against the oracle; every row against the
+    separate launches (the same arithmetic cut at other split points)."""
+    import torch
+    rng = np.random.default_rng(1300 + seed)
+    H, hkv, d, bs = 32, 8, 128, 16
+    nch, ndec = 6, 40
+    ctx = np.concatenate([rng.integers(0, 2001, nch), rng.integers(1, 3000, ndec)]).astype(np.int32)
+    ql = np.concatenate([rng.integers(2, 513, nch), np.ones(ndec)]).astype(np.int32)
+    order = rng.permutation(nch + ndec)
+    ctx, ql = ctx[order], ql[order]
+    nblk = (ctx + ql + bs - 1) // bs
+    nb = int(nblk.sum()) + 3
+    perm = rng.permutation(nb).astype(np.int32)
+    bt = np.zeros((len(ctx), int(nblk.max())), np.int32)
+    c = 0
+    for s, n in enumerate(nblk):
+        bt[s, :n] = perm[c:c + n]
+        c += n
+    rows = int(ql.sum())
+    q = rng.standard_normal((rows, H, d)).astype(np.float16)
+    if dtype == 2:
+        # e4m3 pools with per-block scales, written by one append of every token
+        ksd = torch.zeros(nb, dtype=torch.float16, device="cuda")
+        vsd = torch.zeros_like(ksd)
+        kd = torch.zeros((nb, bs, hkv, d), dtype=torch.uint8, device="cuda")
+        vd = torch.zeros_like(kd)
+        for s in range(len(ctx)):
+            L = int(ctx[s] + ql[s])
+            keys = rng.standard_normal((L, hkv, d)).astype(np.float16)
+            vals = rng.standard_normal((L, hkv, d)).astype(np.float16)
+            engine.append_to_cache(to_dev(keys), to_dev(vals), kd, vd, to_dev(bt[s]), 0, L,
+                                   layer(hkv, hkv, d, bs, 2), k_scale=ksd, v_scale=vsd)
+        kp, vp = to_host(kd), to_host(vd)
+        ks, vs = to_host(ksd).view(np.uint16), to_host(vsd).view(np.uint16)
+    else:
+        kp = rng.standard_normal((nb, bs, hkv, d)).astype(np.float16)
+        vp = rng.standard_normal((nb, bs, hkv, d)).astype(np.float16)
+        kd, vd, ksd, vsd, ks, vs = to_dev(kp), to_dev(vp), None, None, None, None
+    spec = layer(H, hkv, d, bs, dtype)
+    outs = []
+    for mode, pf, dec in [(1, 0, 0), (2, groups[0], groups[1]), (2, groups[0], groups[1])]:
+        engine.set_mixed_launch(mode, pf, dec)
+        out = torch.zeros((rows, H, d), dtype=torch.float16, device="cuda")
+        engine.mixed_step(to_dev(q), out, kd, vd, to_dev(bt), ctx, ql, spec, k_scale=ksd, v_scale=vsd)
+        outs.append(to_host(out).astype(np.float64))
+    engine.set_mixed_launch(0)
+    sep, one, again = outs
+    assert np.array_equal(np.isnan(one), np.isnan(sep))
+    assert np.array_equal(one, again, equal_nan=True), "one launch not repeatable"
+    fin = ~np.isnan(sep).any(axis=-1)
+    assert row_rel_err(one[fin], sep[fin]) <= TOL[1]
+    r0 = 0
+    for s in range(len(ctx)):
+        T = int(ql[s])
+        if T == 1:
+            ref = oracle.prefill(dtype, q[r0:r0 + 1], kp, vp, bt[s], int(ctx[s]), causal=True,
+                                 k_scale=ks, v_scale=vs)
+            err = row_rel_err(one[r0:r0 + 1], ref)
+            assert err <= TOL[dtype], f"decode row of sequence {s} (context {ctx[s]}): rel err {err:.3e}"
+        r0 += T

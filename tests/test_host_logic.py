@@ -78,6 +78,12 @@ def test_error_convention(pam, ctx):
     assert not pam.pam_create_cache_host(ctx, 0, 16, 32, 1, 0)
     assert b"maxBlocks" in pam.pam_last_error(ctx)
     pam.pam_destroy_cache(c)
+    # tuning setters check their arguments on the host
+    assert pam.pam_set_mixed_launch(ctx, 3, 0, 0) == -1
+    assert b"mixed launch mode" in pam.pam_last_error(ctx)
+    assert pam.pam_set_mixed_launch(ctx, 2, -1, 0) == -1
+    assert pam.pam_set_mixed_launch(ctx, 2, 200, 56) == 0
+    assert pam.pam_set_mixed_launch(ctx, 0, 0, 0) == 0
 
 
 def test_no_gpu_paths_fail_cleanly(pam, ctx):
