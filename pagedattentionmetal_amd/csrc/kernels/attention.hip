@@ -212,7 +212,7 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnParams p, int lanes_p
             float v[4] = {acc[hh][0] * inv, acc[hh][1] * inv, acc[hh][2] * inv, acc[hh][3] * inv};
             store4<QT>(out + (c.out_row * H + h0 + hh) * (int64_t)HD + d0, v);
         }
-    } else {
+    } else if (p.seg_count == nullptr) {  // partials for attn_reduce_kernel
 #pragma unroll
         for (int hh = 0; hh < NH; hh++) {
             const int64_t slot = ((int64_t)r * H + h0 + hh) * p.max_parts + part;
@@ -221,6 +221,54 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnParams p, int lanes_p
                 p.part_ml[slot * 2 + 0] = m[hh];
                 p.part_ml[slot * 2 + 1] = l[hh];
             }
+        }
+    } else {
+        // Merged in the kernel (no reduce launch): the partial is published with
+        // write-through stores and counted on the (row, head group) counter; the
+        // wave that completes the count folds all partitions in order, as
+        // attn_reduce_kernel does, and writes the rows.  Offsets are bytes from
+        // part_o (< 2 GiB).
+        const __amdgpu_buffer_rsrc_t prs = part_rsrc(p);
+        const int ml_off = (int)((const char *)p.part_ml - (const char *)p.part_o);
+        auto slot_of = [&](int hh, int pt) { return ((int64_t)r * H + h0 + hh) * p.max_parts + pt; };
+#pragma unroll
+        for (int hh = 0; hh < NH; hh++) {
+            const int64_t slot = slot_of(hh, part);
+            const f32x4 v = {acc[hh][0], acc[hh][1], acc[hh][2], acc[hh][3]};
+            __builtin_amdgcn_raw_buffer_store_b128(v, prs, (int)((slot * HD + d0) * 4), 0, kSc1);
+            if (d0 == 0) {
+                const f32x2 ml = {m[hh], l[hh]};
+                __builtin_amdgcn_raw_buffer_store_b64(ml, prs, ml_off + (int)(slot * 8), 0, kSc1);
+            }
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        uint32_t before = 0;
+        if (lane == 0)  // lane 0 has sub 0 and d0 0: it is active here
+            before = arrive_count(p.seg_count + (int64_t)r * (H / NH) + hg, p.epoch);
+        before = __builtin_amdgcn_readfirstlane(before);
+        if (before != (uint32_t)(pr.nparts - 1)) return;
+        for (int hh = 0; hh < NH; hh++) {
+            float M = -INFINITY;
+            for (int pt = 0; pt < pr.nparts; pt++) {
+                const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)(slot_of(hh, pt) * 8), 0, kSc1);
+                M = fmaxf(M, ml[0]);
+            }
+            float den = 0.0f, a[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int pt = 0; pt < pr.nparts; pt++) {
+                const int64_t slot = slot_of(hh, pt);
+                const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)(slot * 8), 0, kSc1);
+                const f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)((slot * HD + d0) * 4), 0, kSc1);
+                const float w = ml[0] == -INFINITY ? 0.0f : exp2f(ml[0] - M);
+                den += w * ml[1];
+#pragma unroll
+                for (int e = 0; e < 4; e++) a[e] += w * v[e];
+            }
+            const float inv = 1.0f / den;
+#pragma unroll
+            for (int e = 0; e < 4; e++) a[e] *= inv;
+            store4<QT>(out + (c.out_row * H + h0 + hh) * (int64_t)HD + d0, a);
         }
     }
 }
@@ -430,7 +478,8 @@ hipError_t launch_attention(const AttnParams &p_in, int32_t dtype, bool use_mfma
     }
     if (e != hipSuccess) return e;
     if (after_main) (void)hipEventRecord(after_main, stream);
-    if (p.max_parts <= 1 || (use_mfma && p.seg_count != nullptr)) return e;
+    // stream-K (MFMA) and the VALU kernel with counters merge in the kernel
+    if (p.max_parts <= 1 || p.seg_count != nullptr) return e;
     dim3 grid((p.num_heads + 3) / 4, p.rows);
     if (dtype == kF32)
         hipLaunchKernelGGL((attn_reduce_kernel<float>), grid, dim3(256), 0, stream, p);

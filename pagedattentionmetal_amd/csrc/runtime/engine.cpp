@@ -341,14 +341,27 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
     if (p.max_parts <= 1) return 0;
     const int64_t slots_p = (int64_t)p.rows * p.num_heads * p.max_parts;
     const int64_t bytes = slots_p * ((int64_t)p.head_dim + 2) * 4;
+    if (bytes >= ((int64_t)1 << 31)) throw PamError("split-context workspace exceeds 2 GiB");
+    // The VALU kernel merges its partitions itself (one counter per row and
+    // head group; no reduce launch); the MFMA workgroup form leaves them to
+    // attn_reduce_kernel.
+    const int64_t merge_counters = use_mfma ? 0 : (int64_t)p.rows * (p.num_heads / p.heads_per_wave);
     if (fixed) {
         if (bytes > fixed_parts) throw too_big("split-context partials", bytes, fixed_parts);
+        if (merge_counters * 8 > (int64_t)kNoAllocCounterBytes)
+            throw too_big("merge counters", merge_counters * 8, (int64_t)kNoAllocCounterBytes);
         p.part_o = reinterpret_cast<float *>(fixed + kNoAllocZeroBytes + kNoAllocCounterBytes);
+        if (merge_counters) p.seg_count = reinterpret_cast<uint64_t *>(fixed + kNoAllocZeroBytes);
     } else {
         reserve_workspace((size_t)bytes);
         p.part_o = static_cast<float *>(workspace_.ptr);
+        if (merge_counters) {
+            reserve_counters(seg_count_, (size_t)merge_counters * 8);
+            p.seg_count = static_cast<uint64_t *>(seg_count_.ptr);
+        }
     }
     p.part_ml = p.part_o + slots_p * p.head_dim;
+    p.part_bytes = (uint32_t)bytes;
     return bytes;
 }
 
