@@ -129,15 +129,7 @@ def time_decode(torch, eng, w, t, steps, warmup):
 def mixed_setup(torch, api, workloads):
     """Device tensors for the c3 mixed step: cached context in the pool, new tokens to append."""
     w = workloads.mixed_config()
-    g = torch.Generator(device="cuda")
-    g.manual_seed(w.seed)
-    shape = (w.pool_blocks, w.block_size, w.num_kv_heads, w.head_dim)
-    kp = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
-    vp = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
-    rows = w.total_rows
-    q = torch.randn((rows, w.num_heads, w.head_dim), generator=g, device="cuda", dtype=torch.float32).half()
-    nk = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
-    nv = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
+    kp, vp, q, nk, nv = workloads.mixed_pools(w)
     bt = torch.from_numpy(w.block_tables).cuda()
     out = torch.empty_like(q)
     eng = api.PagedAttentionEngine()
@@ -442,7 +434,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic (seeded; K/V ~ N(0, 0.5^2), shuffled pool)",
+        "data": "synthetic (SplitMix64 counter-based generator, seed 0x5EED0002; K/V ~ N(0, 0.5^2), shuffled pool)",
         "config": {"workload": "c2: GQA fp16 ragged paged decode, B=64, L~U[128,4096] (sharers U[513,4096]), "
                                "32 q / 8 kv heads, d=128, bs=16, 32768-block shuffled pool, 32 shared "
                                "prefix blocks in 32 tables",

@@ -491,6 +491,16 @@ int32_t pam_fp8_dequant(void *context, const uint8_t *codes, const uint16_t *sca
 int32_t pam_calib_stream_read(void *context, const void *src, size_t bytes, int32_t blocks, float *ms);
 int32_t pam_calib_stream_copy(void *context, const void *src, void *dst, size_t bytes, int32_t blocks, float *ms);
 
+/* Synthetic data of the measured workloads (no reference counterpart): n
+ * normals N(0, stddev^2) into dst (PAM_FLOAT32 or PAM_FLOAT16), element i from
+ * SplitMix64 outputs (stream << 40) + 2i and + 2i + 1 of the generator seeded
+ * with `seed` (Box-Muller cosine branch in binary64, rounded to binary32, then to
+ * the output type).  outlier_stream >= 0: element i is multiplied by 8 when the
+ * uniform of output (outlier_stream << 40) + i is below outlier_frac.  Streams
+ * < 2^23, n < 2^39.  Enqueued on the context's stream. */
+int32_t pam_synth_normal(void *context, void *dst, int32_t dtype, uint64_t n, uint64_t seed, uint64_t stream,
+                         float stddev, int64_t outlier_stream, float outlier_frac);
+
 /* Test hook: the next n kernel launches of this context report a launch failure
  * (host-side; no GPU work is faulted). */
 int32_t pam_debug_fail_next_launches(void *context, int32_t n);

@@ -425,6 +425,17 @@ class PagedAttentionEngine:
         self._check(lib().pam_calib_stream_read(self._ctx, _ptr(src), _nbytes(src), int(blocks), C.byref(ms)))
         return ms.value
 
+    def synth_normal(self, dst, seed: int, stream: int, stddev: float = 1.0, outlier_stream: int = -1,
+                     outlier_frac: float = 0.0):
+        """Fill a float32 / float16 device tensor with the counter-based normals of
+        (seed, stream) (pam_synth_normal)."""
+        import torch
+        dt = {torch.float32: 0, torch.float16: 1}.get(dst.dtype)
+        if dt is None:
+            raise PagedAttentionError("synthetic data is float32 or float16")
+        self._check(lib().pam_synth_normal(self._ctx, _ptr(dst), dt, dst.numel(), int(seed) & ((1 << 64) - 1),
+                                           int(stream), float(stddev), int(outlier_stream), float(outlier_frac)))
+
     def calib_stream_copy(self, src, dst, blocks=0) -> float:
         ms = C.c_float()
         self._check(lib().pam_calib_stream_copy(self._ctx, _ptr(src), _ptr(dst), _nbytes(src), int(blocks),

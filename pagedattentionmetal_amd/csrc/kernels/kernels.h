@@ -204,6 +204,9 @@ hipError_t launch_stage_copy(const void *host_mapped, void *dst, size_t bytes, h
 // Calibration streams of known size (achievable HBM rates, counter scaling).
 hipError_t launch_stream_read(const void *src, size_t bytes, uint32_t *sink, int blocks, hipStream_t stream);
 hipError_t launch_stream_copy(const void *src, void *dst, size_t bytes, int blocks, hipStream_t stream);
+// Counter-based synthetic normals (synth.hip).
+hipError_t launch_synth_normal(void *dst, int32_t dtype, uint64_t n, uint64_t seed, uint64_t stream, float stddev,
+                               int64_t outlier_stream, float outlier_frac, hipStream_t s);
 
 // Dense chunked-prefill (MFMA, f16): rows [q_offset, q_offset + T) of one sequence.
 // Dense prefill (MFMA): f16 or e4m3 KV, d = 128; Q and O f16.

@@ -697,6 +697,20 @@ static int32_t calib_blocks(int32_t blocks) {
     return 4 * cus;
 }
 
+PAM_API int32_t pam_synth_normal(void *context, void *dst, int32_t dtype, uint64_t n, uint64_t seed, uint64_t stream,
+                                 float stddev, int64_t outlier_stream, float outlier_frac) {
+    return guarded(context, [&](Context *ctx) {
+        if (n > 0 && !dst) throw invalid_configuration("synthetic data needs a destination buffer.");
+        if (dtype != kF32 && dtype != kF16) throw invalid_configuration("synthetic data is float32 or float16.");
+        if (stream >= ((uint64_t)1 << 23) || outlier_stream >= ((int64_t)1 << 23) || n >= ((uint64_t)1 << 39))
+            throw invalid_configuration("synthetic data: stream ids must be < 2^23 and n < 2^39.");
+        ctx->ensure_device();
+        hip_check(launch_synth_normal(dst, dtype, n, seed, stream, stddev, outlier_stream, outlier_frac, ctx->stream()),
+                  "synthetic data");
+        ctx->finish("synthetic data");
+    });
+}
+
 PAM_API int32_t pam_calib_stream_read(void *context, const void *src, size_t bytes, int32_t blocks, float *ms) {
     return guarded(context, [&](Context *ctx) {
         ctx->ensure_device();

@@ -36,6 +36,8 @@ len - W rows attend to no key and come out 0/0 (NaN), as the reference's do.
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 
 from .api import KVCacheManager, ContinuousBatchingScheduler, PagedAttentionEngine, PagedAttentionError, \
@@ -62,7 +64,8 @@ class PagedAttentionInference:
         self.decoded_tokens = 0
         self.prefill_tokens = 0
         self.preemptions = 0
-        self._rng = np.random.default_rng(seed)
+        self._seed = int(seed)
+        self._fills = 0  # synthetic-data streams used so far (workloads.device_normals)
         self._buf_rows = 0
         self._max_new: dict[int, int] = {}
         self.last_launch = None  # (context lengths, query lengths) of the last mixed_step, rows in that order
@@ -184,19 +187,22 @@ class PagedAttentionInference:
             n += for_rows
         return n
 
+    def _normals(self, shape, dtype, std):
+        """Synthetic Q / K / V rows: the counter-based normals of this driver's seed,
+        a fresh stream per buffer (streams from 16 on; the workloads use 0-8)."""
+        from . import workloads
+        self._fills += 1
+        return workloads.device_normals(shape, dtype, self._seed, 15 + self._fills, std)
+
     def _buffers(self, rows):
         import torch
         L = self.layer
         if rows > self._buf_rows:
             n = max(rows, 2 * self._buf_rows, 4096)
-            g = torch.Generator(device="cuda")
-            g.manual_seed(int(self._rng.integers(1 << 31)))
-            self._q = torch.randn((n, L.num_heads, L.head_dim), generator=g, device="cuda", dtype=torch.float16)
+            self._q = self._normals((n, L.num_heads, L.head_dim), torch.float16, 1.0)
             self._out = torch.empty_like(self._q)
-            self._nk = torch.randn((n, L.num_kv_heads, L.head_dim), generator=g, device="cuda",
-                                   dtype=torch.float16).mul_(0.5)
-            self._nv = torch.randn((n, L.num_kv_heads, L.head_dim), generator=g, device="cuda",
-                                   dtype=torch.float16).mul_(0.5)
+            self._nk = self._normals((n, L.num_kv_heads, L.head_dim), torch.float16, 0.5)
+            self._nv = self._normals((n, L.num_kv_heads, L.head_dim), torch.float16, 0.5)
             self._buf_rows = n
         return self._q[:rows], self._out[:rows], self._nk[:rows], self._nv[:rows]
 
@@ -224,15 +230,12 @@ class PagedAttentionInference:
         import torch
         if rows > getattr(self, "_lbuf_rows", 0):
             n = max(rows, 2 * getattr(self, "_lbuf_rows", 0), 1024)
-            g = torch.Generator(device="cuda")
-            g.manual_seed(int(self._rng.integers(1 << 31)))
             dt = torch.float32 if self.layer.data_type == 0 else torch.float16
-            self._lq = [torch.randn((n, l.num_heads, l.head_dim), generator=g, device="cuda", dtype=dt)
-                        for l in self.layers]
+            self._lq = [self._normals((n, l.num_heads, l.head_dim), dt, 1.0) for l in self.layers]
             self._lout = [torch.empty_like(q) for q in self._lq]
             L = self.layer
-            self._lk = torch.randn((n, L.num_kv_heads, L.head_dim), generator=g, device="cuda", dtype=dt).mul_(0.5)
-            self._lv = torch.randn((n, L.num_kv_heads, L.head_dim), generator=g, device="cuda", dtype=dt).mul_(0.5)
+            self._lk = self._normals((n, L.num_kv_heads, L.head_dim), dt, 0.5)
+            self._lv = self._normals((n, L.num_kv_heads, L.head_dim), dt, 0.5)
             self._lbuf_rows = n
         return ([q[:rows] for q in self._lq], [o[:rows] for o in self._lout], self._lk[:rows], self._lv[:rows])
 
@@ -282,13 +285,32 @@ def poisson_trace(inference: PagedAttentionInference, steps: int, rate: float, p
                   seed: int, on_step=None):
     """The BASELINE c5 driver: `steps` scheduler steps with Poisson(`rate`) arrivals
     before each, prompts and output lengths uniform over the given inclusive
-    ranges.  Returns the number of requests admitted."""
-    rng = np.random.default_rng(seed)
+    ranges.  Returns the number of requests admitted.  Draws: SplitMix64 stream 0
+    of `seed` (workloads.uniforms), one uniform per step for its arrival count
+    (Poisson by inversion), then two per arrival for its prompt and output length."""
+    from .workloads import uniforms
     admitted = 0
+    pos = 0
+
+    def draw():
+        nonlocal pos
+        pos += 1
+        return float(uniforms(seed, 0, 1, pos - 1)[0])
+
+    def poisson():
+        u, k = draw(), 0
+        p = math.exp(-rate)
+        F = p
+        while u > F and k < 10_000:
+            k += 1
+            p *= rate / k
+            F += p
+        return k
+
     for i in range(steps):
-        for _ in range(int(rng.poisson(rate))):
-            prompt = int(rng.integers(prompt_range[0], prompt_range[1] + 1))
-            out = int(rng.integers(output_range[0], output_range[1] + 1))
+        for _ in range(poisson()):
+            prompt = prompt_range[0] + int(draw() * (prompt_range[1] - prompt_range[0] + 1))
+            out = output_range[0] + int(draw() * (output_range[1] - output_range[0] + 1))
             if inference.add_request(prompt, out) >= 0:
                 admitted += 1
         inference.step()

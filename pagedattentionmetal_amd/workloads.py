@@ -1,9 +1,14 @@
 """Synthetic workloads for the five configurations the path is measured on.
 
-Metadata (context lengths, block tables, chunk layouts) comes from a seeded
-numpy generator; pool and query contents are drawn on the device with a seeded
-torch generator, so a multi-GiB pool never passes through host memory.  Seed of
-configuration k is ``0x5EED0000 + k``.
+Every draw comes from one counter-based generator, SplitMix64 (output k of the
+generator seeded with S is mix(S + (k + 1) * 0x9E3779B97F4A7C15)), so the data
+does not depend on the numpy, torch or ROCm version.  Seed of configuration k is
+``0x5EED0000 + k``.  Draws are split into streams of 2^40 outputs, one per
+purpose, in the draw order contexts (0) -> block-table permutation (1) -> Q (2)
+-> K (3) -> V (4) -> outliers of K (5) and V (6) -> new keys (7) and values (8).
+Metadata is drawn on the host here; pool and query contents are drawn on the
+device by libpam's ``pam_synth_normal`` (the same generator, one element per
+thread), so a multi-GiB pool never passes through host memory.
 
   c1  B=4 decode, L~U[17,200], MHA 8/8, d=128, bs=16, fp32, 1024-block pool
   c2  B=64 decode, L~U[128,4096], GQA 32/8, fp16, 32768-block shuffled pool,
@@ -60,10 +65,70 @@ class DecodeWorkload:
         return total
 
 
-def _tables(rng, lens, bs, pool_blocks, shared_prefix_blocks=0, sharers=0):
+S_CONTEXTS, S_PERM, S_Q, S_K, S_V, S_K_OUTLIERS, S_V_OUTLIERS, S_NEW_K, S_NEW_V = range(9)
+_GAMMA = np.uint64(0x9E3779B97F4A7C15)
+
+
+def splitmix(seed: int, stream: int, idx) -> np.ndarray:
+    """SplitMix64 outputs at positions (stream << 40) + idx of the generator seeded with `seed`."""
+    k = (np.uint64(stream) << np.uint64(40)) + np.asarray(idx, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed & ((1 << 64) - 1)) + (k + np.uint64(1)) * _GAMMA
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def uniforms(seed: int, stream: int, n: int, start: int = 0) -> np.ndarray:
+    """u in [0, 1) from the top 53 bits of outputs start .. start + n - 1."""
+    z = splitmix(seed, stream, np.arange(start, start + n, dtype=np.uint64))
+    return (z >> np.uint64(11)).astype(np.float64) * 2.0 ** -53
+
+
+def normals(seed: int, stream: int, n: int, start: int = 0) -> np.ndarray:
+    """Standard normals i = start .. start + n - 1 (Box-Muller cosine branch on
+    outputs 2i and 2i + 1, binary64), as pam_synth_normal computes them."""
+    u = uniforms(seed, stream, 2 * n, 2 * start)
+    return np.sqrt(-2.0 * np.log(1.0 - u[0::2])) * np.cos(6.283185307179586 * u[1::2])
+
+
+class _Draws:
+    """Consecutive integer draws from one stream (contexts), in call order."""
+
+    def __init__(self, seed: int, stream: int):
+        self.seed, self.stream, self.pos = seed, stream, 0
+
+    def integers(self, lo: int, hi_excl: int, n: int) -> np.ndarray:
+        u = uniforms(self.seed, self.stream, n, self.pos)
+        self.pos += n
+        return lo + np.floor(u * (hi_excl - lo)).astype(np.int64)
+
+    def normals(self, n: int) -> np.ndarray:
+        # pairs of outputs from the current (even) position
+        self.pos += self.pos & 1
+        v = normals(self.seed, self.stream, n, self.pos // 2)
+        self.pos += 2 * n
+        return v
+
+
+def permutation(seed: int, n: int) -> np.ndarray:
+    """Fisher-Yates over 0..n-1: swap k (k = 0 .. n-2) exchanges i = n-1-k with
+    j = floor(u_k (i + 1)), u_k from stream S_PERM."""
+    perm = np.arange(n, dtype=np.int64)
+    if n < 2:
+        return perm
+    u = uniforms(seed, S_PERM, n - 1)
+    i = np.arange(n - 1, 0, -1)
+    j = np.floor(u * (i + 1)).astype(np.int64)
+    for a, b in zip(i.tolist(), j.tolist()):
+        perm[a], perm[b] = perm[b], perm[a]
+    return perm
+
+
+def _tables(seed, lens, bs, pool_blocks, shared_prefix_blocks=0, sharers=0):
     """Block tables over a shuffled pool; the first `sharers` sequences start with
     the same `shared_prefix_blocks` physical blocks (ref-counted prefix)."""
-    perm = rng.permutation(pool_blocks).astype(np.int32)
+    perm = permutation(seed, pool_blocks).astype(np.int32)
     nblocks = (lens.astype(np.int64) + bs - 1) // bs
     max_nb = int(max(1, nblocks.max()))
     bt = np.zeros((len(lens), max_nb), np.int32)
@@ -85,11 +150,12 @@ def _tables(rng, lens, bs, pool_blocks, shared_prefix_blocks=0, sharers=0):
 
 def config(k: int, batch_scale: float = 1.0) -> DecodeWorkload:
     """Decode workloads c1, c2, c4, c5 (c3 is `mixed_config`)."""
-    rng = np.random.default_rng(SEED_BASE + k)
+    seed = SEED_BASE + k
+    rng = _Draws(seed, S_CONTEXTS)
     if k == 1:
         B = 4
         lens = rng.integers(17, 201, B).astype(np.uint32)
-        bt = _tables(rng, lens, 16, 1024)
+        bt = _tables(seed, lens, 16, 1024)
         return DecodeWorkload("c1", B, 8, 8, 128, 16, 0, 1024, lens, bt, seed=SEED_BASE + k)
     if k == 2:
         B = max(2, int(64 * batch_scale))
@@ -97,21 +163,21 @@ def config(k: int, batch_scale: float = 1.0) -> DecodeWorkload:
         lens = rng.integers(128, 4097, B).astype(np.int64)
         lens[:sharers] = rng.integers(513, 4097, sharers)
         lens = lens.astype(np.uint32)
-        bt = _tables(rng, lens, 16, 32768, shared_prefix_blocks=32, sharers=sharers)
+        bt = _tables(seed, lens, 16, 32768, shared_prefix_blocks=32, sharers=sharers)
         return DecodeWorkload("c2", B, 32, 8, 128, 16, 1, 32768, lens, bt, kv_std=0.5, seed=SEED_BASE + k,
                               shared_prefix_blocks=32, extra={"sharers": sharers})
     if k == 4:
         B = max(2, int(256 * batch_scale))
-        lens = np.clip(np.round(np.exp(rng.normal(np.log(1024.0), 1.0, B))), 16, 8192).astype(np.uint32)
+        lens = np.clip(np.round(np.exp(np.log(1024.0) + rng.normals(B))), 16, 8192).astype(np.uint32)
         need = int(((lens.astype(np.int64) + 15) // 16).sum())
         pool = max(need + 64, 1024)
-        bt = _tables(rng, lens, 16, pool)
+        bt = _tables(seed, lens, 16, pool)
         return DecodeWorkload("c4", B, 32, 8, 128, 16, 2, pool, lens, bt, outlier_frac=0.01, seed=SEED_BASE + k)
     if k == 5:
         B = max(2, int(32 * batch_scale))
         lens = rng.integers(16384, 131073, B).astype(np.uint32)
         need = int(((lens.astype(np.int64) + 15) // 16).sum())
-        bt = _tables(rng, lens, 16, need + 64)
+        bt = _tables(seed, lens, 16, need + 64)
         return DecodeWorkload("c5", B, 64, 8, 128, 16, 1, need + 64, lens, bt, window=4096, seed=SEED_BASE + k)
     raise ValueError(f"no decode workload c{k}")
 
@@ -147,27 +213,55 @@ class MixedWorkload:
 
 
 def mixed_config(n_chunks=8, chunk=512, n_decodes=56) -> MixedWorkload:
-    rng = np.random.default_rng(SEED_BASE + 3)
+    seed = SEED_BASE + 3
+    rng = _Draws(seed, S_CONTEXTS)
     ctx = np.concatenate([rng.integers(0, 3585, n_chunks), rng.integers(256, 4097, n_decodes) - 1]).astype(np.int32)
     ql = np.concatenate([np.full(n_chunks, chunk), np.ones(n_decodes)]).astype(np.int32)
     total = (ctx.astype(np.int64) + ql)
     need = int(((total + 15) // 16).sum())
-    bt = _tables(rng, total.astype(np.uint32), 16, need + 64)
+    bt = _tables(seed, total.astype(np.uint32), 16, need + 64)
     return MixedWorkload("c3", 32, 8, 128, 16, ctx, ql, bt, need + 64, SEED_BASE + 3)
 
 
-def device_pools(w: DecodeWorkload, device="cuda"):
-    """K/V pools (f32/f16) or the f16 source values for an FP8 pool, drawn on the device."""
+_synth = None
+
+
+def device_normals(shape, dtype, seed: int, stream: int, std: float = 1.0, outlier_stream: int = -1,
+                   outlier_frac: float = 0.0, device="cuda"):
+    """A device tensor of the counter-based normals of (seed, stream) in row-major
+    element order, drawn by pam_synth_normal (float32 or float16)."""
     import torch
-    g = torch.Generator(device=device)
-    g.manual_seed(w.seed)
+
+    from . import api
+    global _synth
+    if _synth is None:
+        _synth = api.PagedAttentionEngine()
+    t = torch.empty(shape, dtype=dtype, device=device)
+    _synth.synth_normal(t, seed, stream, std, outlier_stream, outlier_frac)
+    return t
+
+
+def device_pools(w: DecodeWorkload, device="cuda"):
+    """Q and the K/V pools (f32/f16), or the f16 source values of an FP8 pool."""
+    import torch
     shape = (w.pool_blocks, w.block_size, w.num_kv_heads, w.head_dim)
     dt = torch.float32 if w.data_type == 0 else torch.float16
-    k = torch.randn(shape, generator=g, device=device, dtype=torch.float32).mul_(w.kv_std)
-    v = torch.randn(shape, generator=g, device=device, dtype=torch.float32).mul_(w.kv_std)
-    if w.outlier_frac > 0:
-        for t in (k, v):
-            m = torch.rand(shape, generator=g, device=device) < w.outlier_frac
-            t[m] *= 8.0
-    q = torch.randn((w.batch, w.num_heads, w.head_dim), generator=g, device=device, dtype=torch.float32)
-    return q.to(dt), k.to(dt), v.to(dt)
+    ko, vo = (S_K_OUTLIERS, S_V_OUTLIERS) if w.outlier_frac > 0 else (-1, -1)
+    q = device_normals((w.batch, w.num_heads, w.head_dim), dt, w.seed, S_Q, device=device)
+    k = device_normals(shape, dt, w.seed, S_K, w.kv_std, ko, w.outlier_frac, device)
+    v = device_normals(shape, dt, w.seed, S_V, w.kv_std, vo, w.outlier_frac, device)
+    return q, k, v
+
+
+def mixed_pools(w: MixedWorkload, device="cuda"):
+    """f16 K/V pools (N(0, 0.5^2)), Q (N(0, 1)) and the step's new keys and values
+    (N(0, 0.5^2)) of a mixed step."""
+    import torch
+    shape = (w.pool_blocks, w.block_size, w.num_kv_heads, w.head_dim)
+    rows = w.total_rows
+    kp = device_normals(shape, torch.float16, w.seed, S_K, 0.5, device=device)
+    vp = device_normals(shape, torch.float16, w.seed, S_V, 0.5, device=device)
+    q = device_normals((rows, w.num_heads, w.head_dim), torch.float16, w.seed, S_Q, device=device)
+    nk = device_normals((rows, w.num_kv_heads, w.head_dim), torch.float16, w.seed, S_NEW_K, 0.5, device=device)
+    nv = device_normals((rows, w.num_kv_heads, w.head_dim), torch.float16, w.seed, S_NEW_V, 0.5, device=device)
+    return kp, vp, q, nk, nv

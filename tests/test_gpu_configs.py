@@ -91,15 +91,8 @@ def test_decode_config_full_size(torch, k):
 def test_mixed_step_c3_full_size(torch):
     from pagedattentionmetal_amd import api, workloads
     w = workloads.mixed_config()
-    g = torch.Generator(device="cuda")
-    g.manual_seed(w.seed)
-    shape = (w.pool_blocks, w.block_size, w.num_kv_heads, w.head_dim)
-    kp = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
-    vp = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
+    kp, vp, q, nk, nv = workloads.mixed_pools(w)
     rows = w.total_rows
-    q = torch.randn((rows, w.num_heads, w.head_dim), generator=g, device="cuda", dtype=torch.float32).half()
-    nk = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
-    nv = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
     bt = torch.from_numpy(w.block_tables).cuda()
     out = torch.empty_like(q)
     eng = api.PagedAttentionEngine()
@@ -157,15 +150,9 @@ def test_mixed_step_c3_full_size_fp8(torch):
     (compared after dequantisation)."""
     from pagedattentionmetal_amd import api, workloads
     w = workloads.mixed_config()
-    g = torch.Generator(device="cuda")
-    g.manual_seed(w.seed)
-    shape = (w.pool_blocks, w.block_size, w.num_kv_heads, w.head_dim)
-    src_k = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
-    src_v = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).mul_(0.5).half()
+    src_k, src_v, q, nk, nv = workloads.mixed_pools(w)
+    shape = tuple(src_k.shape)
     rows = w.total_rows
-    q = torch.randn((rows, w.num_heads, w.head_dim), generator=g, device="cuda", dtype=torch.float32).half()
-    nk = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
-    nv = torch.randn((rows, w.num_kv_heads, w.head_dim), generator=g, device="cuda").mul_(0.5).half()
     bt = torch.from_numpy(w.block_tables).cuda()
     bs = w.block_size
     kp = torch.zeros(shape, dtype=torch.uint8, device="cuda")
