@@ -184,7 +184,8 @@ struct BackwardParams {
     const int32_t *block_table;
     const float *m, *l;
     void *d_q, *d_k_pool, *d_v_pool;
-    float *row_d;
+    float *row_d;  // [seq_len][num_heads]: D_i = sum_j P_ij dP_ij
+    float *row_c;  // [seq_len][num_heads]: m_i log2(e) + log2(l_i) (MFMA path)
     int32_t seq_len, window_start;
     int32_t num_heads, num_kv_heads, head_dim, block_size;
     float scale;  // 1 / sqrt(head_dim)

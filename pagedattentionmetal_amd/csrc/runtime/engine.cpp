@@ -1122,9 +1122,10 @@ void Context::backward(const pam_backward_request &r) {
     p.head_dim = l.head_dim;
     p.block_size = l.block_size;
     p.scale = 1.0f / std::sqrt((float)l.head_dim);
-    const int64_t tmp = (int64_t)r.seq_len * l.num_heads * 4;
+    const int64_t tmp = (int64_t)r.seq_len * l.num_heads * 4 * 2;
     reserve_workspace((size_t)tmp);
     p.row_d = static_cast<float *>(workspace_.ptr);
+    p.row_c = p.row_d + (int64_t)r.seq_len * l.num_heads;
     with_retry("backward", [&] {
         mark(ev0_);
         check_launch([&] { return launch_backward(p, l.data_type, stream()); }, "backward");

@@ -21,6 +21,11 @@ pytestmark = pytest.mark.gpu
     (1, 64, 16, 4, 128, 16, 0),
     (1, 50, 8, 8, 64, 16, 0),
     (0, 17, 2, 1, 256, 16, 0),     # d = 256, MQA
+    # f16, d = 128: the MFMA kernels (ragged row and key tiles, windows, G = 1..8)
+    (1, 300, 32, 4, 128, 16, 0),
+    (1, 257, 8, 8, 128, 32, 100),
+    (1, 131, 16, 2, 128, 16, 0),
+    (1, 96, 64, 8, 128, 16, 45),
 ])
 def test_backward_parity(dtype, T, H, hkv, d, bs, W):
     import torch
