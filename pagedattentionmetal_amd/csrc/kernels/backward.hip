@@ -176,6 +176,8 @@ __global__ __launch_bounds__(64) void bwd_keys_kernel(BackwardParams p) {
 typedef float bw_f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBwdWaves = 4;             // waves per workgroup, 32 rows / keys each
 constexpr float kBwdPScale = 256.0f;
+constexpr int kBwdRing = 4;                // LDS tiles per operand (kBwdRing - 1 loads in flight)
+constexpr int kBwdBtCache = 8192;          // block-table entries the dQ kernel keeps in LDS
 
 // LDS tile of 32 rows x 128 halves; 16-byte piece p of row r sits at
 // p ^ (4 (r % 4) + (r / 4) % 4): 16 consecutive rows reading one piece
@@ -222,263 +224,361 @@ __device__ __forceinline__ void to_chunks(const bw_f32x16 &v, f16x8 (&out)[2]) {
     for (int r = 0; r < 16; r++) out[r >> 3][r & 7] = (f16)v[r];
 }
 
-__global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams p) {
-    __shared__ __attribute__((aligned(16))) f16 k_lds[2][32 * 128];
-    __shared__ __attribute__((aligned(16))) f16 v_lds[2][32 * 128];
+// 16 bytes per lane from global memory straight into LDS: lane L of the wave
+// writes lds_base + 16 L (global_load_lds_dwordx4, counted by vmcnt).  With 4
+// bytes, lane L writes lds_base + 4 L; inactive lanes write nothing.  Issued
+// as inline assembly so that the compiler, which does not see these LDS writes,
+// adds no wait for them before unrelated LDS reads: the rings below order them
+// with explicit vmcnt waits and barriers (ring_barrier).
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p);
+}
+__device__ __forceinline__ void lds_dma16(const void *g, const void *lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr(lds_base)), "v"(g)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void *g, const void *lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_addr(lds_base)), "v"(g)
+                 : "memory", "m0");
+}
+
+// Workgroup barrier for the LDS rings: this wave's LDS reads and all but its
+// last `N` loads are complete, then every wave arrives.  No fence: a
+// __syncthreads would wait for every load in flight (the ring's prefetch).
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Loads of one 32-row tile (8 KB) of a [row][128] f16 operand into `tile`, two
+// instructions per wave: instruction i of wave w fills rows 4 (2w + i) .. +3,
+// lane L the 16-byte slot L % 16 of row 4 (2w + i) + L / 16, which holds
+// logical piece (L % 16) ^ swz(row) (bw_at's layout).  `row_ptr(r)` gives the
+// global address of tile row r.
+template <typename F>
+__device__ __forceinline__ void tile_dma(f16 *tile, int wave, int lane, F row_ptr) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int blk = 2 * wave + i, R = 4 * blk + (lane >> 4), S = lane & 15;
+        const int piece = S ^ (((R & 3) << 2) | ((R >> 2) & 3));
+        lds_dma16(row_ptr(R) + 8 * piece, tile + 512 * blk);
+    }
+}
+
+template <int NB>
+__global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams p, int group_shift) {
+    __shared__ __attribute__((aligned(16))) f16 k_lds[kBwdRing][32 * 128];
+    __shared__ __attribute__((aligned(16))) f16 v_lds[kBwdRing][32 * 128];
+    __shared__ int32_t bt_lds[kBwdBtCache];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
-    const int H = p.num_heads, G = H / p.num_kv_heads, kvh = blockIdx.y;
-    const int T = p.seq_len, ws = p.window_start;
+    const int H = p.num_heads, G = 1 << group_shift, kvh = blockIdx.y;
+    const int T = p.seq_len, ws = p.window_start, bs = p.block_size;
     const int rows = T * G;
-    const int r = (blockIdx.x * kBwdWaves + wave) * 32 + n;  // this lane's row: token r / G, head r % G
-    const bool row_ok = r < rows;
-    const int tok = row_ok ? r / G : 0, hq = kvh * G + (row_ok ? r % G : 0);
-    const int64_t qo = ((int64_t)tok * H + hq) * 128;
     const f16 *Q = static_cast<const f16 *>(p.q), *dO = static_cast<const f16 *>(p.d_out);
     const f16 *K = static_cast<const f16 *>(p.k_pool), *V = static_cast<const f16 *>(p.v_pool);
-    f16x8 qv[8], gv[8];
+    // the sequence's block-table entries from the window start on
+    const int blk0 = ws / bs, nblk = (T - 1) / bs - blk0 + 1;
+    for (int i = tid; i < nblk; i += 64 * kBwdWaves) bt_lds[i] = p.block_table[blk0 + i];
+    // the wave's NB blocks of 32 rows; lane n's row of block b: token r / G, head r % G
+    bool row_ok[NB];
+    int64_t qo[NB], so[NB];
+    f16x8 qv[NB][8], gv[NB][8];
+    float crow[NB];
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
-        qv[c] = row_ok ? *reinterpret_cast<const f16x8 *>(Q + qo + 16 * c + 8 * h) : (f16x8)(f16)0.0f;
-        gv[c] = row_ok ? *reinterpret_cast<const f16x8 *>(dO + qo + 16 * c + 8 * h) : (f16x8)(f16)0.0f;
+    for (int b = 0; b < NB; b++) {
+        const int r = ((blockIdx.x * kBwdWaves + wave) * NB + b) * 32 + n;
+        row_ok[b] = r < rows;
+        const int tok = row_ok[b] ? r >> group_shift : 0, hq = kvh * G + (row_ok[b] ? r & (G - 1) : 0);
+        so[b] = (int64_t)tok * H + hq;
+        qo[b] = so[b] * 128;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            qv[b][c] = row_ok[b] ? *reinterpret_cast<const f16x8 *>(Q + qo[b] + 16 * c + 8 * h) : (f16x8)(f16)0.0f;
+            gv[b][c] = row_ok[b] ? *reinterpret_cast<const f16x8 *>(dO + qo[b] + 16 * c + 8 * h) : (f16x8)(f16)0.0f;
+        }
+        crow[b] = row_ok[b] ? p.m[so[b]] * kLog2e + __builtin_log2f(p.l[so[b]]) : INFINITY;
     }
-    const float m = row_ok ? p.m[(int64_t)tok * H + hq] : 0.0f, l = row_ok ? p.l[(int64_t)tok * H + hq] : 1.0f;
-    const float crow = row_ok ? m * kLog2e + __builtin_log2f(l) : INFINITY;
     const float sl2 = p.scale * kLog2e;
-
-    // staging: thread -> piece tid % 16 of tile rows tid / 16 and tid / 16 + 16
-    const int sp = tid & 15, sr = tid >> 4;
-    const int t0 = ws / 32, t1 = (T + 31) / 32, NT = t1 - t0;
-    auto fetch = [&](int t, f16x8 (&kr)[2], f16x8 (&vr)[2]) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            int j = t * 32 + sr + 16 * i;
-            j = j < ws ? ws : (j >= T ? T - 1 : j);  // finite rows outside the keys (masked)
-            kr[i] = *reinterpret_cast<const f16x8 *>(pool_row(K, p, j, kvh) + 8 * sp);
-            vr[i] = *reinterpret_cast<const f16x8 *>(pool_row(V, p, j, kvh) + 8 * sp);
-        }
-    };
-    auto stage = [&](int buf, const f16x8 (&kr)[2], const f16x8 (&vr)[2]) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            *reinterpret_cast<f16x8 *>(&k_lds[buf][bw_at(sr + 16 * i, sp)]) = kr[i];
-            *reinterpret_cast<f16x8 *>(&v_lds[buf][bw_at(sr + 16 * i, sp)]) = vr[i];
-        }
+    __syncthreads();  // bt_lds
+    const int t0 = ws / 32, t1 = (T + 31) / 32, NT = t1 - t0, NI = 2 * NT;
+    // iteration it reads key tile t0 + it % NT (both passes) from ring slot it % kBwdRing
+    auto issue = [&](int it) {
+        const int t = t0 + (it < NI ? it : NI - 1) % NT, slot = it % kBwdRing;
+        auto key_row = [&](const f16 *pool) {
+            return [&, pool](int R) {
+                int j = t * 32 + R;
+                j = j < ws ? ws : (j >= T ? T - 1 : j);  // finite rows outside the keys (masked)
+                const int64_t phys = bt_lds[j / bs - blk0];
+                return pool + ((phys * bs + j % bs) * p.num_kv_heads + kvh) * 128;
+            };
+        };
+        tile_dma(k_lds[slot], wave, lane, key_row(K));
+        tile_dma(v_lds[slot], wave, lane, key_row(V));
     };
     const TrAddr ta = tr_addr(lane);
-    bw_f32x16 dq[4];
+    bw_f32x16 dq[NB][4];
+    float dsum[NB], D[NB];
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++) dq[dt] = (bw_f32x16)0.0f;
-    float dsum = 0.0f, D = 0.0f;
-    f16x8 kr[2], vr[2];
-    fetch(t0, kr, vr);
-    stage(0, kr, vr);
-    __syncthreads();
-    for (int it = 0; it < 2 * NT; it++) {
-        const int t = t0 + it % NT, buf = it & 1;
+    for (int b = 0; b < NB; b++) {
+        dsum[b] = D[b] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) dq[b][dt] = (bw_f32x16)0.0f;
+    }
+    // the operand loads are complete before the ring starts (as in bwd_dkv_mfma)
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+#pragma unroll
+        for (int c = 0; c < 8; c++) asm volatile("" ::"v"(qv[b][c]), "v"(gv[b][c]));
+        asm volatile("" ::"v"(crow[b]));
+    }
+#pragma unroll
+    for (int u = 0; u < kBwdRing - 1; u++) issue(u);
+    for (int it = 0; it < NI; it++) {
+        // this wave's loads of tile it are done (4 loads per tile), then every
+        // wave's, and every wave has finished iteration it - 1
+        ring_barrier<4 * (kBwdRing - 2)>();
+        issue(it + kBwdRing - 1);  // into the slot iteration it - 1 read
+        const int t = t0 + it % NT, slot = it % kBwdRing;
         const bool second = it >= NT;
-        if (it + 1 < 2 * NT) fetch(t0 + (it + 1) % NT, kr, vr);
-        if (it == NT) {  // pass 1 done: the row's D (the two lane halves hold different keys)
-            D = dsum + __shfl_xor(dsum, 32, 64);
+        if (it == NT) {  // pass 1 done: each row's D (the two lane halves hold different keys)
+#pragma unroll
+            for (int b = 0; b < NB; b++) D[b] = dsum[b] + __shfl_xor(dsum[b], 32, 64);
         }
-        const f16 *kt = k_lds[buf], *vt = v_lds[buf];
-        bw_f32x16 s = (bw_f32x16)0.0f, dp = (bw_f32x16)0.0f;
+        const f16 *kt = k_lds[slot], *vt = v_lds[slot];
+        bw_f32x16 s[NB], dp[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) s[b] = dp[b] = (bw_f32x16)0.0f;
 #pragma unroll
         for (int c = 0; c < 8; c++) {
             const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[bw_at(n, 2 * c + h)]);
             const f16x8 va = *reinterpret_cast<const f16x8 *>(&vt[bw_at(n, 2 * c + h)]);
-            s = bw_mfma(ka, qv[c], s);
-            dp = bw_mfma(va, gv[c], dp);
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                s[b] = bw_mfma(ka, qv[b][c], s[b]);
+                dp[b] = bw_mfma(va, gv[b][c], dp[b]);
+            }
         }
         const bool edge = t * 32 < ws || t * 32 + 32 > T;
 #pragma unroll
-        for (int r2 = 0; r2 < 16; r2++) {
-            float pr = __builtin_amdgcn_exp2f(s[r2] * sl2 - crow);
-            if (edge) {
-                const int j = t * 32 + 8 * (r2 >> 2) + 4 * h + (r2 & 3);
-                pr = (j >= ws && j < T) ? pr : 0.0f;
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int r2 = 0; r2 < 16; r2++) {
+                float pr = __builtin_amdgcn_exp2f(s[b][r2] * sl2 - crow[b]);
+                if (edge) {
+                    const int j = t * 32 + 8 * (r2 >> 2) + 4 * h + (r2 & 3);
+                    pr = (j >= ws && j < T) ? pr : 0.0f;
+                }
+                s[b][r2] = pr;
             }
-            s[r2] = pr;
-        }
         if (!second) {
 #pragma unroll
-            for (int r2 = 0; r2 < 16; r2++) dsum = fmaf(s[r2], dp[r2], dsum);
-        } else {
-            bw_f32x16 ds;
+            for (int b = 0; b < NB; b++)
 #pragma unroll
-            for (int r2 = 0; r2 < 16; r2++) ds[r2] = s[r2] * (dp[r2] - D) * kBwdPScale;
-            f16x8 db[2];
-            to_chunks(ds, db);
+                for (int r2 = 0; r2 < 16; r2++) dsum[b] = fmaf(s[b][r2], dp[b][r2], dsum[b]);
+        } else {
+            f16x8 db[NB][2];
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                bw_f32x16 ds;
+#pragma unroll
+                for (int r2 = 0; r2 < 16; r2++) ds[r2] = s[b][r2] * (dp[b][r2] - D[b]) * kBwdPScale;
+                to_chunks(ds, db[b]);
+            }
 #pragma unroll
             for (int c = 0; c < 2; c++)
 #pragma unroll
-                for (int dt = 0; dt < 4; dt++) dq[dt] = bw_mfma(tr_operand(kt, ta, dt, c), db[c], dq[dt]);
+                for (int dt = 0; dt < 4; dt++) {
+                    const f16x8 kT = tr_operand(kt, ta, dt, c);
+#pragma unroll
+                    for (int b = 0; b < NB; b++) dq[b][dt] = bw_mfma(kT, db[b][c], dq[b][dt]);
+                }
         }
-        __syncthreads();  // every wave is done with buffer buf ^ 1 (read two iterations ago)
-        if (it + 1 < 2 * NT) stage(buf ^ 1, kr, vr);
-        __syncthreads();
     }
-    if (NT == 0) D = 0.0f;
-    if (!row_ok) return;
-    if (h == 0) {
-        p.row_d[(int64_t)tok * H + hq] = D;
-        p.row_c[(int64_t)tok * H + hq] = crow;
-    }
-    // dQ^T accumulator: lane (row n, h) holds dims 32 dt + 8 q + 4 h + (0..3)
-    f16 *dQ = static_cast<f16 *>(p.d_q) + qo + 4 * h;
+    ring_barrier<0>();  // the loads issued past the last tile
     const float f = p.scale / kBwdPScale;
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            f16x4 v;
-#pragma unroll
-            for (int e = 0; e < 4; e++) v[e] = (f16)(dq[dt][4 * q + e] * f);
-            *reinterpret_cast<f16x4 *>(dQ + 32 * dt + 8 * q) = v;
+    for (int b = 0; b < NB; b++) {
+        if (!row_ok[b]) continue;
+        if (h == 0) {
+            p.row_d[so[b]] = NT > 0 ? D[b] : 0.0f;
+            p.row_c[so[b]] = crow[b];
         }
+        // dQ^T accumulator: lane (row n, h) holds dims 32 dt + 8 q + 4 h + (0..3)
+        f16 *dQ = static_cast<f16 *>(p.d_q) + qo[b] + 4 * h;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                f16x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = (f16)(dq[b][dt][4 * q + e] * f);
+                *reinterpret_cast<f16x4 *>(dQ + 32 * dt + 8 * q) = v;
+            }
+    }
 }
 
-__global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dkv_mfma(BackwardParams p) {
-    __shared__ __attribute__((aligned(16))) f16 q_lds[2][32 * 128];
-    __shared__ __attribute__((aligned(16))) f16 g_lds[2][32 * 128];
-    __shared__ __attribute__((aligned(16))) float c_lds[2][32];
-    __shared__ __attribute__((aligned(16))) float d_lds[2][32];
+
+template <int NB>
+__global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dkv_mfma(BackwardParams p, int group_shift) {
+    __shared__ __attribute__((aligned(16))) f16 q_lds[kBwdRing][32 * 128];
+    __shared__ __attribute__((aligned(16))) f16 g_lds[kBwdRing][32 * 128];
+    __shared__ __attribute__((aligned(16))) float c_lds[kBwdRing][32];
+    __shared__ __attribute__((aligned(16))) float d_lds[kBwdRing][32];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
-    const int H = p.num_heads, G = H / p.num_kv_heads, kvh = blockIdx.y;
+    const int H = p.num_heads, G = 1 << group_shift, kvh = blockIdx.y;
     const int T = p.seq_len, ws = p.window_start;
     const int rows = T * G;
-    const int key = ws + (blockIdx.x * kBwdWaves + wave) * 32 + n;  // this lane's key
-    const bool key_ok = key < T;
-    const int kj = key_ok ? key : T - 1;
     const f16 *Q = static_cast<const f16 *>(p.q), *dO = static_cast<const f16 *>(p.d_out);
     const f16 *K = static_cast<const f16 *>(p.k_pool), *V = static_cast<const f16 *>(p.v_pool);
-    // K^T and V^T as B operands: lane (key n, h) holds dims 16c + 8h .. +7
-    f16x8 kb[8], vb[8];
-    {
+    // the wave's NB blocks of 32 keys; K^T and V^T as B operands: lane (key n,
+    // h) holds dims 16c + 8h .. +7
+    int key[NB];
+    f16x8 kb[NB][8], vb[NB][8];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        key[b] = ws + ((blockIdx.x * kBwdWaves + wave) * NB + b) * 32 + n;
+        const int kj = key[b] < T ? key[b] : T - 1;
         const f16 *kr = pool_row(K, p, kj, kvh), *vr = pool_row(V, p, kj, kvh);
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            kb[c] = *reinterpret_cast<const f16x8 *>(kr + 16 * c + 8 * h);
-            vb[c] = *reinterpret_cast<const f16x8 *>(vr + 16 * c + 8 * h);
+            kb[b][c] = *reinterpret_cast<const f16x8 *>(kr + 16 * c + 8 * h);
+            vb[b][c] = *reinterpret_cast<const f16x8 *>(vr + 16 * c + 8 * h);
         }
     }
     const float sl2 = p.scale * kLog2e;
-    const int sp = tid & 15, sr = tid >> 4;
     const int NT = (rows + 31) / 32;
-    // row tile t: rows 32t .. 32t + 31 (token r / G, head kvh G + r % G)
-    auto fetch = [&](int t, f16x8 (&qr)[2], f16x8 (&gr)[2], float &cr, float &dr) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int r = t * 32 + sr + 16 * i;
-            if (r < rows) {
-                const int64_t o = ((int64_t)(r / G) * H + kvh * G + r % G) * 128 + 8 * sp;
-                qr[i] = *reinterpret_cast<const f16x8 *>(Q + o);
-                gr[i] = *reinterpret_cast<const f16x8 *>(dO + o);
-            } else {
-                qr[i] = gr[i] = (f16x8)(f16)0.0f;
-            }
-        }
-        if (tid < 32) {
-            const int r = t * 32 + tid;
-            const int64_t o = (int64_t)(r / G) * H + kvh * G + r % G;
-            cr = r < rows ? p.row_c[o] : INFINITY;  // rows past the end: P = 0
-            dr = r < rows ? p.row_d[o] : 0.0f;
-        }
+    // row tile t: rows 32t .. 32t + 31 (token r / G, head kvh G + r % G); rows
+    // past the end load the last row and are masked
+    auto head_row = [&](int r) -> int64_t {
+        r = r < rows ? r : rows - 1;
+        return (int64_t)(r >> group_shift) * H + kvh * G + (r & (G - 1));
     };
-    auto stage = [&](int buf, const f16x8 (&qr)[2], const f16x8 (&gr)[2], float cr, float dr) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            *reinterpret_cast<f16x8 *>(&q_lds[buf][bw_at(sr + 16 * i, sp)]) = qr[i];
-            *reinterpret_cast<f16x8 *>(&g_lds[buf][bw_at(sr + 16 * i, sp)]) = gr[i];
-        }
-        if (tid < 32) {
-            c_lds[buf][tid] = cr;
-            d_lds[buf][tid] = dr;
-        }
+    // five loads per wave and tile: Q and dO (two each), then the row terms c
+    // (even waves) or D (odd waves) for lanes 0-31 (two waves write each, the same values)
+    auto issue = [&](int t, f16 *qs, f16 *gs, float *cs, float *ds) {
+        t = t < NT ? t : NT - 1;
+        tile_dma(qs, wave, lane, [&](int R) { return Q + head_row(t * 32 + R) * 128; });
+        tile_dma(gs, wave, lane, [&](int R) { return dO + head_row(t * 32 + R) * 128; });
+        const float *src = (wave & 1) ? p.row_d : p.row_c;
+        float *dst = (wave & 1) ? ds : cs;
+        if (lane < 32) lds_dma4(src + head_row(t * 32 + lane), dst);
     };
     const TrAddr ta = tr_addr(lane);
-    bw_f32x16 dk[4], dv[4];
+    bw_f32x16 dk[NB][4], dv[NB][4];
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++) dk[dt] = dv[dt] = (bw_f32x16)0.0f;
-    f16x8 qr[2], gr[2];
-    float cr = 0.0f, dr = 0.0f;
-    fetch(0, qr, gr, cr, dr);
-    stage(0, qr, gr, cr, dr);
-    __syncthreads();
-    for (int t = 0; t < NT; t++) {
-        const int buf = t & 1;
-        if (t + 1 < NT) fetch(t + 1, qr, gr, cr, dr);
-        const f16 *qt = q_lds[buf], *gt = g_lds[buf];
-        bw_f32x16 s = (bw_f32x16)0.0f, dp = (bw_f32x16)0.0f;
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) dk[b][dt] = dv[b][dt] = (bw_f32x16)0.0f;
+    auto compute = [&](int t, const f16 *qt, const f16 *gt, const float *ct, const float *dtab) {
+        bw_f32x16 s[NB], dp[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) s[b] = dp[b] = (bw_f32x16)0.0f;
 #pragma unroll
         for (int c = 0; c < 8; c++) {
             const f16x8 qa = *reinterpret_cast<const f16x8 *>(&qt[bw_at(n, 2 * c + h)]);
             const f16x8 ga = *reinterpret_cast<const f16x8 *>(&gt[bw_at(n, 2 * c + h)]);
-            s = bw_mfma(qa, kb[c], s);
-            dp = bw_mfma(ga, vb[c], dp);
-        }
-        // registers r hold rows 8 (r / 4) + 4 h + r % 4 of the tile
-        bw_f32x16 pr, ds;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 cq = *reinterpret_cast<const float4 *>(&c_lds[buf][8 * q + 4 * h]);
-            const float4 dq = *reinterpret_cast<const float4 *>(&d_lds[buf][8 * q + 4 * h]);
-            const float cv[4] = {cq.x, cq.y, cq.z, cq.w}, dv4[4] = {dq.x, dq.y, dq.z, dq.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float P = __builtin_amdgcn_exp2f(s[4 * q + e] * sl2 - cv[e]);
-                pr[4 * q + e] = P * kBwdPScale;
-                ds[4 * q + e] = P * (dp[4 * q + e] - dv4[e]) * kBwdPScale;
+            for (int b = 0; b < NB; b++) {
+                s[b] = bw_mfma(qa, kb[b][c], s[b]);
+                dp[b] = bw_mfma(ga, vb[b][c], dp[b]);
             }
         }
-        f16x8 pb[2], db[2];
-        to_chunks(pr, pb);
-        to_chunks(ds, db);
+        // registers r hold rows 8 (r / 4) + 4 h + r % 4 of the tile
+        const bool tail = t * 32 + 32 > rows;
+        f16x8 pb[NB][2], db[NB][2];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            bw_f32x16 pr, ds;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 cq = *reinterpret_cast<const float4 *>(&ct[8 * q + 4 * h]);
+                const float4 dq = *reinterpret_cast<const float4 *>(&dtab[8 * q + 4 * h]);
+                const float cv[4] = {cq.x, cq.y, cq.z, cq.w}, dd[4] = {dq.x, dq.y, dq.z, dq.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float P = __builtin_amdgcn_exp2f(s[b][4 * q + e] * sl2 - cv[e]);
+                    if (tail) P = t * 32 + 8 * q + 4 * h + e < rows ? P : 0.0f;
+                    pr[4 * q + e] = P * kBwdPScale;
+                    ds[4 * q + e] = P * (dp[b][4 * q + e] - dd[e]) * kBwdPScale;
+                }
+            }
+            to_chunks(pr, pb[b]);
+            to_chunks(ds, db[b]);
+        }
 #pragma unroll
         for (int c = 0; c < 2; c++)
 #pragma unroll
             for (int dt = 0; dt < 4; dt++) {
-                dv[dt] = bw_mfma(tr_operand(gt, ta, dt, c), pb[c], dv[dt]);
-                dk[dt] = bw_mfma(tr_operand(qt, ta, dt, c), db[c], dk[dt]);
+                const f16x8 gT = tr_operand(gt, ta, dt, c), qT = tr_operand(qt, ta, dt, c);
+#pragma unroll
+                for (int b = 0; b < NB; b++) {
+                    dv[b][dt] = bw_mfma(gT, pb[b][c], dv[b][dt]);
+                    dk[b][dt] = bw_mfma(qT, db[b][c], dk[b][dt]);
+                }
             }
-        __syncthreads();
-        if (t + 1 < NT) stage(buf ^ 1, qr, gr, cr, dr);
-        __syncthreads();
+    };
+    // the operand loads are complete before the ring starts: the compiler does
+    // not count the ring's loads, and would otherwise wait on them in the loop
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int c = 0; c < 8; c++) asm volatile("" ::"v"(kb[b][c]), "v"(vb[b][c]));
+#pragma unroll
+    for (int u = 0; u < kBwdRing - 1; u++) issue(u, q_lds[u], g_lds[u], c_lds[u], d_lds[u]);
+    // tile t is read from slot t % 4; at its barrier the loads of tile t are done
+    // (tiles t + 1 and t + 2 may still be in flight: 5 loads each) and every wave
+    // has left tile t - 1, whose slot then receives tile t + 3
+    for (int t = 0; t < NT; t++) {
+        ring_barrier<5 * (kBwdRing - 2)>();
+        const int w = (t + kBwdRing - 1) % kBwdRing, r = t % kBwdRing;
+        issue(t + kBwdRing - 1, q_lds[w], g_lds[w], c_lds[w], d_lds[w]);
+        compute(t, q_lds[r], g_lds[r], c_lds[r], d_lds[r]);
     }
-    if (!key_ok) return;
+    ring_barrier<0>();  // the loads issued past the last tile
     // accumulators: lane (key n, h) holds dims 32 dt + 8 q + 4 h + (0..3); this
-    // wave alone owns the key's rows of the gradient pools
-    f16 *dkr = const_cast<f16 *>(pool_row(static_cast<const f16 *>(p.d_k_pool), p, key, kvh)) + 4 * h;
-    f16 *dvr = const_cast<f16 *>(pool_row(static_cast<const f16 *>(p.d_v_pool), p, key, kvh)) + 4 * h;
+    // wave alone owns its keys' rows of the gradient pools
     const float fk = p.scale / kBwdPScale, fv = 1.0f / kBwdPScale;
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
+    for (int b = 0; b < NB; b++) {
+        if (key[b] >= T) continue;
+        f16 *dkr = const_cast<f16 *>(pool_row(static_cast<const f16 *>(p.d_k_pool), p, key[b], kvh)) + 4 * h;
+        f16 *dvr = const_cast<f16 *>(pool_row(static_cast<const f16 *>(p.d_v_pool), p, key[b], kvh)) + 4 * h;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            f16x4 a = *reinterpret_cast<const f16x4 *>(dkr + 32 * dt + 8 * q);
-            f16x4 b = *reinterpret_cast<const f16x4 *>(dvr + 32 * dt + 8 * q);
+        for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                a[e] = (f16)((float)a[e] + dk[dt][4 * q + e] * fk);
-                b[e] = (f16)((float)b[e] + dv[dt][4 * q + e] * fv);
+            for (int q = 0; q < 4; q++) {
+                f16x4 a = *reinterpret_cast<const f16x4 *>(dkr + 32 * dt + 8 * q);
+                f16x4 c = *reinterpret_cast<const f16x4 *>(dvr + 32 * dt + 8 * q);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    a[e] = (f16)((float)a[e] + dk[b][dt][4 * q + e] * fk);
+                    c[e] = (f16)((float)c[e] + dv[b][dt][4 * q + e] * fv);
+                }
+                *reinterpret_cast<f16x4 *>(dkr + 32 * dt + 8 * q) = a;
+                *reinterpret_cast<f16x4 *>(dvr + 32 * dt + 8 * q) = c;
             }
-            *reinterpret_cast<f16x4 *>(dkr + 32 * dt + 8 * q) = a;
-            *reinterpret_cast<f16x4 *>(dvr + 32 * dt + 8 * q) = b;
-        }
+    }
 }
+
+constexpr int kBwdNB = 1;  // 32-row / 32-key blocks per wave (2 needs more than 512 registers)
 
 hipError_t launch_backward(const BackwardParams &p, int32_t dtype, hipStream_t stream) {
     if (p.seq_len <= 0) return hipSuccess;
     if (p.head_dim > 64 * kBwdMaxDims || p.row_d == nullptr) return hipErrorInvalidValue;
     const dim3 rows(p.seq_len, p.num_heads), keys(p.seq_len - p.window_start, p.num_kv_heads);
-    if (dtype == kF16 && p.head_dim == 128 && p.row_c != nullptr) {
-        const int64_t qrows = (int64_t)p.seq_len * (p.num_heads / p.num_kv_heads);
+    const int G = p.num_heads / p.num_kv_heads;
+    const int64_t nblk = p.block_size > 0 ? (int64_t)(p.seq_len - 1) / p.block_size - p.window_start / p.block_size + 1 : 0;
+    if (dtype == kF16 && p.head_dim == 128 && p.row_c != nullptr && (G & (G - 1)) == 0 && nblk <= kBwdBtCache) {
+        const int64_t qrows = (int64_t)p.seq_len * G;
         const int64_t nkeys = p.seq_len - p.window_start;
-        const int per = 32 * kBwdWaves;
-        hipLaunchKernelGGL(bwd_dq_mfma, dim3((unsigned)((qrows + per - 1) / per), p.num_kv_heads), dim3(64 * kBwdWaves),
-                           0, stream, p);
+        const int per = 32 * kBwdWaves * kBwdNB, gs = __builtin_ctz((unsigned)G);
+        hipLaunchKernelGGL(bwd_dq_mfma<kBwdNB>, dim3((unsigned)((qrows + per - 1) / per), p.num_kv_heads),
+                           dim3(64 * kBwdWaves), 0, stream, p, gs);
         if (nkeys > 0)
-            hipLaunchKernelGGL(bwd_dkv_mfma, dim3((unsigned)((nkeys + per - 1) / per), p.num_kv_heads),
-                               dim3(64 * kBwdWaves), 0, stream, p);
+            hipLaunchKernelGGL(bwd_dkv_mfma<kBwdNB>, dim3((unsigned)((nkeys + per - 1) / per), p.num_kv_heads),
+                               dim3(64 * kBwdWaves), 0, stream, p, gs);
         return hipGetLastError();
     }
     if (dtype == kF32) {
