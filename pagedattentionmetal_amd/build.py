@@ -22,6 +22,9 @@ ARCH = "gfx950"
 # Packed FP32 VALU forms are disabled for all device code; hipcc's host pass
 # warns that it does not know the feature, which is harmless.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# per-source additions: the backward kernels keep their MFMA results in VGPRs
+# (with the default AGPR form the compiler copies every score tile out of AGPRs)
+FILE_FLAGS = {"backward.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", f"--offload-arch={ARCH}",
           "-fvisibility=hidden"]
 
@@ -45,7 +48,7 @@ def _hipcc():
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.relpath(src, CSRC).replace(os.sep, "_") + ".o")
-    cmd = [_hipcc(), *COMMON, *DEVICE_FLAGS, "-c", src, "-o", obj]
+    cmd = [_hipcc(), *COMMON, *DEVICE_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd = [_hipcc(), *COMMON, "-x", "hip", *DEVICE_FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -18,6 +18,8 @@
 //     f32.
 // Lanes hold dims lane + 64 t of the head (t < 4, d <= 256); dot products are
 // wave reductions, loads of a key or query row are 64 lanes over contiguous dims.
+#include <type_traits>
+
 #include "kernels.h"
 #include "pam_device.h"
 
@@ -176,6 +178,7 @@ __global__ __launch_bounds__(64) void bwd_keys_kernel(BackwardParams p) {
 typedef float bw_f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBwdWaves = 4;             // waves per workgroup, 32 rows / keys each
 constexpr float kBwdPScale = 256.0f;
+constexpr float kPScaleLog2 = 8.0f;  // log2(kBwdPScale)
 constexpr int kBwdRing = 4;                // LDS tiles per operand (kBwdRing - 1 loads in flight)
 constexpr int kBwdBtCache = 8192;          // block-table entries the dQ kernel keeps in LDS
 
@@ -344,7 +347,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams 
         const bool second = it >= NT;
         if (it == NT) {  // pass 1 done: each row's D (the two lane halves hold different keys)
 #pragma unroll
-            for (int b = 0; b < NB; b++) D[b] = dsum[b] + __shfl_xor(dsum[b], 32, 64);
+            for (int b = 0; b < NB; b++) D[b] = (dsum[b] + __shfl_xor(dsum[b], 32, 64)) * (1.0f / kBwdPScale);
         }
         const f16 *kt = k_lds[slot], *vt = v_lds[slot];
         bw_f32x16 s[NB], dp[NB];
@@ -361,17 +364,24 @@ __global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams 
             }
         }
         const bool edge = t * 32 < ws || t * 32 + 32 > T;
+        // 2^8 P straight from the exponential (c - 8)
+        auto probs = [&](auto edge) {
 #pragma unroll
-        for (int b = 0; b < NB; b++)
+            for (int b = 0; b < NB; b++)
 #pragma unroll
-            for (int r2 = 0; r2 < 16; r2++) {
-                float pr = __builtin_amdgcn_exp2f(s[b][r2] * sl2 - crow[b]);
-                if (edge) {
-                    const int j = t * 32 + 8 * (r2 >> 2) + 4 * h + (r2 & 3);
-                    pr = (j >= ws && j < T) ? pr : 0.0f;
+                for (int r2 = 0; r2 < 16; r2++) {
+                    float pr = __builtin_amdgcn_exp2f(fmaf(s[b][r2], sl2, kPScaleLog2 - crow[b]));
+                    if (decltype(edge)::value) {
+                        const int j = t * 32 + 8 * (r2 >> 2) + 4 * h + (r2 & 3);
+                        pr = (j >= ws && j < T) ? pr : 0.0f;
+                    }
+                    s[b][r2] = pr;
                 }
-                s[b][r2] = pr;
-            }
+        };
+        if (edge)
+            probs(std::true_type{});
+        else
+            probs(std::false_type{});
         if (!second) {
 #pragma unroll
             for (int b = 0; b < NB; b++)
@@ -383,7 +393,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams 
             for (int b = 0; b < NB; b++) {
                 bw_f32x16 ds;
 #pragma unroll
-                for (int r2 = 0; r2 < 16; r2++) ds[r2] = s[b][r2] * (dp[b][r2] - D[b]) * kBwdPScale;
+                for (int r2 = 0; r2 < 16; r2++) ds[r2] = s[b][r2] * (dp[b][r2] - D[b]);
                 to_chunks(ds, db[b]);
             }
 #pragma unroll
@@ -485,28 +495,34 @@ __global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dkv_mfma(BackwardParams
                 dp[b] = bw_mfma(ga, vb[b][c], dp[b]);
             }
         }
-        // registers r hold rows 8 (r / 4) + 4 h + r % 4 of the tile
-        const bool tail = t * 32 + 32 > rows;
+        // registers r hold rows 8 (r / 4) + 4 h + r % 4 of the tile; 2^8 P comes
+        // straight from the exponential (c - 8)
         f16x8 pb[NB][2], db[NB][2];
+        auto probs = [&](auto tail) {
 #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            bw_f32x16 pr, ds;
+            for (int b = 0; b < NB; b++) {
+                bw_f32x16 pr, ds;
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 cq = *reinterpret_cast<const float4 *>(&ct[8 * q + 4 * h]);
-                const float4 dq = *reinterpret_cast<const float4 *>(&dtab[8 * q + 4 * h]);
-                const float cv[4] = {cq.x, cq.y, cq.z, cq.w}, dd[4] = {dq.x, dq.y, dq.z, dq.w};
+                for (int q = 0; q < 4; q++) {
+                    const float4 cq = *reinterpret_cast<const float4 *>(&ct[8 * q + 4 * h]);
+                    const float4 dq = *reinterpret_cast<const float4 *>(&dtab[8 * q + 4 * h]);
+                    const float cv[4] = {cq.x, cq.y, cq.z, cq.w}, dd[4] = {dq.x, dq.y, dq.z, dq.w};
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float P = __builtin_amdgcn_exp2f(s[b][4 * q + e] * sl2 - cv[e]);
-                    if (tail) P = t * 32 + 8 * q + 4 * h + e < rows ? P : 0.0f;
-                    pr[4 * q + e] = P * kBwdPScale;
-                    ds[4 * q + e] = P * (dp[b][4 * q + e] - dd[e]) * kBwdPScale;
+                    for (int e = 0; e < 4; e++) {
+                        float P = __builtin_amdgcn_exp2f(fmaf(s[b][4 * q + e], sl2, kPScaleLog2 - cv[e]));
+                        if (decltype(tail)::value) P = t * 32 + 8 * q + 4 * h + e < rows ? P : 0.0f;
+                        pr[4 * q + e] = P;
+                        ds[4 * q + e] = P * (dp[b][4 * q + e] - dd[e]);
+                    }
                 }
+                to_chunks(pr, pb[b]);
+                to_chunks(ds, db[b]);
             }
-            to_chunks(pr, pb[b]);
-            to_chunks(ds, db[b]);
-        }
+        };
+        if (t * 32 + 32 > rows)
+            probs(std::true_type{});
+        else
+            probs(std::false_type{});
 #pragma unroll
         for (int c = 0; c < 2; c++)
 #pragma unroll
