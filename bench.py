@@ -11,7 +11,8 @@ of the whole batch with Q, pools and tables already resident in HBM.
 
 Prints one JSON line.  "configs" holds the c1, c4 and c5 decode lines (skipped
 with --no-configs); "trace_c5" the 200-step scheduler trace of c5 (skipped with
---no-trace).  Every configuration carries a CPU baseline: the oracle on
+--no-trace); "next_rows" the fused prefill, backward, copy-on-write and adapter
+measurements (skipped with --no-next).  Every configuration carries a CPU baseline: the oracle on
 the host's cores over a bounded sample of the same inputs (skipped with
 --no-cpu).  The roofline block times the dominant kernel (the decode attention
 kernel) with HIP events on the stream it is launched on.
@@ -250,6 +251,147 @@ def cpu_baseline_prefill(torch, w3, t3, threads, rows=64, min_seconds=1.0, max_r
     return flops * reps / dt / 1e12, dt, reps, f"rows [{ctx}, {ctx + T}) of a causal prefill at context {ctx} (chunk 0)"
 
 
+def run_next_rows(torch, api, workloads, cpu=True, threads=16):
+    """The rows after the hot path, each on one shape with its roofline and a CPU
+    baseline: fused append + prefill (one 4096-token prompt), the backward (a
+    4096-token sequence), copy-on-write of a shared prefix block, and the
+    framework adapter's decode step."""
+    import numpy as np
+
+    out = {}
+    H, hkv, d, bs = 32, 8, 128, 16
+    eng = api.PagedAttentionEngine()
+    eng.set_graceful_degradation(False)
+    stream = torch.cuda.current_stream()
+    eng.set_stream(stream)
+    layer = api.PagedLayerSpec(d, H, hkv, bs, 1)
+    seed = workloads.SEED_BASE + 6
+
+    def timed(fn, reps, warm=3):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        ms = median(event_steps(torch, stream, fn, reps))
+        return ms
+
+    # f2: fused append + prefill of one prompt (PagedAttentionEngine.fusedPrefill)
+    T = 4096
+    nbl = T // bs
+    perm = torch.from_numpy(workloads.permutation(seed, 2 * nbl)[:nbl].astype(np.int32)).cuda()
+    kp = torch.zeros((2 * nbl, bs, hkv, d), dtype=torch.float16, device="cuda")
+    vp = torch.zeros_like(kp)
+    q = workloads.device_normals((T, H, d), torch.float16, seed, workloads.S_Q)
+    rk = workloads.device_normals((T, hkv, d), torch.float16, seed, workloads.S_NEW_K, 0.5)
+    rv = workloads.device_normals((T, hkv, d), torch.float16, seed, workloads.S_NEW_V, 0.5)
+    o = torch.empty_like(q)
+    eng.synchronous = False
+    eng.set_gpu_timing(False)
+    fused_ms = timed(lambda: eng.fused_prefill(q, rk, rv, perm, kp, vp, o, T, layer), 20)
+    sep_ms = timed(lambda: (eng.append_to_cache(rk, rv, kp, vp, perm, 0, T, layer),
+                            eng.prefill(q, kp, vp, perm, o, T, layer, causal=True)), 20)
+    flops = 4 * d * H * T * (T + 1) // 2
+    f2 = {"workload": f"one {T}-token causal prompt, append of its K/V included, {H}/{hkv} heads, d={d}, bs={bs}, f16",
+          "ms": round(fused_ms, 4), "tflops": round(flops / (fused_ms * 1e-3) / 1e12, 1),
+          "peak_tflops": 2500.0, "frac": round(flops / (fused_ms * 1e-3) / 1e12 / 2500.0, 4),
+          "append_then_prefill_ms": round(sep_ms, 4)}
+    if cpu:
+        import oracle
+        rows = 32
+        qh, kh, vh = q[T - rows:].cpu().numpy(), kp.cpu().numpy(), vp.cpu().numpy()
+        bth = perm.cpu().numpy()
+        cf = 4 * d * H * (rows * (T - rows) + rows * (rows + 1) // 2)
+        t0, reps = time.perf_counter(), 0
+        while True:
+            oracle.prefill(1, qh, kh, vh, bth, T - rows, causal=True, n_threads=threads)
+            reps += 1
+            if time.perf_counter() - t0 >= 2.0 or reps >= 50:
+                break
+        dt = time.perf_counter() - t0
+        f2["cpu_baseline"] = {"value": round(cf * reps / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                              "kind": "port",
+                              "sample": f"{reps} x the last {rows} rows of the prompt through the C oracle, {dt:.2f} s"}
+    out["f2_fused_prefill"] = f2
+
+    # f4: backward of one sequence (PagedAttentionEngine.backward)
+    go = workloads.device_normals((T, H, d), torch.float16, seed, 9)
+    m = torch.zeros((T, H), dtype=torch.float32, device="cuda")
+    lsum = torch.full((T, H), float(T), dtype=torch.float32, device="cuda")
+    dq = torch.empty_like(q)
+    dk, dv = torch.zeros_like(kp), torch.zeros_like(vp)
+    bwd_ms = timed(lambda: eng.backward(q, kp, vp, perm, go, m, lsum, dq, dk, dv, T, layer), 10, warm=2)
+    bflops = 10 * T * T * d * H
+    f4 = {"workload": f"non-causal backward of one {T}-token sequence, {H}/{hkv} heads, d={d}, f16 "
+                      "(dQ, dK, dV; flops 10 T^2 d H)",
+          "ms": round(bwd_ms, 4), "tflops": round(bflops / (bwd_ms * 1e-3) / 1e12, 1), "peak_tflops": 2500.0,
+          "frac": round(bflops / (bwd_ms * 1e-3) / 1e12 / 2500.0, 4)}
+    if cpu:
+        import oracle
+        Ts = 256
+        rng = np.random.default_rng(1)
+        qs = rng.standard_normal((Ts, H, d)).astype(np.float16)
+        ks = rng.standard_normal((Ts // bs, bs, hkv, d)).astype(np.float16)
+        vs = rng.standard_normal((Ts // bs, bs, hkv, d)).astype(np.float16)
+        gs = rng.standard_normal((Ts, H, d)).astype(np.float16)
+        bts = np.arange(Ts // bs, dtype=np.int32)
+        mm, ll, _ = oracle.forward_stats(qs, ks, vs, bts)
+        t0, reps = time.perf_counter(), 0
+        while True:
+            oracle.backward(qs, ks, vs, bts, gs, mm, ll)
+            reps += 1
+            if time.perf_counter() - t0 >= 2.0 or reps >= 20:
+                break
+        dt = time.perf_counter() - t0
+        f4["cpu_baseline"] = {"value": round(10 * Ts * Ts * d * H * reps / dt / 1e12, 6), "unit": "TFLOP/s",
+                              "cores": 1, "kind": "port",
+                              "sample": f"{reps} x the backward of a {Ts}-token sequence (same heads) through the "
+                                        f"oracle, {dt:.2f} s"}
+    out["f4_backward"] = f4
+    eng.synchronous = True
+    eng.set_gpu_timing(True)
+
+    # f1: copy-on-write of a shared prefix block (KVCacheManager.ensureExclusiveAccess)
+    nseq = 64
+    cache = api.KVCacheManager(eng, 4 * nseq, bs, d, hkv, 1)
+    cache.allocate_sequence(0)
+    cache.append_tokens(0, bs, block_hashes=[0xC0FFEE])
+    for sid in range(1, nseq + 1):
+        cache.allocate_sequence(sid)
+        cache.append_tokens(sid, bs, block_hashes=[0xC0FFEE])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for sid in range(1, nseq + 1):
+        cache.ensure_exclusive_access(sid, 0)
+    torch.cuda.synchronize()
+    cow_us = (time.perf_counter() - t0) / nseq * 1e6
+    out["f1_copy_on_write"] = {"workload": f"{nseq} sequences sharing one {bs}-token f16 prefix block "
+                                           f"({hkv} kv heads, d={d}) each made exclusive",
+                               "us_per_call": round(cow_us, 2), "bytes_per_call": 2 * bs * hkv * d * 2,
+                               "note": "one synchronous call per block: host bookkeeping plus a device copy"}
+
+    # f3: the adapter's decode step (PagedMetalKVCache.pagedAttention)
+    from pagedattentionmetal_amd.adapter import PagedTorchKVCache
+    ctx_len = 4096
+    ad = PagedTorchKVCache(1, layer, (ctx_len + 64) // bs + 2)  # its own engine, on the torch stream
+    qp = workloads.device_normals((1, H, ctx_len, d), torch.float16, seed, 10)
+    kpf = workloads.device_normals((1, hkv, ctx_len, d), torch.float16, seed, 11, 0.5)
+    vpf = workloads.device_normals((1, hkv, ctx_len, d), torch.float16, seed, 12, 0.5)
+    ad.paged_attention(qp, kpf, vpf, mask="causal")
+    q1, k1, v1 = qp[:, :, :1].contiguous(), kpf[:, :, :1].contiguous(), vpf[:, :, :1].contiguous()
+    steps = 32
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ad.paged_attention(q1, k1, v1)
+    torch.cuda.synchronize()
+    step_us = (time.perf_counter() - t0) / steps * 1e6
+    out["f3_adapter"] = {"workload": f"decode steps of one sequence after a {ctx_len}-token prompt through "
+                                     "PagedTorchKVCache.paged_attention (append + decode, batch 1)",
+                         "us_per_step": round(step_us, 1),
+                         "kv_bytes_per_step": (ctx_len + steps // 2) * hkv * d * 2 * 2,
+                         "note": "batch 1 is launch- and host-bound; the step includes the cache bookkeeping"}
+    return out
+
+
 def run_trace_c5(torch, api, steps=200, seed=0x5EED0005):
     """BASELINE c5's serving trace: `steps` ContinuousBatchingScheduler steps with
     Poisson(2) arrivals, prompts U[64,8192], outputs U[16,512], max batch 32,
@@ -330,6 +472,8 @@ def main():
     ap.add_argument("--trace-only", action="store_true",
                     help="run only the c5 scheduler trace and print its JSON object (for profiling it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-next", action="store_true",
+                    help="skip the next rows (fused prefill, backward, copy-on-write, adapter)")
     ap.add_argument("--only", choices=("c1", "c2", "c3", "c4", "c5"),
                     help="time one configuration alone and print its JSON object (for profiling it)")
     ap.add_argument("--calibrate", action="store_true",
@@ -503,6 +647,9 @@ def main():
     if not args.no_trace:
         log("bench: c5 scheduler trace")
         result["trace_c5"] = run_trace_c5(torch, api)
+    if not args.no_next:
+        log("bench: next rows (fused prefill, backward, copy-on-write, adapter)")
+        result["next_rows"] = run_next_rows(torch, api, workloads, cpu=not args.no_cpu)
     print(json.dumps(result), flush=True)
 
 

@@ -409,6 +409,10 @@ int32_t pam_set_decode_kernel(void *context, int32_t choice);
  * at most 1024 decode rows).  prefill_groups / decode_groups set the one
  * launch's workgroups of each part (0 = automatic). */
 int32_t pam_set_mixed_launch(void *context, int32_t mode, int32_t prefill_groups, int32_t decode_groups);
+/* pam_engine_fused_prefill for f16 caches with d = 128: false (default) appends
+ * then prefills, two launches in the one call; true runs one kernel that writes
+ * the new rows into the pools as it reads them.  Results are identical. */
+int32_t pam_set_fused_prefill_kernel(void *context, bool one_kernel);
 /* true (default): time every call's kernels with HIP events (the elapsed, kernel
  * and reduce times of pam_engine_last_stats); false: no events are recorded and
  * those times read -1. */

@@ -168,6 +168,7 @@ SIGNATURES = {
     "pam_set_partition_tokens": (I32, [P, I32]),
     "pam_set_decode_kernel": (I32, [P, I32]),
     "pam_set_mixed_launch": (I32, [P, I32, I32, I32]),
+    "pam_set_fused_prefill_kernel": (I32, [P, C.c_bool]),
     "pam_set_gpu_timing": (I32, [P, C.c_bool]),
     "pam_engine_mixed_step": (I32, [P, C.POINTER(MixedRequest)]),
     "pam_engine_set_config": (I32, [P, C.POINTER(EngineConfig)]),

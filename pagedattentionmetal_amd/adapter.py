@@ -24,6 +24,8 @@ Differences from the reference, both deliberate:
 """
 from __future__ import annotations
 
+import ctypes as C
+
 from . import api
 from .api import PagedAttentionDataType, PagedAttentionError, PagedLayerSpec
 
@@ -65,7 +67,14 @@ class PagedTorchKVCache:
     def __init__(self, sequence_id: int, layer: PagedLayerSpec, max_blocks: int,
                  engine: api.PagedAttentionEngine | None = None):
         layer.validate()
-        self.engine = engine or api.PagedAttentionEngine()
+        if engine is None:
+            # its own engine enqueues on the caller's current torch stream and
+            # returns at once: the outputs are ordered after the inputs by the stream
+            import torch
+            engine = api.PagedAttentionEngine()
+            engine.set_stream(torch.cuda.current_stream())
+            engine.synchronous = False
+        self.engine = engine
         self.sequence_id = int(sequence_id)
         self.layer = layer
         self.cache_manager = api.KVCacheManager(self.engine, max_blocks, layer.block_size, layer.head_dim,
@@ -117,6 +126,20 @@ class PagedTorchKVCache:
         cm = self.cache_manager
         cur = self.offset
         cm.append_tokens(self.sequence_id, S)
+        if S == 1:
+            # a decode step through the cache's own calls (pam_append_kv, pam_decode):
+            # the library stages the table and length, no tensor is built per step
+            k = keys[0, :, 0].to(io).contiguous()    # [Hkv, d]
+            v = values[0, :, 0].to(io).contiguous()
+            q = queries[0, :, 0].to(io).contiguous()  # [H, d]
+            out = torch.empty_like(q)
+            self.engine._check(api.lib().pam_append_kv(self.engine.handle, cm.handle, self.sequence_id,
+                                                       k.data_ptr(), v.data_ptr(), cur, 1, L.num_kv_heads))
+            ids = (C.c_int64 * 1)(self.sequence_id)
+            self.engine._check(api.lib().pam_decode(self.engine.handle, cm.handle, ids, 1, q.data_ptr(),
+                                                    out.data_ptr(), L.num_heads))
+            self.offset += 1
+            return out.view(1, H, 1, d).to(queries.dtype)
         table = cm.get_block_table(self.sequence_id)
         bt = torch.tensor(table if table else [0], dtype=torch.int32, device=queries.device)
         k = keys[0].transpose(0, 1).to(io).contiguous()    # [S, Hkv, d]

@@ -180,6 +180,11 @@ class PagedAttentionEngine:
         (0 = automatic)."""
         self._check(lib().pam_set_mixed_launch(self._ctx, int(mode), int(prefill_groups), int(decode_groups)))
 
+    def set_fused_prefill_one_kernel(self, one_kernel: bool):
+        """fused_prefill for f16 with d = 128: append then prefill (False, the
+        default) or the one kernel that appends as it reads (True)."""
+        self._check(lib().pam_set_fused_prefill_kernel(self._ctx, bool(one_kernel)))
+
     def set_gpu_timing(self, enabled: bool):
         """HIP-event timing of every call (last_stats times); off: no events, times -1."""
         self._check(lib().pam_set_gpu_timing(self._ctx, bool(enabled)))

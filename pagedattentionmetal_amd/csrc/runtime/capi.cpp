@@ -662,6 +662,10 @@ PAM_API int32_t pam_set_mixed_launch(void *context, int32_t mode, int32_t prefil
     });
 }
 
+PAM_API int32_t pam_set_fused_prefill_kernel(void *context, bool one_kernel) {
+    return guarded(context, [&](Context *ctx) { ctx->fused_one_kernel = one_kernel; });
+}
+
 PAM_API int32_t pam_set_decode_kernel(void *context, int32_t choice) {
     return guarded(context, [&](Context *ctx) {
         if (choice < 0 || choice > 2) throw invalid_configuration("decode kernel choice must be 0, 1 or 2");

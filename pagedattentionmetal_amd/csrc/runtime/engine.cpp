@@ -1073,7 +1073,7 @@ void Context::fused_prefill_gpu(const pam_fused_prefill_request &r) {
     PrefillPlan pl = plan_prefill(q);
     // the dense f16 kernel appends as it reads: one launch; other cases append
     // first, then attend
-    const bool one_kernel = pl.dense && l.data_type == kF16;
+    const bool one_kernel = fused_one_kernel && pl.dense && l.data_type == kF16;
     if (one_kernel) {
         pl.p.fuse_k = r.raw_k;
         pl.p.fuse_v = r.raw_v;

@@ -138,6 +138,9 @@ class Context {
     int32_t decode_kernel_choice = 0;
     // mixed step: 0 automatic, 1 separate launches, 2 one launch; its groups (0: automatic)
     int32_t mixed_launch_mode = 0, mixed_prefill_groups = 0, mixed_decode_groups = 0;
+    // fused prefill, f16 with d = 128: false appends then prefills (two launches,
+    // the faster on gfx950), true runs the one kernel that appends as it reads
+    bool fused_one_kernel = false;
     // HIP events around each call's kernels (the timings of last_stats); off
     // saves their queue packets between back-to-back launches
     bool gpu_timing = true;

@@ -195,8 +195,8 @@ def test_gpu_timing_switch(torch):
 def test_fused_prefill_equals_append_then_prefill(torch, dtype, H, hkv, d, bs, T, causal, window):
     """Pool bytes (and FP8 scales) equal a separate append; the output equals a
     separate prefill over that pool, bit for bit, and the oracle within tolerance.
-    (f16 with d = 128 runs as one kernel that reads the new keys from the inputs
-    and writes them into the pools; the other cases append, then attend.)"""
+    (f16 with d = 128 also runs as the one kernel that reads the new keys from
+    the inputs and writes them into the pools: same bytes and output.)"""
     from pagedattentionmetal_amd import PagedAttentionEngine, PagedLayerSpec
     eng = PagedAttentionEngine()
     eng.set_graceful_degradation(False)
@@ -225,6 +225,18 @@ def test_fused_prefill_equals_append_then_prefill(torch, dtype, H, hkv, d, bs, T
     kp, vp, ks, vs = pools[0]
     eng.fused_prefill(q, rk, rv, btd, kp, vp, out_f, T, layer, causal=causal, k_scale=ks, v_scale=vs)
     assert eng.last_stats["operation"] == 1  # reported as prefillSinglePass, as the reference does
+    if dtype == 1 and d == 128:
+        # the one-kernel form writes the same pool bytes and output
+        kp1, vp1 = torch.zeros_like(kp), torch.zeros_like(vp)
+        out_1 = torch.zeros_like(out_f)
+        eng.set_fused_prefill_one_kernel(True)
+        eng.fused_prefill(q, rk, rv, btd, kp1, vp1, out_1, T, layer, causal=causal)
+        eng.set_fused_prefill_one_kernel(False)
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host(kp1).view(np.uint8), to_host(kp).view(np.uint8))
+        assert np.array_equal(to_host(vp1).view(np.uint8), to_host(vp).view(np.uint8))
+        assert np.array_equal(to_host(out_1).view(np.uint8), to_host(out_f).view(np.uint8)), "one kernel != two"
+
     out_s = torch.zeros_like(out_f)
     kp2, vp2, ks2, vs2 = pools[1]
     eng.append_to_cache(rk, rv, kp2, vp2, btd, 0, T, layer, k_scale=ks2, v_scale=vs2)
