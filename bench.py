@@ -474,7 +474,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-next", action="store_true",
                     help="skip the next rows (fused prefill, backward, copy-on-write, adapter)")
-    ap.add_argument("--only", choices=("c1", "c2", "c3", "c4", "c5"),
+    ap.add_argument("--only", choices=("c1", "c2", "c3", "c4", "c5", "next"),
                     help="time one configuration alone and print its JSON object (for profiling it)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run the 1 GiB read and copy calibration streams (achievable HBM rate; "
@@ -504,6 +504,9 @@ def main():
             ec.calib_stream_copy(src, dst)
         del src, dst, ec
         torch.cuda.empty_cache()
+    if args.only == "next":
+        print(json.dumps({"next_rows": run_next_rows(torch, api, workloads, cpu=False)}), flush=True)
+        return
     if args.only == "c3":
         w3, e3, t3 = mixed_setup(torch, api, workloads)
         ms3, pk_ms = time_mixed(torch, e3, w3, t3, args.steps, args.warmup)
