@@ -307,18 +307,29 @@ __global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams 
     __syncthreads();  // bt_lds
     const int t0 = ws / 32, t1 = (T + 31) / 32, NT = t1 - t0, NI = 2 * NT;
     // iteration it reads key tile t0 + it % NT (both passes) from ring slot it % kBwdRing
+    // The lane's two tile rows (tile_dma's map) and 16-byte pieces, fixed for the
+    // kernel; per tile only the key, its block-table entry and one multiply-add
+    // remain.  Blocks are a power of two in tokens.
+    const int bsh = __builtin_ctz((unsigned)bs);
+    const int64_t row_stride = (int64_t)p.num_kv_heads * 128;  // halves per pool row
+    int dma_row[2], dma_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int blk = 2 * wave + i, R = 4 * blk + (lane >> 4);
+        dma_row[i] = R;
+        dma_off[i] = kvh * 128 + 8 * ((lane & 15) ^ (((R & 3) << 2) | ((R >> 2) & 3)));
+    }
     auto issue = [&](int it) {
         const int t = t0 + (it < NI ? it : NI - 1) % NT, slot = it % kBwdRing;
-        auto key_row = [&](const f16 *pool) {
-            return [&, pool](int R) {
-                int j = t * 32 + R;
-                j = j < ws ? ws : (j >= T ? T - 1 : j);  // finite rows outside the keys (masked)
-                const int64_t phys = bt_lds[j / bs - blk0];
-                return pool + ((phys * bs + j % bs) * p.num_kv_heads + kvh) * 128;
-            };
-        };
-        tile_dma(k_lds[slot], wave, lane, key_row(K));
-        tile_dma(v_lds[slot], wave, lane, key_row(V));
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            int j = t * 32 + dma_row[i];
+            j = j < ws ? ws : (j >= T ? T - 1 : j);  // finite rows outside the keys (masked)
+            const int64_t row = ((int64_t)bt_lds[(j >> bsh) - blk0] << bsh) | (j & (bs - 1));
+            const int64_t o = row * row_stride + dma_off[i];
+            lds_dma16(K + o, k_lds[slot] + 512 * (2 * wave + i));
+            lds_dma16(V + o, v_lds[slot] + 512 * (2 * wave + i));
+        }
     };
     const TrAddr ta = tr_addr(lane);
     bw_f32x16 dq[NB][4];
