@@ -406,7 +406,7 @@ int32_t pam_set_decode_kernel(void *context, int32_t choice);
 /* How pam_engine_mixed_step runs its attention: 1 the prefill chunks and the
  * decode rows as separate launches, 2 one launch holding both (when supported:
  * f16 or e4m3, d = 128, blocks of 16 tokens or more, G >= 4, at most 1024
- * decode rows), 0 automatic (the one launch where supported).
+ * decode rows), 0 automatic (separate launches, the faster on gfx950).
  * prefill_groups / decode_groups set the one launch's workgroups of each part
  * (0 = automatic: one per CU each). */
 int32_t pam_set_mixed_launch(void *context, int32_t mode, int32_t prefill_groups, int32_t decode_groups);

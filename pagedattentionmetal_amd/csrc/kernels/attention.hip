@@ -346,6 +346,7 @@ static hipError_t streamk_grid(int *grid) {
             e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_streamk<KV, HD, BLK, false>,
                                                              64 * kMfmaWaves, 0);
         if (e != hipSuccess) return e;
+        if (per_cu > MfmaShape<KV, HD>::GRID_PER_CU) per_cu = MfmaShape<KV, HD>::GRID_PER_CU;
         resident = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
     }
     *grid = resident;

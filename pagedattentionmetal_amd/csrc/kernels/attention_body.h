@@ -154,6 +154,10 @@ struct MfmaShape {
     // per CU for both f16 and e4m3; a third e4m3 workgroup forces spills)
     static constexpr int DEPTH = (sizeof(KV) == 2 && HD <= 128) ? 3 : 2;
     static constexpr int OCC = HD >= 256 ? 1 : (HD == 128 ? 2 : 3);
+    // stream-K workgroups launched per CU: f16 with d = 128 streams fastest with
+    // one (four waves per CU: c2 and c5 8-9% faster than with two, e4m3, whose
+    // dequantisation needs the second workgroup, 40% slower with one)
+    static constexpr int GRID_PER_CU = (sizeof(KV) == 2 && HD == 128) ? 1 : OCC;
     static constexpr int WT = 16 * (KL + VL);                 // halves of one wave's K and V tiles
     static constexpr int kSmemBytes = NW * WT * 2 > NW * 16 * HD * 4 ? NW * WT * 2 : NW * 16 * HD * 4;
     static_assert(64 % LPR == 0 && 16 % RPI == 0, "token rows must tile the wave");

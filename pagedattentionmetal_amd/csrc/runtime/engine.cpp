@@ -1306,11 +1306,12 @@ void Context::mixed_step(const pam_mixed_request &r) {
     pf.num_kv_heads = l.num_kv_heads;
     pf.window = W;
     pf.causal = 1;
-    // One launch for the chunks and the decode rows (mixed.hip): the prefill's
-    // workgroups first, the decode's after them; the automatic choice where it
-    // applies (measured within 2% of separate launches either way on c3).  The
-    // prefill is planned for every CU and the decode's resident grid follows it.
-    const bool one_launch = mixed_launch_mode != 1 && !chunks.empty() && ragged_rows > 0 && use_mfma &&
+    // One launch for the chunks and the decode rows (mixed.hip), on request: the
+    // prefill's workgroups first, the decode's after them.  The automatic choice
+    // is separate launches (c3 measured 1.6% faster that way with the decode's
+    // one-workgroup-per-CU grid).  The prefill is planned for every CU and the
+    // decode's grid follows it.
+    const bool one_launch = mixed_launch_mode == 2 && !chunks.empty() && ragged_rows > 0 && use_mfma &&
                             part_tokens_override == 0 &&
                             mixed_launch_supported(l.data_type, l.head_dim, G, bs, ragged_rows);
     const int32_t mix_pf_groups = mixed_prefill_groups > 0 ? mixed_prefill_groups : cus_;
