@@ -180,7 +180,8 @@ constexpr int kBwdWaves = 4;             // waves per workgroup, 32 rows / keys 
 constexpr float kBwdPScale = 256.0f;
 constexpr float kPScaleLog2 = 8.0f;  // log2(kBwdPScale)
 constexpr int kBwdRing = 4;                // LDS tiles per operand (kBwdRing - 1 loads in flight)
-constexpr int kBwdBtCache = 8192;          // block-table entries the dQ kernel keeps in LDS
+constexpr int kBwdBtCache = 8192;          // block-table entries the dQ kernel can keep in LDS
+constexpr int kBwdBtCacheSmall = 2048;     // ... in its two-workgroups-per-CU form
 
 // LDS tile of 32 rows x 128 halves; 16-byte piece p of row r sits at
 // p ^ (4 (r % 4) + (r / 4) % 4): 16 consecutive rows reading one piece
@@ -270,11 +271,15 @@ __device__ __forceinline__ void tile_dma(f16 *tile, int wave, int lane, F row_pt
     }
 }
 
-template <int NB>
-__global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams p, int group_shift) {
+// BT block-table entries in LDS: with kBwdBtCacheSmall two workgroups fit a CU
+// (registers and LDS), which measured 12% faster at T = 4096; longer tables take
+// the one-workgroup form.
+template <int NB, int BT>
+__global__ __launch_bounds__(64 * kBwdWaves, BT == kBwdBtCacheSmall ? 2 : 1) void bwd_dq_mfma(BackwardParams p,
+                                                                                              int group_shift) {
     __shared__ __attribute__((aligned(16))) f16 k_lds[kBwdRing][32 * 128];
     __shared__ __attribute__((aligned(16))) f16 v_lds[kBwdRing][32 * 128];
-    __shared__ int32_t bt_lds[kBwdBtCache];
+    __shared__ int32_t bt_lds[BT];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
     const int H = p.num_heads, G = 1 << group_shift, kvh = blockIdx.y;
     const int T = p.seq_len, ws = p.window_start, bs = p.block_size;
@@ -349,19 +354,10 @@ __global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams 
     }
 #pragma unroll
     for (int u = 0; u < kBwdRing - 1; u++) issue(u);
-    for (int it = 0; it < NI; it++) {
-        // this wave's loads of tile it are done (4 loads per tile), then every
-        // wave's, and every wave has finished iteration it - 1
-        ring_barrier<4 * (kBwdRing - 2)>();
-        issue(it + kBwdRing - 1);  // into the slot iteration it - 1 read
+    // scores and 2^8 P of iteration it's tile (P straight from the exponential, c - 8)
+    auto tile_probs = [&](int it, bw_f32x16 (&s)[NB], bw_f32x16 (&dp)[NB]) {
         const int t = t0 + it % NT, slot = it % kBwdRing;
-        const bool second = it >= NT;
-        if (it == NT) {  // pass 1 done: each row's D (the two lane halves hold different keys)
-#pragma unroll
-            for (int b = 0; b < NB; b++) D[b] = (dsum[b] + __shfl_xor(dsum[b], 32, 64)) * (1.0f / kBwdPScale);
-        }
         const f16 *kt = k_lds[slot], *vt = v_lds[slot];
-        bw_f32x16 s[NB], dp[NB];
 #pragma unroll
         for (int b = 0; b < NB; b++) s[b] = dp[b] = (bw_f32x16)0.0f;
 #pragma unroll
@@ -374,8 +370,6 @@ __global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams 
                 dp[b] = bw_mfma(va, gv[b][c], dp[b]);
             }
         }
-        const bool edge = t * 32 < ws || t * 32 + 32 > T;
-        // 2^8 P straight from the exponential (c - 8)
         auto probs = [&](auto edge) {
 #pragma unroll
             for (int b = 0; b < NB; b++)
@@ -389,33 +383,50 @@ __global__ __launch_bounds__(64 * kBwdWaves, 1) void bwd_dq_mfma(BackwardParams 
                     s[b][r2] = pr;
                 }
         };
-        if (edge)
+        if (t * 32 < ws || t * 32 + 32 > T)
             probs(std::true_type{});
         else
             probs(std::false_type{});
-        if (!second) {
+    };
+    // The two passes are two loops over the same ring (iterations 0 .. NT - 1,
+    // then NT .. 2 NT - 1): at each barrier this wave's loads of the iteration's
+    // tile are done (4 loads per tile), then every wave's, and every wave has
+    // finished the iteration before, whose slot then takes a new tile.
+    for (int it = 0; it < NT; it++) {  // pass 1: D
+        ring_barrier<4 * (kBwdRing - 2)>();
+        issue(it + kBwdRing - 1);
+        bw_f32x16 s[NB], dp[NB];
+        tile_probs(it, s, dp);
 #pragma unroll
-            for (int b = 0; b < NB; b++)
+        for (int b = 0; b < NB; b++)
 #pragma unroll
-                for (int r2 = 0; r2 < 16; r2++) dsum[b] = fmaf(s[b][r2], dp[b][r2], dsum[b]);
-        } else {
-            f16x8 db[NB][2];
+            for (int r2 = 0; r2 < 16; r2++) dsum[b] = fmaf(s[b][r2], dp[b][r2], dsum[b]);
+    }
+    // each row's D: the two lane halves hold different keys
 #pragma unroll
-            for (int b = 0; b < NB; b++) {
-                bw_f32x16 ds;
+    for (int b = 0; b < NB; b++) D[b] = (dsum[b] + __shfl_xor(dsum[b], 32, 64)) * (1.0f / kBwdPScale);
+    for (int it = NT; it < NI; it++) {  // pass 2: dQ^T += K^T dS^T
+        ring_barrier<4 * (kBwdRing - 2)>();
+        issue(it + kBwdRing - 1);
+        bw_f32x16 s[NB], dp[NB];
+        tile_probs(it, s, dp);
+        const f16 *kt = k_lds[it % kBwdRing];
+        f16x8 db[NB][2];
 #pragma unroll
-                for (int r2 = 0; r2 < 16; r2++) ds[r2] = s[b][r2] * (dp[b][r2] - D[b]);
-                to_chunks(ds, db[b]);
-            }
+        for (int b = 0; b < NB; b++) {
+            bw_f32x16 ds;
 #pragma unroll
-            for (int c = 0; c < 2; c++)
-#pragma unroll
-                for (int dt = 0; dt < 4; dt++) {
-                    const f16x8 kT = tr_operand(kt, ta, dt, c);
-#pragma unroll
-                    for (int b = 0; b < NB; b++) dq[b][dt] = bw_mfma(kT, db[b][c], dq[b][dt]);
-                }
+            for (int r2 = 0; r2 < 16; r2++) ds[r2] = s[b][r2] * (dp[b][r2] - D[b]);
+            to_chunks(ds, db[b]);
         }
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const f16x8 kT = tr_operand(kt, ta, dt, c);
+#pragma unroll
+                for (int b = 0; b < NB; b++) dq[b][dt] = bw_mfma(kT, db[b][c], dq[b][dt]);
+            }
     }
     ring_barrier<0>();  // the loads issued past the last tile
     const float f = p.scale / kBwdPScale;
@@ -601,8 +612,11 @@ hipError_t launch_backward(const BackwardParams &p, int32_t dtype, hipStream_t s
         const int64_t qrows = (int64_t)p.seq_len * G;
         const int64_t nkeys = p.seq_len - p.window_start;
         const int per = 32 * kBwdWaves * kBwdNB, gs = __builtin_ctz((unsigned)G);
-        hipLaunchKernelGGL(bwd_dq_mfma<kBwdNB>, dim3((unsigned)((qrows + per - 1) / per), p.num_kv_heads),
-                           dim3(64 * kBwdWaves), 0, stream, p, gs);
+        const dim3 dq_grid((unsigned)((qrows + per - 1) / per), p.num_kv_heads);
+        if (nblk <= kBwdBtCacheSmall)
+            hipLaunchKernelGGL((bwd_dq_mfma<kBwdNB, kBwdBtCacheSmall>), dq_grid, dim3(64 * kBwdWaves), 0, stream, p, gs);
+        else
+            hipLaunchKernelGGL((bwd_dq_mfma<kBwdNB, kBwdBtCache>), dq_grid, dim3(64 * kBwdWaves), 0, stream, p, gs);
         if (nkeys > 0)
             hipLaunchKernelGGL(bwd_dkv_mfma<kBwdNB>, dim3((unsigned)((nkeys + per - 1) / per), p.num_kv_heads),
                                dim3(64 * kBwdWaves), 0, stream, p, gs);

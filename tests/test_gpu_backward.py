@@ -26,6 +26,7 @@ pytestmark = pytest.mark.gpu
     (1, 257, 8, 8, 128, 32, 100),
     (1, 131, 16, 2, 128, 16, 0),
     (1, 96, 64, 8, 128, 16, 45),
+    (1, 2100, 4, 4, 128, 1, 0),    # 2100 one-token blocks: the dQ kernel's large block-table form
 ])
 def test_backward_parity(dtype, T, H, hkv, d, bs, W):
     import torch
