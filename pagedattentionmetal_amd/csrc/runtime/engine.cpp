@@ -57,6 +57,22 @@ static int64_t kv_bytes_per_token(const pam_layer_spec &l) {
 static int64_t pool_bytes_for(int64_t blocks, const pam_layer_spec &l) { return blocks * l.block_size * kv_bytes_per_token(l); }
 static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// The prefill regime lastStats.operation names, by the reference's rule
+// (PagedAttentionEngine.swift:420-433, 436-438, 512-516, 1952-1958): MMA for f16
+// with headDim a multiple of 64 up to 256, else flash for f16/f32 up to headDim
+// 64, else the tiled pass when its single-pass form would not fit a threadgroup
+// (blockSize * headDim * 12 bytes over 32 KiB, or blockSize * headDim threads
+// over 1024 - Apple GPU limits, kept so the same call reports the same regime)
+// or seqLen exceeds splitThreshold, else the single pass.  The kernels that run
+// here are chosen separately; usedSplitPass says whether the work was split.
+int32_t Context::prefill_operation(const pam_layer_spec &l, int32_t seq_len) const {
+    if (l.data_type == kF16 && l.head_dim <= 256 && l.head_dim % 64 == 0) return PAM_OP_PREFILL_MMA;
+    if (l.data_type != kFP8 && l.head_dim <= 64) return PAM_OP_PREFILL_FLASH;
+    const int64_t cells = (int64_t)l.block_size * l.head_dim;
+    if (cells * 12 > 32768 || cells > 1024 || seq_len > split_threshold) return PAM_OP_PREFILL_TILED_PASS;
+    return PAM_OP_PREFILL_SINGLE_PASS;
+}
+
 // ------------------------------------------------------------------ context
 
 Context::Context() {}
@@ -794,7 +810,8 @@ void Context::prefill_layers(const pam_prefill_layers_request &r) {
             mark(ev1_);
             finish("prefillLayers");
         });
-        record_stats(PAM_OP_PREFILL_MMA, 1, r.seq_len, (int32_t)ceil_div(r.seq_len, reqs[0].layer.block_size), tmp,
+        record_stats(prefill_operation(reqs[0].layer, r.seq_len), 1, r.seq_len,
+                     (int32_t)ceil_div(r.seq_len, reqs[0].layer.block_size), tmp,
                      split, false);
     };
     if (graceful_degradation) {
@@ -1010,7 +1027,7 @@ void Context::prefill_gpu(const pam_prefill_request &r) {
         mark(ev1_);
         finish("prefill");
     });
-    const int32_t op = (pl.dense || pl.use_mfma) ? PAM_OP_PREFILL_MMA : PAM_OP_PREFILL_TILED_PASS;
+    const int32_t op = prefill_operation(l, r.seq_len);
     // split: the dense kernel cut items into pieces merged in the kernel, or the
     // row kernels used split-context partitions
     const bool split = pl.dense ? pl.p.pf_part != nullptr : (pl.p.max_parts > 1 || pl.p.seg_count != nullptr);

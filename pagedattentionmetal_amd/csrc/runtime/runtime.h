@@ -210,6 +210,7 @@ class Context {
     };
     DensePlan plan_dense_prefill(AttnParams &p, const int4 *chunks, int32_t n, StageList &sl, int32_t groups = 0);
     static void bind_dense_prefill(AttnParams &p, const DensePlan &d, const char *base);
+    int32_t prefill_operation(const pam_layer_spec &l, int32_t seq_len) const;
     void record_stats(int32_t op, int32_t batch, int32_t seq_len, int32_t blocks, int64_t tmp, bool split,
                       bool has_mid);
 
