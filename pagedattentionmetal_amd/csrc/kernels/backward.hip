@@ -247,8 +247,9 @@ __device__ __forceinline__ void lds_dma4(const void *g, const void *lds_base) {
 }
 
 // Workgroup barrier for the LDS rings: this wave's LDS reads and all but its
-// last `N` loads are complete, then every wave arrives.  No fence: a
-// __syncthreads would wait for every load in flight (the ring's prefetch).
+// last `N` loads are complete, then every wave arrives.  A __syncthreads would
+// not do: the compiler does not count the inline-assembly loads, so it emits
+// no wait for them.
 template <int N>
 __device__ __forceinline__ void ring_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
