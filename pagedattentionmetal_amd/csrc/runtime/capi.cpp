@@ -715,22 +715,39 @@ PAM_API int32_t pam_synth_normal(void *context, void *dst, int32_t dtype, uint64
     });
 }
 
+// Two events around work on `stream`; both are released however the caller
+// leaves (a failed create or record throws).
+struct TimedSpan {
+    hipEvent_t a = nullptr, b = nullptr;
+    hipStream_t stream;
+    explicit TimedSpan(hipStream_t s) : stream(s) {
+        hip_check(hipEventCreate(&a), "hipEventCreate");
+        hip_check(hipEventCreate(&b), "hipEventCreate");
+        hip_check(hipEventRecord(a, stream), "hipEventRecord");
+    }
+    // milliseconds from the first event to now on the stream (-1 if not measurable)
+    float end() {
+        float t = -1.0f;
+        if (hipEventRecord(b, stream) == hipSuccess && hipEventSynchronize(b) == hipSuccess)
+            (void)hipEventElapsedTime(&t, a, b);
+        return t;
+    }
+    ~TimedSpan() {
+        if (a) (void)hipEventDestroy(a);
+        if (b) (void)hipEventDestroy(b);
+    }
+    TimedSpan(const TimedSpan &) = delete;
+    TimedSpan &operator=(const TimedSpan &) = delete;
+};
+
 PAM_API int32_t pam_calib_stream_read(void *context, const void *src, size_t bytes, int32_t blocks, float *ms) {
     return guarded(context, [&](Context *ctx) {
         ctx->ensure_device();
         const int32_t nb = calib_blocks(blocks);
         uint32_t *sink = static_cast<uint32_t *>(ctx->device_scratch(5, (size_t)nb * 4));
-        hipEvent_t a, b;
-        hip_check(hipEventCreate(&a), "hipEventCreate");
-        hip_check(hipEventCreate(&b), "hipEventCreate");
-        hip_check(hipEventRecord(a, ctx->stream()), "hipEventRecord");
-        hipError_t e = launch_stream_read(src, bytes, sink, nb, ctx->stream());
-        (void)hipEventRecord(b, ctx->stream());
-        (void)hipEventSynchronize(b);
-        float t = -1.0f;
-        (void)hipEventElapsedTime(&t, a, b);
-        (void)hipEventDestroy(a);
-        (void)hipEventDestroy(b);
+        TimedSpan span(ctx->stream());
+        const hipError_t e = launch_stream_read(src, bytes, sink, nb, ctx->stream());
+        const float t = span.end();
         hip_check(e, "stream read");
         if (ms) *ms = t;
     });
@@ -741,17 +758,9 @@ PAM_API int32_t pam_calib_stream_copy(void *context, const void *src, void *dst,
     return guarded(context, [&](Context *ctx) {
         ctx->ensure_device();
         const int32_t nb = calib_blocks(blocks);
-        hipEvent_t a, b;
-        hip_check(hipEventCreate(&a), "hipEventCreate");
-        hip_check(hipEventCreate(&b), "hipEventCreate");
-        hip_check(hipEventRecord(a, ctx->stream()), "hipEventRecord");
-        hipError_t e = launch_stream_copy(src, dst, bytes, nb, ctx->stream());
-        (void)hipEventRecord(b, ctx->stream());
-        (void)hipEventSynchronize(b);
-        float t = -1.0f;
-        (void)hipEventElapsedTime(&t, a, b);
-        (void)hipEventDestroy(a);
-        (void)hipEventDestroy(b);
+        TimedSpan span(ctx->stream());
+        const hipError_t e = launch_stream_copy(src, dst, bytes, nb, ctx->stream());
+        const float t = span.end();
         hip_check(e, "stream copy");
         if (ms) *ms = t;
     });

@@ -288,3 +288,16 @@ def test_stream_switch_orders_work(torch):
         eng.set_stream(None)
     for (out, _), case in zip(outs, cases):
         assert row_rel_err(to_host(out), case[5]) <= TOL[1]
+
+
+def test_calibration_streams(torch):
+    """pam_calib_stream_read / pam_calib_stream_copy: each times its stream with
+    HIP events (a positive time), and the copy leaves an exact copy."""
+    from pagedattentionmetal_amd import PagedAttentionEngine
+    eng = PagedAttentionEngine()
+    src = torch.randint(-2**31, 2**31 - 1, (16 << 20,), dtype=torch.int32, device="cuda")
+    dst = torch.zeros_like(src)
+    assert eng.calib_stream_read(src) > 0
+    assert eng.calib_stream_copy(src, dst) > 0
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
