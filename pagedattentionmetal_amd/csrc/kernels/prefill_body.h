@@ -366,9 +366,12 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
             // MFMAs while they arrive.
             f16x8 ka[KH][DC];
             uint32_t nslot[KPT];
-            auto vphase = [&](int t, Regs &r) {
+            // `slot` = t % NBUF as a compile-time constant (std::integral_constant):
+            // the ring buffers' LDS offsets then need no per-phase arithmetic
+            auto vphase = [&](int t, auto slot, Regs &r) {
+                constexpr int S = decltype(slot)::value;
                 if (t + 1 < T) {
-                    const f16 *kt = k_lds[(t + 1) % NBUF];
+                    const f16 *kt = k_lds[(S + 1) % NBUF];
 #pragma unroll
                     for (int e = 0; e < KH; e++)
 #pragma unroll
@@ -403,10 +406,11 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                     for (int c = 0; c < 2 * KH; c++) asm volatile("" : "+v"(pb[b][c]));
                     asm volatile("" : "+v"(l_run[b]));
                 }
-                stage((t + 2) % NBUF, r);  // tile t + 2, fetched at M_t-2
+                stage((S + 2) % NBUF, r);  // tile t + 2, fetched at M_t-2
             };
-            auto mphase = [&](int t, Regs &r) {
-                const f16 *vt = v_lds[t % NBUF];
+            auto mphase = [&](int t, auto slot, Regs &r) {
+                constexpr int S = decltype(slot)::value;
+                const f16 *vt = v_lds[S];
                 f16x8 va[2 * KH][DT];
 #pragma unroll
                 for (int c = 0; c < 2 * KH; c++)
@@ -447,14 +451,37 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                 }
                 load(nslot, r);  // tile t + 4
             };
-            for (int t = 0; t < T; t += 2) {
-                vphase(t, ra);
+            using S0 = std::integral_constant<int, 0>;
+            using S1 = std::integral_constant<int, 1>;
+            using S2 = std::integral_constant<int, 2>;
+            using S3 = std::integral_constant<int, 3>;
+            int t = 0;
+            for (; t + 4 <= T; t += 4) {  // four tiles: one turn of the ring
+                vphase(t, S0{}, ra);
                 __syncthreads();
-                mphase(t, ra);
+                mphase(t, S0{}, ra);
                 __syncthreads();
-                vphase(t + 1, rb);
+                vphase(t + 1, S1{}, rb);
                 __syncthreads();
-                mphase(t + 1, rb);
+                mphase(t + 1, S1{}, rb);
+                __syncthreads();
+                vphase(t + 2, S2{}, ra);
+                __syncthreads();
+                mphase(t + 2, S2{}, ra);
+                __syncthreads();
+                vphase(t + 3, S3{}, rb);
+                __syncthreads();
+                mphase(t + 3, S3{}, rb);
+                __syncthreads();
+            }
+            if (t < T) {  // T is even: two tiles left, starting at slot 0
+                vphase(t, S0{}, ra);
+                __syncthreads();
+                mphase(t, S0{}, ra);
+                __syncthreads();
+                vphase(t + 1, S1{}, rb);
+                __syncthreads();
+                mphase(t + 1, S1{}, rb);
                 __syncthreads();
             }
             if (!lag) __syncthreads();
