@@ -157,6 +157,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
         };
         Regs ra, rb;
         int blk0 = 0;  // first block of the block-table segment held in bt_lds
+        const int32_t *bt_seg = bt_lds;  // bt_lds - blk0: indexed by logical block
         // pool row of this thread's key(s) of a tile, then the loads from it
         auto lookup = [&](int tile, uint32_t(&slot)[KPT]) {
 #pragma unroll
@@ -164,17 +165,27 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                 int j = tile * KT + my_key + i * KEYS_PER_PASS;
                 // keys outside [ws, kv_len) read the nearest key inside instead: finite
                 // data whose probability is zero after masking (and a block-table entry
-                // of the current segment)
-                j = j < ws ? ws : (j >= kv_len ? kv_len - 1 : j);
-                slot[i] = ((uint32_t)bt_lds[(j >> bsh) - blk0] << bsh) | (uint32_t)(j & bsm);
+                // of the current segment); ws < kv_len
+                j = min(max(j, ws), kv_len - 1);
+                slot[i] = ((uint32_t)bt_seg[(uint32_t)j >> bsh] << bsh) | ((uint32_t)j & bsm);
                 // fused append: a new token's row of the inputs (top bit set)
                 if (FUSED && j >= ch.y) slot[i] = 0x80000000u | (uint32_t)(ch.w + j - ch.y);
             }
         };
+        // the V pool's distance from the K pool (bytes): one multiply-add gives a
+        // row's K address, one add its V address
+        const int64_t kv_gap = (const char *)vpool - (const char *)kpool;
+        const uint64_t row_bytes = (uint64_t)row_stride * sizeof(KV);
         auto load = [&](const uint32_t(&slot)[KPT], Regs &r) {
 #pragma unroll
             for (int i = 0; i < KPT; i++) {
                 const uint32_t row = slot[i] & 0x7FFFFFFFu;
+                if constexpr (!FP8 && !FUSED) {
+                    const char *ka = (const char *)kpool + (uint64_t)row * row_bytes;
+                    r.k[i] = *reinterpret_cast<const f16x8 *>(ka);
+                    r.v[i] = *reinterpret_cast<const f16x8 *>(ka + kv_gap);
+                    continue;
+                }
                 const uint64_t off = (uint64_t)row * row_stride;
                 if constexpr (FP8) {
                     r.k[i] = *reinterpret_cast<const uint2 *>(kpool + off);
@@ -246,11 +257,14 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                 v_rd[dt] = v_lds_at(row, 4 * dt + 2 * hh + ((o & 3) >> 1)) + 4 * (o & 1);
         }
 
-        float m_use[RB], l_run[RB], lmax[RB];
+        // lmax: the tile's raw row max (score units); m_thr: the score above which
+        // the reference max must move, (m_use + kRescaleLog2) / scale_log2
+        float m_use[RB], l_run[RB], lmax[RB], m_thr[RB];
         f32x16 o[RB][DT];
 #pragma unroll
         for (int b = 0; b < RB; b++) {
             m_use[b] = -INFINITY;
+            m_thr[b] = -INFINITY;
             l_run[b] = 0.0f;
             lmax[b] = -INFINITY;
 #pragma unroll
@@ -281,8 +295,8 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
 #pragma unroll
                     for (int r2 = 2; r2 < 16; r2 += 2) mx = vmax3(mx, sc[b][e][r2], sc[b][e][r2 + 1]);
                 }
-                lmax[b] = mx * sl2;
-                need |= lmax[b] > m_use[b] + kRescaleLog2;
+                lmax[b] = mx;
+                need |= mx > m_thr[b];
             }
             return need;
         };
@@ -290,13 +304,14 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
         auto rescale = [&]() {
 #pragma unroll
             for (int b = 0; b < RB; b++) {
-                const float mt = fmaxf(lmax[b], shfl_xor(lmax[b], 32));
+                const float mt = fmaxf(lmax[b], shfl_xor(lmax[b], 32)) * sl2;
                 const float m_new = fmaxf(m_use[b], mt);
                 const float corr = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use[b] - m_new);
                 l_run[b] *= corr;
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++) o[b][dt] *= corr;
                 m_use[b] = m_new;
+                m_thr[b] = (m_new + kRescaleLog2) / sl2;
             }
         };
 
@@ -324,6 +339,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
             const int seg_end = min(t_hi, seg + seg_tiles);
             const int T = (seg_end - seg + 1) & ~1;
             blk0 = (seg * KT) >> bsh;
+            bt_seg = bt_lds - blk0;
             const int nblk = (((min(seg_end * KT, kv_len) - 1) >> bsh) - blk0) + 1;
             __syncthreads();  // previous segment done with bt_lds and the ring
             int i0 = tid;
