@@ -386,6 +386,11 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
             // the ring buffers' LDS offsets then need no per-phase arithmetic
             auto vphase = [&](int t, auto slot, Regs &r) {
                 constexpr int S = decltype(slot)::value;
+                // the LDS staging of tile t + 2 (fetched at M_t-2) goes first: its
+                // writes then overlap the rest of the phase (measured 2% faster
+                // than staging last)
+                stage((S + 2) % NBUF, r);
+                __builtin_amdgcn_sched_barrier(0);
                 if (t + 1 < T) {
                     const f16 *kt = k_lds[(S + 1) % NBUF];
 #pragma unroll
@@ -422,7 +427,6 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                     for (int c = 0; c < 2 * KH; c++) asm volatile("" : "+v"(pb[b][c]));
                     asm volatile("" : "+v"(l_run[b]));
                 }
-                stage((S + 2) % NBUF, r);  // tile t + 2, fetched at M_t-2
             };
             auto mphase = [&](int t, auto slot, Regs &r) {
                 constexpr int S = decltype(slot)::value;
