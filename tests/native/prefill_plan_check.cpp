@@ -80,7 +80,7 @@ static int check(const std::vector<int4> &ch, int H, int Hkv, int W, int causal,
 
 int main() {
     std::mt19937 rng(5);
-    int failures = 0, split_plans = 0;
+    int failures = 0, split_plans = 0, multi_plans = 0;
     for (int trial = 0; trial < 3000; trial++) {
         const int n = 1 + rng() % 10, Hkv = 1 << (rng() % 4), G = 1 << (rng() % 4);
         std::vector<int4> ch;
@@ -106,7 +106,11 @@ int main() {
         PrefillSplit ps;
         prefill_split_plan(ch.data(), (int)ch.size(), p, groups, ps);
         split_plans += ps.slots > 0;
+        bool several = false;
+        for (const int2 &r : ps.range) several |= r.y - r.x > 1;
+        multi_plans += ps.slots == 0 && several;  // static grid, or a balanced split that cut nothing
     }
-    std::printf("%d failures, %d of 3000 plans split items\n", failures, split_plans);
+    std::printf("%d failures, %d of 3000 plans split items, %d run several whole items per workgroup\n", failures,
+                split_plans, multi_plans);
     return failures ? 1 : 0;
 }

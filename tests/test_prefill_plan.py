@@ -21,6 +21,8 @@ def test_prefill_work_list_invariants(tmp_path):
     assert r.returncode == 0, r.stderr[-2000:]
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout[-2000:]
-    # the random set must exercise both schedules
+    # the random set must exercise every schedule
     split = int(r.stdout.split(" of 3000")[0].split()[-1])
+    multi = int(r.stdout.split(" run several")[0].split()[-1])
     assert 0 < split < 3000, r.stdout
+    assert 0 < multi < 3000 - split, r.stdout
