@@ -54,8 +54,13 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
     constexpr int KPT = KT / KEYS_PER_PASS;          // keys per thread per tile
     constexpr int ROWS = 32 * RB * kPrefillWaves;
     static_assert(KT % KEYS_PER_PASS == 0 && KPT <= 2, "whole keys per thread");
-    __shared__ __attribute__((aligned(16))) f16 k_lds[kPrefillBufs][KT * kPrefillKL];
-    __shared__ __attribute__((aligned(16))) f16 v_lds[kPrefillBufs][KT * kPrefillVL];
+    // the K and V rings in one array: after a segment's tile loop the whole of
+    // it holds the waves' output rows on their way to memory (finish, below)
+    constexpr int kRingK = kPrefillBufs * KT * kPrefillKL, kRingV = kPrefillBufs * KT * kPrefillVL;
+    __shared__ __attribute__((aligned(16))) f16 ring_lds[kRingK + kRingV];
+    f16(*k_lds)[KT * kPrefillKL] = reinterpret_cast<f16(*)[KT * kPrefillKL]>(ring_lds);
+    f16(*v_lds)[KT * kPrefillVL] = reinterpret_cast<f16(*)[KT * kPrefillVL]>(ring_lds + kRingK);
+    static_assert(RB == 1 && kPrefillWaves * 32 * HD <= kRingK + kRingV, "one 32-row output tile per wave in the ring");
     __shared__ int32_t bt_lds[kBtCache];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
@@ -572,23 +577,42 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
             }
         }
 
-        // finish: l summed over the two lane halves, O / l, rows in range only
-#pragma unroll
-        for (int b = 0; b < RB; b++) {
-            const float l = l_run[b] + shfl_xor(l_run[b], 32);
-            if (!row_ok[b]) continue;
-            // no key in range (window past the row): 0/0, as the reference's m/l bookkeeping gives
+        // finish: O / l (l summed over the two lane halves) into the wave's
+        // 32-row slice of the ring, idle since every wave left the tile loop
+        // (the barrier after it), then out as whole rows: 16 lanes store one
+        // 256-byte row with 16-byte stores, where the accumulator layout would
+        // have each store instruction touch 32 rows.  Row r's 16-byte piece p
+        // sits at p ^ (r % 16), so neither side's LDS accesses conflict.
+        // A row with no key in range (window past the row) is 0/0, as the
+        // reference's m/l bookkeeping gives.
+        {
+            // the lane's row and piece indices pass through an empty asm so the
+            // compiler cannot compute this block's addresses ahead of the tile
+            // loop (they would hold registers through it)
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int on = ln & 31, oh = ln >> 5;
+            f16 *ot = ring_lds + wave * 32 * HD;
+            const float l = l_run[0] + shfl_xor(l_run[0], 32);
             const float inv = 1.0f / l;
-            f16 *op = static_cast<f16 *>(p.out) + ((int64_t)(ch.w + my_tok[b]) * H + kvh * G + my_head[b]) * HD + 4 * h;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     f16x4 v;
 #pragma unroll
-                    for (int r2 = 0; r2 < 4; r2++) v[r2] = (f16)(o[b][dt][4 * q + r2] * inv);
-                    *reinterpret_cast<f16x4 *>(op + 32 * dt + 8 * q) = v;
+                    for (int r2 = 0; r2 < 4; r2++) v[r2] = (f16)(o[0][dt][4 * q + r2] * inv);
+                    *reinterpret_cast<f16x4 *>(ot + on * HD + (((4 * dt + q) ^ (on & 15)) << 3) + 4 * oh) = v;
                 }
+#pragma unroll
+            for (int i = 0; i < 32 / 4; i++) {
+                const int rl = 4 * i + (ln >> 4), pc = ln & 15;
+                const f16x8 v = *reinterpret_cast<const f16x8 *>(ot + rl * HD + ((pc ^ (rl & 15)) << 3));
+                const int rr = wave * 32 + rl, tk = tok0 + rr / G;
+                if (tk < tok_end)
+                    *reinterpret_cast<f16x8 *>(static_cast<f16 *>(p.out) +
+                                               ((int64_t)(ch.w + tk) * H + kvh * G + rr % G) * HD + 8 * pc) = v;
+            }
         }
     }
 }
