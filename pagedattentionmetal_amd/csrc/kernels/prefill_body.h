@@ -80,7 +80,13 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
         nx_wb = p.pf_work[3 * rg.x + 2];
     }
     int32_t pre_bt = 0;    // a block-table entry of the next segment, loaded ahead
+    int pre_nb = 0;        // how many of them the next segment's first block-table part holds
     bool pre_ok = false;
+    // Workgroup barrier for LDS only: this wave's LDS accesses are complete, then
+    // every wave arrives.  A __syncthreads at an item's start would also wait for
+    // the wave's outstanding global accesses (the item's Q loads, the last item's
+    // output stores), which the LDS it protects does not depend on.
+    auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
     for (int sgi = rg.x; sgi < rg.y; sgi++) {
         const bool use_pre = pre_ok;
         pre_ok = false;
@@ -346,14 +352,11 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
             blk0 = (seg * KT) >> bsh;
             bt_seg = bt_lds - blk0;
             const int nblk = (((min(seg_end * KT, kv_len) - 1) >> bsh) - blk0) + 1;
-            __syncthreads();  // previous segment done with bt_lds and the ring
-            int i0 = tid;
-            if (seg == t_lo && use_pre) {  // entries loaded during the previous segment
-                if (tid < nblk) bt_lds[tid] = pre_bt;
-                i0 += THREADS;
-            }
+            lds_barrier();  // previous segment done with bt_lds and the ring
+            // entries loaded during the previous item are in bt_lds already
+            const int i0 = tid + (seg == t_lo && use_pre ? THREADS : 0);
             for (int i = i0; i < nblk; i += THREADS) bt_lds[i] = bt[blk0 + i];
-            __syncthreads();
+            lds_barrier();
             // the first four tiles are requested together
             {
                 Regs rc, rd;
@@ -366,10 +369,10 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                 ra = rc;
                 rb = rd;
             }
-            __syncthreads();
-            if (lag) __syncthreads();
+            lds_barrier();
+            if (lag) lds_barrier();
             score(0, sacc);  // M_-1
-            __syncthreads();
+            lds_barrier();
             // request the first block-table entries of the workgroup's next segment
             // (its descriptors arrived long ago); they are stored at its start
             if (seg == t_lo && sgi + 1 < rg.y) {
@@ -378,6 +381,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                 const int b0 = (tlo_n * KT) >> bsh;
                 const int nb = send > tlo_n ? (((min(send * KT, kvn) - 1) >> bsh) - b0) + 1 : 0;
                 if (tid < nb) pre_bt = p.block_tables[(int64_t)nx_ch.x * p.bt_stride + b0 + tid];
+                pre_nb = nb;
                 pre_ok = true;
             }
 
@@ -509,8 +513,12 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                 mphase(t + 1, S1{}, rb);
                 __syncthreads();
             }
-            if (!lag) __syncthreads();
+            if (!lag) lds_barrier();
         }
+        // every wave has left the item's tile loop: the next item's first
+        // block-table entries go into bt_lds now, with nothing of the next item
+        // in flight yet
+        if (pre_ok && tid < pre_nb) bt_lds[tid] = pre_bt;
 
         // A piece of a split item publishes its state (O^T, reference max and row
         // sums, per lane) in its slot with write-through stores and counts it;
