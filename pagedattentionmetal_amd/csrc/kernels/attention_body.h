@@ -345,6 +345,10 @@ __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, 
         // LDS ops of one wave execute in order; the wave barrier pins the compiler's
         __builtin_amdgcn_wave_barrier();
         load_tile(tile + S::DEPTH, t);
+        // e4m3: the scores, softmax and PV run at raised wave priority, ahead
+        // of the other waves' dequantising (c4 1% faster; f16 measured 0.9%
+        // slower with it)
+        if constexpr (kFp8) __builtin_amdgcn_s_setprio(1);
 
         // S^T[token][head] over HD dims: K row `row`, dims 32i + 8g .. +8
         f32x4 s = (f32x4)0.0f;
@@ -393,6 +397,7 @@ __device__ __forceinline__ void mfma_core(const AttnParams &p, const RowCtx &c, 
 #pragma unroll
         for (int i = 0; i < NO; i++)
             o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(lds_read_tr16(vrow + 16 * i), pb, o[i], 0, 0, 0);
+        if constexpr (kFp8) __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_wave_barrier();
     };
 
