@@ -72,13 +72,24 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
     const int2 rg = p.pf_range[blockIdx.x];
     __shared__ int32_t merge_flag;
     const int bsh = __builtin_ctz(p.block_size), bsm = p.block_size - 1;  // block_size is a power of two
-    // descriptors of the next segment are requested while this one runs
+    // descriptors of the next segment are requested while this one runs.  They
+    // are uniform, but loaded through an offset the compiler cannot see is zero
+    // so that they stay in vector registers until the next segment reads them
+    // into scalars: loaded as uniform values they would be moved to scalar
+    // registers, and waited for, right after the load.
+    int vzero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+    const int4 *work = p.pf_work + vzero;
     int4 nx_ch = make_int4(0, 0, 0, 0), nx_wa = nx_ch, nx_wb = nx_ch;
     if (rg.x < rg.y) {
-        nx_ch = p.pf_work[3 * rg.x];
-        nx_wa = p.pf_work[3 * rg.x + 1];
-        nx_wb = p.pf_work[3 * rg.x + 2];
+        nx_ch = work[3 * rg.x];
+        nx_wa = work[3 * rg.x + 1];
+        nx_wb = work[3 * rg.x + 2];
     }
+    auto uniform4 = [](const int4 v) {
+        return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                         __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+    };
     int32_t pre_bt = 0;    // a block-table entry of the next segment, loaded ahead
     int pre_nb = 0;        // how many of them the next segment's first block-table part holds
     bool pre_ok = false;
@@ -90,13 +101,13 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
     for (int sgi = rg.x; sgi < rg.y; sgi++) {
         const bool use_pre = pre_ok;
         pre_ok = false;
-        const int4 ch = nx_ch;  // {bt_row, q_offset, len, row_base}
-        const int4 wa = nx_wa;  // {kv head, first token, t_lo, t_hi}
-        const int4 wb = nx_wb;  // {slot0, piece, pieces, 0}
+        const int4 ch = uniform4(nx_ch);  // {bt_row, q_offset, len, row_base}
+        const int4 wa = uniform4(nx_wa);  // {kv head, first token, t_lo, t_hi}
+        const int4 wb = uniform4(nx_wb);  // {slot0, piece, pieces, 0}
         if (sgi + 1 < rg.y) {
-            nx_ch = p.pf_work[3 * sgi + 3];
-            nx_wa = p.pf_work[3 * sgi + 4];
-            nx_wb = p.pf_work[3 * sgi + 5];
+            nx_ch = work[3 * sgi + 3];
+            nx_wa = work[3 * sgi + 4];
+            nx_wb = work[3 * sgi + 5];
         }
         const int kvh = wa.x, tok0 = wa.y;
         const int32_t *bt = p.block_tables + (int64_t)ch.x * p.bt_stride;
@@ -376,11 +387,12 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
             // request the first block-table entries of the workgroup's next segment
             // (its descriptors arrived long ago); they are stored at its start
             if (seg == t_lo && sgi + 1 < rg.y) {
-                const int kvn = nx_ch.y + nx_ch.z, tlo_n = nx_wa.z;
-                const int send = min(nx_wa.w, tlo_n + seg_tiles);
+                const int4 nch = uniform4(nx_ch), nwa = uniform4(nx_wa);
+                const int kvn = nch.y + nch.z, tlo_n = nwa.z;
+                const int send = min(nwa.w, tlo_n + seg_tiles);
                 const int b0 = (tlo_n * KT) >> bsh;
                 const int nb = send > tlo_n ? (((min(send * KT, kvn) - 1) >> bsh) - b0) + 1 : 0;
-                if (tid < nb) pre_bt = p.block_tables[(int64_t)nx_ch.x * p.bt_stride + b0 + tid];
+                if (tid < nb) pre_bt = p.block_tables[(int64_t)nch.x * p.bt_stride + b0 + tid];
                 pre_nb = nb;
                 pre_ok = true;
             }
