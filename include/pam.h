@@ -471,14 +471,15 @@ int32_t pam_module_launch(void *context, void *function, uint32_t grid_x, uint32
 const char *pam_module_default_path(void);
 
 /* Allocation-free decode.  No counterpart in the reference: it is for callers
- * that cannot allocate device memory (code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc).  pam_engine_decode_noalloc
+ * that cannot allocate device memory (tight serving loops, harnesses that
+ * forbid hipMalloc).  Not for HIP graph capture: the host picks each launch's
+ * merge-counter epoch, which a replayed graph would repeat.  pam_engine_decode_noalloc
  * takes the same request and gives the same results as pam_engine_decode, but
  * its kernels keep their split-context partials, merge counters and zero page
  * in one fixed per-GPU array of the library (32 MiB, held until the process
  * ends) and it calls no hipMalloc / hipFree; a request whose workspace does not
  * fit (stream-K partials above 31 MiB - 4 KiB, or more than 131072 merge
- * counters) fails with an error.  Every call on one GPU shares that array:
+ * counters) fails with an error, also under graceful degradation.  Every call on one GPU shares that array:
  * calls that overlap on one GPU (other contexts or streams) race.
  * pam_engine_setup_noalloc prepares the context and the array (it may
  * allocate; call it once, outside the no-allocation region). */

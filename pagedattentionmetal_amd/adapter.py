@@ -67,6 +67,7 @@ class PagedTorchKVCache:
     def __init__(self, sequence_id: int, layer: PagedLayerSpec, max_blocks: int,
                  engine: api.PagedAttentionEngine | None = None):
         layer.validate()
+        owns = engine is None
         if engine is None:
             # its own engine enqueues on the caller's current torch stream and
             # returns at once: the outputs are ordered after the inputs by the stream
@@ -74,6 +75,8 @@ class PagedTorchKVCache:
             engine = api.PagedAttentionEngine()
             engine.set_stream(torch.cuda.current_stream())
             engine.synchronous = False
+            self._stream = torch.cuda.current_stream().cuda_stream
+        self._own_engine = owns
         self.engine = engine
         self.sequence_id = int(sequence_id)
         self.layer = layer
@@ -103,6 +106,14 @@ class PagedTorchKVCache:
     def paged_attention(self, queries, keys, values, mask="none"):
         """pagedAttention(queries:keys:values:mask:) (PagedMetalKVCache.swift:74-154)."""
         import torch
+        if self._own_engine:
+            # the cache's own engine follows the caller's current stream, so its
+            # kernels stay ordered after the producers of the inputs and before
+            # the consumers of the output (and the allocator's reuse of both)
+            cur_stream = torch.cuda.current_stream().cuda_stream
+            if cur_stream != self._stream:
+                self.engine.set_stream(cur_stream)
+                self._stream = cur_stream
         if _is_tensor_mask(mask):
             raise UnsupportedMask("materialized masks fall back to native attention")
         if mask not in ("none", "causal"):

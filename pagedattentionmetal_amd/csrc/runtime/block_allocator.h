@@ -26,6 +26,11 @@ namespace pam {
 struct PamError : std::runtime_error {
     explicit PamError(const std::string &m) : std::runtime_error(m) {}
 };
+// A request larger than the allocation-free decode's fixed scratch: always
+// reported as an error, also under graceful degradation.
+struct ScratchLimitError : PamError {
+    explicit ScratchLimitError(const std::string &m) : PamError(m) {}
+};
 // A failure reported by the GPU after work was enqueued (never retried).
 struct ExecutionError : PamError {
     explicit ExecutionError(const std::string &m) : PamError(m) {}

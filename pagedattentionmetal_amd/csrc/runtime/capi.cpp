@@ -721,9 +721,20 @@ struct TimedSpan {
     hipEvent_t a = nullptr, b = nullptr;
     hipStream_t stream;
     explicit TimedSpan(hipStream_t s) : stream(s) {
-        hip_check(hipEventCreate(&a), "hipEventCreate");
-        hip_check(hipEventCreate(&b), "hipEventCreate");
-        hip_check(hipEventRecord(a, stream), "hipEventRecord");
+        // a constructor that throws runs no destructor: release here
+        try {
+            hip_check(hipEventCreate(&a), "hipEventCreate");
+            hip_check(hipEventCreate(&b), "hipEventCreate");
+            hip_check(hipEventRecord(a, stream), "hipEventRecord");
+        } catch (...) {
+            release();
+            throw;
+        }
+    }
+    void release() {
+        if (a) (void)hipEventDestroy(a);
+        if (b) (void)hipEventDestroy(b);
+        a = b = nullptr;
     }
     // milliseconds from the first event to now on the stream (-1 if not measurable)
     float end() {
@@ -732,10 +743,7 @@ struct TimedSpan {
             (void)hipEventElapsedTime(&t, a, b);
         return t;
     }
-    ~TimedSpan() {
-        if (a) (void)hipEventDestroy(a);
-        if (b) (void)hipEventDestroy(b);
-    }
+    ~TimedSpan() { release(); }
     TimedSpan(const TimedSpan &) = delete;
     TimedSpan &operator=(const TimedSpan &) = delete;
 };

@@ -217,6 +217,8 @@ void Context::with_retry(const char *op, F &&fn) {
             fn();
             consecutive_failures = 0;
             return;
+        } catch (const ScratchLimitError &) {
+            throw;  // a size limit: the same request would fail again
         } catch (const ExecutionError &) {
             // work that reached the GPU and failed there is not replayed
             consecutive_failures += 1;
@@ -325,7 +327,7 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
     // zero page | counters | partials); requests that do not fit it are refused
     const int64_t fixed_parts = (int64_t)(kNoAllocScratchBytes - kNoAllocZeroBytes - kNoAllocCounterBytes);
     auto too_big = [](const char *what, int64_t need, int64_t have) {
-        return PamError(std::string("Unsupported paged attention path: the allocation-free decode's ") + what +
+        return ScratchLimitError(std::string("Unsupported paged attention path: the allocation-free decode's ") + what +
                         " needs " + std::to_string(need) + " bytes of its fixed " + std::to_string(have) +
                         "-byte scratch.");
     };
@@ -467,6 +469,13 @@ void Context::module_load(const char *path) {
         throw PamError(std::string("GPU device or stream could not be initialized: hipModuleLoad(") + path +
                        "): " + hipGetErrorString(e));
     }
+    // unloaded on every way out until the context takes it over below
+    struct ModuleGuard {
+        hipModule_t m;
+        ~ModuleGuard() {
+            if (m) (void)hipModuleUnload(m);
+        }
+    } guard{m};
     KernelTable t{};
     auto get = [&](const char *name) {
         hipFunction_t f = nullptr;
@@ -493,12 +502,12 @@ void Context::module_load(const char *path) {
             hip_check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&mod, t.streamk[dt][fl], 256, 0),
                       "code object occupancy");
             if (mod != lib) {
-                (void)hipModuleUnload(m);
                 throw PamError("Unsupported paged attention path: the code object's stream-K entry runs " +
                                std::to_string(mod) + " workgroups per CU, the library's kernel " +
                                std::to_string(lib) + ".");
             }
         }
+    guard.m = nullptr;
     module_ = m;
     ktab_ = t;
 }
@@ -579,6 +588,8 @@ void Context::decode_checked(const pam_decode_request &r, bool noalloc) {
     if (graceful_degradation) {
         try {
             decode_gpu(r, fixed);
+        } catch (const ScratchLimitError &) {
+            throw;  // a size limit of the fixed scratch, not a failure to degrade from
         } catch (const PamError &e) {
             std::fprintf(stderr, "[pam] decode failed: %s\n", e.what());
             zero_output(r.output, (size_t)(r.batch_size * q_bytes_per_token(r.layer)));

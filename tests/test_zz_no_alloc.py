@@ -82,5 +82,9 @@ def test_noalloc_refuses_what_does_not_fit():
         # (2048 rows + units) x 64 heads x (256 + 2) floats: far above 32 MiB
         assert lib.pam_engine_decode_noalloc(ctx, C.byref(r)) == -1
         assert b"fixed" in lib.pam_last_error(ctx)
+        # graceful degradation does not turn the size limit into zeros and success
+        assert lib.pam_engine_set_graceful_degradation(ctx, True) == 0
+        assert lib.pam_engine_decode_noalloc(ctx, C.byref(r)) == -1
+        assert b"fixed" in lib.pam_last_error(ctx)
     finally:
         lib.pam_destroy_context(ctx)
