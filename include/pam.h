@@ -452,18 +452,28 @@ int32_t pam_engine_mixed_step(void *context, const pam_mixed_request *request);
  * pipeline manager (PagedAttentionEngine.swift:151-198 builds the shader library
  * at start-up, :248-333 looks pipelines up by function name).  The build writes
  * libpam_kernels.hsaco (gfx950 code object, pam_module_default_path gives its
- * path beside libpam.so) with named entries: pam_decode_streamk_{f16,e4m3}_d128,
- * pam_decode_layers_streamk_{f16,e4m3}_d128, pam_prefill_f16_d128,
- * pam_prefill_fused_f16_d128, pam_prefill_e4m3_d128 and pam_fill_u32.
+ * path beside libpam.so) with a named entry for every kernel of the forward
+ * path:
+ *   decode   pam_decode_streamk_{f16,e4m3}_d128, pam_decode_layers_streamk_{f16,e4m3}_d128,
+ *            pam_decode_wg_{f16,e4m3}_d128, pam_decode_valu_{f32,f16,e4m3}_h{1,2,4,8},
+ *            pam_reduce_{f32,f16}
+ *   prefill  pam_prefill_f16_d128, pam_prefill_fused_f16_d128, pam_prefill_e4m3_d128,
+ *            pam_mixed_step_{f16,e4m3}_d128
+ *   append   pam_append_b{16,4,2}, pam_append_batch_b{16,4,2}, pam_append_fp8
+ *   staging  pam_stage_copy;  and pam_fill_u32 for callers' own launches.
  * pam_module_load loads one with hipModuleLoad; while it is loaded the context
- * launches those configurations through hipModuleLaunchKernel (same kernel
- * bodies: the same results bit for bit) and all others from the library.
+ * launches every configuration the object holds through hipModuleLaunchKernel
+ * (same kernel bodies: the same results bit for bit) and all others (MFMA
+ * decode at d != 128 or blocks of 8, the backward) from the library.
+ * pam_module_set_strict(ctx, 1) makes those others fail with an error instead,
+ * for hosts that must run only from the code object.
  * pam_module_function / pam_module_launch are the thin launch shim a host
  * language binds: any entry, grid and block sizes, and the packed kernel
  * arguments (args_bytes bytes at args, laid out as the kernel's parameters),
  * on the context's stream. */
 int32_t pam_module_load(void *context, const char *path);
 int32_t pam_module_unload(void *context);
+int32_t pam_module_set_strict(void *context, int32_t strict);
 int32_t pam_module_function(void *context, const char *name, void **function);
 int32_t pam_module_launch(void *context, void *function, uint32_t grid_x, uint32_t grid_y, uint32_t grid_z,
                           uint32_t block_x, uint32_t block_y, uint32_t block_z, uint32_t shared_bytes, void *args,

@@ -202,6 +202,11 @@ class PagedAttentionEngine:
     def unload_module(self):
         self._check(lib().pam_module_unload(self._ctx))
 
+    def set_module_strict(self, strict: bool):
+        """Strict: launches the loaded code object has no entry for fail instead of
+        running the library's kernel."""
+        self._check(lib().pam_module_set_strict(self._ctx, int(bool(strict))))
+
     def module_function(self, name: str) -> int:
         f = C.c_void_p()
         self._check(lib().pam_module_function(self._ctx, name.encode(), C.byref(f)))

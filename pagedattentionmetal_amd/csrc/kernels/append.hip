@@ -11,131 +11,29 @@
 // the new elements with it.  A deterministic block reduction replaces the
 // reference's scratch buffer + CAS atomics, and one launch replaces its two
 // synchronous passes.
-#include "kernels.h"
-#include "pam_device.h"
+#include "append_body.h"
 
 namespace pam {
 
+// The kernels (the fat binary's entries); the bodies also back the named
+// entries of the code object (module_entry.hip).
 template <typename CH>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p, int64_t chunks_per_row, int64_t total) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const int64_t t = i / chunks_per_row, c = i % chunks_per_row;
-        int64_t slot;
-        if (p.slot_mapping) {
-            slot = p.slot_mapping[t];
-            if (slot < 0) continue;  // padding token
-        } else {
-            const int64_t pos = (int64_t)p.token_offset + t;
-            slot = (int64_t)p.block_table[pos / p.block_size] * p.block_size + pos % p.block_size;
-        }
-        const CH *ks = static_cast<const CH *>(p.keys) + t * chunks_per_row + c;
-        const CH *vs = static_cast<const CH *>(p.values) + t * chunks_per_row + c;
-        static_cast<CH *>(p.k_pool)[slot * chunks_per_row + c] = *ks;
-        static_cast<CH *>(p.v_pool)[slot * chunks_per_row + c] = *vs;
-    }
+    append_body<CH>(p, chunks_per_row, total);
 }
 
-// One workgroup per touched (sequence, logical block).  The block's new tokens
-// are consecutive rows of the input and consecutive slots of the physical block,
-// so both passes (the max for the scale rule, then the quantisation) stream one
-// contiguous range: 8 halves in, 8 codes out per thread and step when the rows
-// are 16-byte multiples, one element at a time otherwise.
 __global__ __launch_bounds__(256) void kv_append_fp8_kernel(AppendBatchParams p, int32_t first_lb,
                                                             int32_t single_offset) {
-    int seq, lb;
-    if (p.work) {
-        const int4 w = p.work[blockIdx.x];
-        seq = w.x;
-        lb = w.y;
-    } else {
-        seq = 0;
-        lb = first_lb + blockIdx.x;
-    }
-    const int64_t row = (int64_t)p.num_kv_heads * p.head_dim;  // elements per token
-    const int64_t tok_base = p.cu_tokens ? p.cu_tokens[seq] : 0;
-    const int64_t n_tok = p.cu_tokens ? p.cu_tokens[seq + 1] - tok_base : p.total_tokens;
-    const int64_t off = p.token_offsets ? p.token_offsets[seq] : single_offset;
-    const int bs = p.block_size;
-    int64_t t0 = (int64_t)lb * bs - off, t1 = t0 + bs;
-    if (t0 < 0) t0 = 0;
-    if (t1 > n_tok) t1 = n_tok;
-    const int32_t phys = p.block_tables[(int64_t)seq * p.bt_stride + lb];
-    // input elements [t0 * row, t1 * row) -> pool elements from the slot of t0
-    const int64_t n = (t1 - t0) * row;
-    const f16 *kin = static_cast<const f16 *>(p.keys) + (tok_base + t0) * row;
-    const f16 *vin = static_cast<const f16 *>(p.values) + (tok_base + t0) * row;
-    const int64_t dst0 = ((int64_t)phys * bs + (off + t0 - (int64_t)lb * bs)) * row;
-    uint8_t *kp = static_cast<uint8_t *>(p.k_pool) + dst0;
-    uint8_t *vp = static_cast<uint8_t *>(p.v_pool) + dst0;
-    // 16-byte input rows and aligned buffers: every token row keeps the alignment
-    const bool vec = (row % 8) == 0 && (((uintptr_t)p.keys | (uintptr_t)p.values) & 15) == 0 &&
-                     (((uintptr_t)p.k_pool | (uintptr_t)p.v_pool) & 7) == 0;
-
-    float mk = 0.0f, mv = 0.0f;
-    if (vec) {
-        for (int64_t e = (int64_t)threadIdx.x * 8; e < n; e += (int64_t)blockDim.x * 8) {
-            const f16x8 a = *reinterpret_cast<const f16x8 *>(kin + e);
-            const f16x8 b = *reinterpret_cast<const f16x8 *>(vin + e);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                mk = fmaxf(mk, fabsf((float)a[i]));
-                mv = fmaxf(mv, fabsf((float)b[i]));
-            }
-        }
-    } else {
-        for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
-            mk = fmaxf(mk, fabsf((float)kin[e]));
-            mv = fmaxf(mv, fabsf((float)vin[e]));
-        }
-    }
-    mk = wave_max_xor(mk, 1, 64);
-    mv = wave_max_xor(mv, 1, 64);
-    __shared__ float red[2][4];
-    __shared__ uint16_t scales[2];
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        red[0][wave] = mk;
-        red[1][wave] = mv;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float a = red[0][0], b = red[1][0];
-        for (int w = 1; w < (int)(blockDim.x >> 6); w++) {
-            a = fmaxf(a, red[0][w]);
-            b = fmaxf(b, red[1][w]);
-        }
-        scales[0] = f16_to_bits(fp8_scale_rule(a, bits_to_f16(p.k_scale[phys])));
-        scales[1] = f16_to_bits(fp8_scale_rule(b, bits_to_f16(p.v_scale[phys])));
-    }
-    __syncthreads();
-    const f16 ks = bits_to_f16(scales[0]), vs = bits_to_f16(scales[1]);
-    if (vec) {
-        for (int64_t e = (int64_t)threadIdx.x * 8; e < n; e += (int64_t)blockDim.x * 8) {
-            const f16x8 a = *reinterpret_cast<const f16x8 *>(kin + e);
-            const f16x8 b = *reinterpret_cast<const f16x8 *>(vin + e);
-            uint32_t kw[2] = {0u, 0u}, vw[2] = {0u, 0u};
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                kw[i >> 2] |= fp8_quantize(a[i], ks) << (8 * (i & 3));
-                vw[i >> 2] |= fp8_quantize(b[i], vs) << (8 * (i & 3));
-            }
-            *reinterpret_cast<uint2 *>(kp + e) = make_uint2(kw[0], kw[1]);
-            *reinterpret_cast<uint2 *>(vp + e) = make_uint2(vw[0], vw[1]);
-        }
-    } else {
-        for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
-            kp[e] = (uint8_t)fp8_quantize(kin[e], ks);
-            vp[e] = (uint8_t)fp8_quantize(vin[e], vs);
-        }
-    }
-    if (threadIdx.x == 0) {
-        p.k_scale[phys] = scales[0];
-        p.v_scale[phys] = scales[1];
-    }
+    append_fp8_body(p, first_lb, single_offset);
 }
 
-hipError_t launch_append(const AppendParams &p, int32_t dtype, hipStream_t stream) {
+template <typename CH>
+__global__ __launch_bounds__(256) void kv_append_batch_kernel(AppendBatchParams p, int64_t chunks_per_row,
+                                                              int64_t total) {
+    append_batch_body<CH>(p, chunks_per_row, total);
+}
+
+hipError_t launch_append(const AppendParams &p, int32_t dtype, hipStream_t stream, const KernelTable *kt) {
     if (p.num_tokens <= 0) return hipSuccess;
     const int64_t row_elems = (int64_t)p.num_kv_heads * p.head_dim;
     if (dtype == kFP8) {
@@ -159,8 +57,11 @@ hipError_t launch_append(const AppendParams &p, int32_t dtype, hipStream_t strea
         b.num_kv_heads = p.num_kv_heads;
         b.head_dim = p.head_dim;
         b.block_size = p.block_size;
-        hipLaunchKernelGGL(kv_append_fp8_kernel, dim3(last_lb - first_lb + 1), dim3(256), 0, stream, b, first_lb,
-                           p.token_offset);
+        const dim3 grid(last_lb - first_lb + 1);
+        const int32_t off = p.token_offset;
+        hipError_t e;
+        if (via_module(kt, kt ? kt->append_fp8 : nullptr, &e, grid, dim3(256), stream, b, first_lb, off)) return e;
+        hipLaunchKernelGGL(kv_append_fp8_kernel, grid, dim3(256), 0, stream, b, first_lb, off);
         return hipGetLastError();
     }
     const int64_t row_bytes = row_elems * (dtype == kF32 ? 4 : 2);
@@ -170,37 +71,24 @@ hipError_t launch_append(const AppendParams &p, int32_t dtype, hipStream_t strea
         int64_t b = (total + threads - 1) / threads;
         return (int)(b < 65536 ? b : 65536);
     };
-    if (row_bytes % 16 == 0) {
-        const int64_t cpr = row_bytes / 16, total = total_bytes / 16;
-        hipLaunchKernelGGL(kv_append_kernel<uint4>, dim3(blocks_for(total)), dim3(threads), 0, stream, p, cpr, total);
-    } else if (row_bytes % 4 == 0) {
-        const int64_t cpr = row_bytes / 4, total = total_bytes / 4;
-        hipLaunchKernelGGL(kv_append_kernel<uint32_t>, dim3(blocks_for(total)), dim3(threads), 0, stream, p, cpr,
-                           total);
-    } else {
-        const int64_t cpr = row_bytes / 2, total = total_bytes / 2;
-        hipLaunchKernelGGL(kv_append_kernel<uint16_t>, dim3(blocks_for(total)), dim3(threads), 0, stream, p, cpr,
-                           total);
-    }
+    // piece width: 16, 4 or 2 bytes, the widest that divides a token row
+    const int w = row_bytes % 16 == 0 ? 0 : (row_bytes % 4 == 0 ? 1 : 2);
+    const int64_t piece = w == 0 ? 16 : (w == 1 ? 4 : 2);
+    const int64_t cpr = row_bytes / piece, total = total_bytes / piece;
+    const dim3 grid(blocks_for(total));
+    hipError_t e;
+    if (via_module(kt, kt ? kt->append[w] : nullptr, &e, grid, dim3(threads), stream, p, cpr, total)) return e;
+    if (w == 0)
+        hipLaunchKernelGGL(kv_append_kernel<uint4>, grid, dim3(threads), 0, stream, p, cpr, total);
+    else if (w == 1)
+        hipLaunchKernelGGL(kv_append_kernel<uint32_t>, grid, dim3(threads), 0, stream, p, cpr, total);
+    else
+        hipLaunchKernelGGL(kv_append_kernel<uint16_t>, grid, dim3(threads), 0, stream, p, cpr, total);
     return hipGetLastError();
 }
 
-template <typename CH>
-__global__ __launch_bounds__(256) void kv_append_batch_kernel(AppendBatchParams p, int64_t chunks_per_row,
-                                                              int64_t total) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const int64_t t = i / chunks_per_row, c = i % chunks_per_row;
-        const int2 tp = p.token_pos[t];
-        const int64_t slot =
-            (int64_t)p.block_tables[(int64_t)tp.x * p.bt_stride + tp.y / p.block_size] * p.block_size +
-            tp.y % p.block_size;
-        static_cast<CH *>(p.k_pool)[slot * chunks_per_row + c] = static_cast<const CH *>(p.keys)[i];
-        static_cast<CH *>(p.v_pool)[slot * chunks_per_row + c] = static_cast<const CH *>(p.values)[i];
-    }
-}
-
-hipError_t launch_append_batch(const AppendBatchParams &p, int32_t dtype, hipStream_t stream) {
+hipError_t launch_append_batch(const AppendBatchParams &p, int32_t dtype, hipStream_t stream,
+                               const KernelTable *kt) {
     if (dtype != kFP8) {
         if (p.token_pos == nullptr) return hipErrorInvalidValue;
         if (p.total_tokens <= 0) return hipSuccess;
@@ -210,19 +98,25 @@ hipError_t launch_append_batch(const AppendBatchParams &p, int32_t dtype, hipStr
             int64_t b = (total + 255) / 256;
             return (int)(b < 65536 ? b : 65536);
         };
-        if (row_bytes % 16 == 0)
-            hipLaunchKernelGGL(kv_append_batch_kernel<uint4>, dim3(blocks_for(total_bytes / 16)), dim3(256), 0, stream,
-                               p, row_bytes / 16, total_bytes / 16);
-        else if (row_bytes % 4 == 0)
-            hipLaunchKernelGGL(kv_append_batch_kernel<uint32_t>, dim3(blocks_for(total_bytes / 4)), dim3(256), 0,
-                               stream, p, row_bytes / 4, total_bytes / 4);
+        const int w = row_bytes % 16 == 0 ? 0 : (row_bytes % 4 == 0 ? 1 : 2);
+        const int64_t piece = w == 0 ? 16 : (w == 1 ? 4 : 2);
+        const int64_t cpr = row_bytes / piece, total = total_bytes / piece;
+        const dim3 grid(blocks_for(total));
+        hipError_t e;
+        if (via_module(kt, kt ? kt->append_batch[w] : nullptr, &e, grid, dim3(256), stream, p, cpr, total)) return e;
+        if (w == 0)
+            hipLaunchKernelGGL(kv_append_batch_kernel<uint4>, grid, dim3(256), 0, stream, p, cpr, total);
+        else if (w == 1)
+            hipLaunchKernelGGL(kv_append_batch_kernel<uint32_t>, grid, dim3(256), 0, stream, p, cpr, total);
         else
-            hipLaunchKernelGGL(kv_append_batch_kernel<uint16_t>, dim3(blocks_for(total_bytes / 2)), dim3(256), 0,
-                               stream, p, row_bytes / 2, total_bytes / 2);
+            hipLaunchKernelGGL(kv_append_batch_kernel<uint16_t>, grid, dim3(256), 0, stream, p, cpr, total);
         return hipGetLastError();
     }
     if (p.work == nullptr || p.token_offsets == nullptr || p.cu_tokens == nullptr) return hipErrorInvalidValue;
     if (p.num_work <= 0) return hipSuccess;
+    const int32_t zero = 0;
+    hipError_t e;
+    if (via_module(kt, kt ? kt->append_fp8 : nullptr, &e, dim3(p.num_work), dim3(256), stream, p, zero, zero)) return e;
     hipLaunchKernelGGL(kv_append_fp8_kernel, dim3(p.num_work), dim3(256), 0, stream, p, 0, 0);
     return hipGetLastError();
 }

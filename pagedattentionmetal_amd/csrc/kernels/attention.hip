@@ -22,6 +22,7 @@
 // All keep the online-softmax state of Reference/paged_attention_sim.py:94-123
 // (in log2 units).
 #include "attention_body.h"
+#include "valu_body.h"
 
 namespace pam {
 
@@ -39,291 +40,16 @@ __global__ __launch_bounds__(64 * kMfmaWaves, (MfmaShape<KV, HD>::OCC)) void att
     streamk_body<KV, HD, BLK, FL>(p, blockIdx.x, gridDim.x);
 }
 
-// ------------------------------------------------------------------ VALU body
-
-template <typename T>
-__device__ __forceinline__ void load4(const T *ptr, float *v);
-template <>
-__device__ __forceinline__ void load4<float>(const float *ptr, float *v) {
-    const float4 x = *reinterpret_cast<const float4 *>(ptr);
-    v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
-}
-template <>
-__device__ __forceinline__ void load4<f16>(const f16 *ptr, float *v) {
-    const f16x4 x = *reinterpret_cast<const f16x4 *>(ptr);
-    v[0] = (float)x[0], v[1] = (float)x[1], v[2] = (float)x[2], v[3] = (float)x[3];
-}
-
-template <typename T>
-__device__ __forceinline__ void store4(T *ptr, const float *v);
-template <>
-__device__ __forceinline__ void store4<float>(float *ptr, const float *v) {
-    *reinterpret_cast<float4 *>(ptr) = make_float4(v[0], v[1], v[2], v[3]);
-}
-template <>
-__device__ __forceinline__ void store4<f16>(f16 *ptr, const float *v) {
-    f16x4 x;
-    x[0] = (f16)v[0], x[1] = (f16)v[1], x[2] = (f16)v[2], x[3] = (f16)v[3];
-    *reinterpret_cast<f16x4 *>(ptr) = x;
-}
-
-// KV element slice of 4 as floats (fp8: dequantised in half, then widened)
-template <typename KV>
-__device__ __forceinline__ void load_kv4(const KV *ptr, f16 scale, float *v);
-template <>
-__device__ __forceinline__ void load_kv4<float>(const float *ptr, f16, float *v) {
-    load4<float>(ptr, v);
-}
-template <>
-__device__ __forceinline__ void load_kv4<f16>(const f16 *ptr, f16, float *v) {
-    load4<f16>(ptr, v);
-}
-template <>
-__device__ __forceinline__ void load_kv4<uint8_t>(const uint8_t *ptr, f16 scale, float *v) {
-    const uint32_t w = *reinterpret_cast<const uint32_t *>(ptr);
-#pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = (float)fp8_dequant((w >> (8 * i)) & 0xFFu, scale);
-}
-
-constexpr int kValuBatch = 8;  // steps of the VALU kernel whose loads are in flight together
-
-// lanes_per_row: power of two >= head_dim / 4 (<= 64); heads NH share one kv head.
+// The kernels (the fat binary's entries); valu_body and reduce_body also back
+// the named entries of the code object (module_entry.hip).
 template <typename KV, typename QT, int NH>
 __global__ __launch_bounds__(64) void attn_valu_kernel(AttnParams p, int lanes_per_row) {
-    const int lane = threadIdx.x;
-    const int part = blockIdx.x, hg = blockIdx.y, r = blockIdx.z;
-    const int HD = p.head_dim, H = p.num_heads;
-    const int G = H / p.num_kv_heads;
-    const int h0 = hg * NH;
-    const int kvh = h0 / G;
-    const RowCtx c = row_ctx(p, r);
-    const PartRange pr = part_range(c, part, p.part_tokens);
-    if (part >= (pr.nparts > 1 ? pr.nparts : 1)) return;
-
-    const int LPR = lanes_per_row, TPI = 64 / lanes_per_row;
-    const int sub = lane / LPR;
-    const int d0 = (lane % LPR) * 4;
-    const bool dim_ok = d0 < HD;
-    QT *out = static_cast<QT *>(p.out);
-    if (pr.nparts == 0) {
-        if (sub == 0 && dim_ok) {
-            float nanv[4] = {__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
-            for (int hh = 0; hh < NH; hh++) store4<QT>(out + (c.out_row * H + h0 + hh) * (int64_t)HD + d0, nanv);
-        }
-        return;
-    }
-
-    float q[NH][4];
-#pragma unroll
-    for (int hh = 0; hh < NH; hh++) {
-        if (dim_ok)
-            load4<QT>(static_cast<const QT *>(p.q) + ((int64_t)c.out_row * H + h0 + hh) * HD + d0, q[hh]);
-        else
-            q[hh][0] = q[hh][1] = q[hh][2] = q[hh][3] = 0.0f;
-    }
-
-    float m[NH], l[NH], acc[NH][4];
-#pragma unroll
-    for (int hh = 0; hh < NH; hh++) {
-        m[hh] = -INFINITY;
-        l[hh] = 0.0f;
-        acc[hh][0] = acc[hh][1] = acc[hh][2] = acc[hh][3] = 0.0f;
-    }
-    const int64_t row_stride = (int64_t)p.num_kv_heads * HD;
-    const KV *kpool = static_cast<const KV *>(p.k_pool);
-    const KV *vpool = static_cast<const KV *>(p.v_pool);
-    const int bs = p.block_size;
-
-    // Tokens go in batches of kValuBatch steps of TPI tokens: the block-table
-    // entries of a batch are requested together, then its K/V slices, so a batch
-    // waits on two memory latencies; one online-softmax update covers the batch.
-    constexpr int UB = kValuBatch;
-    for (int j0 = pr.t_begin * 16; j0 < pr.t_end * 16; j0 += UB * TPI) {
-        bool ok[UB];
-        int64_t phys[UB];
-#pragma unroll
-        for (int u = 0; u < UB; u++) {
-            const int j = j0 + u * TPI + sub;
-            ok[u] = j >= c.k_lo && j < c.k_hi && j < pr.t_end * 16;
-            phys[u] = ok[u] ? (int64_t)c.bt[j / bs] : 0;
-        }
-        float kv[UB][4], vv[UB][4];
-#pragma unroll
-        for (int u = 0; u < UB; u++) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) kv[u][e] = vv[u][e] = 0.0f;
-            if (ok[u] && dim_ok) {
-                const int j = j0 + u * TPI + sub;
-                const int64_t off = (phys[u] * bs + j % bs) * row_stride + (int64_t)kvh * HD + d0;
-                f16 ks = (f16)1.0f, vs = (f16)1.0f;
-                if constexpr (sizeof(KV) == 1) {
-                    ks = bits_to_f16(p.k_scale[phys[u]]);
-                    vs = bits_to_f16(p.v_scale[phys[u]]);
-                }
-                load_kv4<KV>(kpool + off, ks, kv[u]);
-                load_kv4<KV>(vpool + off, vs, vv[u]);
-            }
-        }
-#pragma unroll
-        for (int hh = 0; hh < NH; hh++) {
-            float sv[UB];
-            float mt = -INFINITY;
-#pragma unroll
-            for (int u = 0; u < UB; u++) {
-                float sd = q[hh][0] * kv[u][0] + q[hh][1] * kv[u][1] + q[hh][2] * kv[u][2] + q[hh][3] * kv[u][3];
-                sd = wave_sum_xor(sd, 1, LPR);
-                sv[u] = ok[u] ? sd * p.scale_log2 : -INFINITY;
-                mt = fmaxf(mt, sv[u]);
-            }
-            mt = wave_max_xor(mt, LPR, 64);
-            const float m_new = fmaxf(m[hh], mt);
-            // a batch whose tokens all fall outside the key range keeps the state
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float corr = exp2f(m[hh] - m_use);
-            float ls = l[hh] * corr;
-            float a4[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) a4[e] = acc[hh][e] * corr;
-#pragma unroll
-            for (int u = 0; u < UB; u++) {
-                const float pj = exp2f(sv[u] - m_use);
-                ls += pj;
-#pragma unroll
-                for (int e = 0; e < 4; e++) a4[e] += pj * vv[u][e];
-            }
-            l[hh] = ls;
-            m[hh] = m_new;
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[hh][e] = a4[e];
-        }
-    }
-
-#pragma unroll
-    for (int hh = 0; hh < NH; hh++) {
-        l[hh] = wave_sum_xor(l[hh], LPR, 64);
-#pragma unroll
-        for (int e = 0; e < 4; e++) acc[hh][e] = wave_sum_xor(acc[hh][e], LPR, 64);
-    }
-    if (sub != 0 || !dim_ok) return;
-    if (pr.nparts == 1) {
-#pragma unroll
-        for (int hh = 0; hh < NH; hh++) {
-            const float inv = 1.0f / l[hh];
-            float v[4] = {acc[hh][0] * inv, acc[hh][1] * inv, acc[hh][2] * inv, acc[hh][3] * inv};
-            store4<QT>(out + (c.out_row * H + h0 + hh) * (int64_t)HD + d0, v);
-        }
-    } else if (p.seg_count == nullptr) {  // partials for attn_reduce_kernel
-#pragma unroll
-        for (int hh = 0; hh < NH; hh++) {
-            const int64_t slot = ((int64_t)r * H + h0 + hh) * p.max_parts + part;
-            store4<float>(p.part_o + slot * HD + d0, acc[hh]);
-            if (d0 == 0) {
-                p.part_ml[slot * 2 + 0] = m[hh];
-                p.part_ml[slot * 2 + 1] = l[hh];
-            }
-        }
-    } else {
-        // Merged in the kernel (no reduce launch): the partial is published with
-        // write-through stores and counted on the (row, head group) counter; the
-        // wave that completes the count folds all partitions in order, as
-        // attn_reduce_kernel does, and writes the rows.  Offsets are bytes from
-        // part_o (< 2 GiB).
-        const __amdgpu_buffer_rsrc_t prs = part_rsrc(p);
-        const int ml_off = (int)((const char *)p.part_ml - (const char *)p.part_o);
-        auto slot_of = [&](int hh, int pt) { return ((int64_t)r * H + h0 + hh) * p.max_parts + pt; };
-#pragma unroll
-        for (int hh = 0; hh < NH; hh++) {
-            const int64_t slot = slot_of(hh, part);
-            const f32x4 v = {acc[hh][0], acc[hh][1], acc[hh][2], acc[hh][3]};
-            __builtin_amdgcn_raw_buffer_store_b128(v, prs, (int)((slot * HD + d0) * 4), 0, kSc1);
-            if (d0 == 0) {
-                const f32x2 ml = {m[hh], l[hh]};
-                __builtin_amdgcn_raw_buffer_store_b64(ml, prs, ml_off + (int)(slot * 8), 0, kSc1);
-            }
-        }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        uint32_t before = 0;
-        if (lane == 0)  // lane 0 has sub 0 and d0 0: it is active here
-            before = arrive_count(p.seg_count + (int64_t)r * (H / NH) + hg, p.epoch);
-        before = __builtin_amdgcn_readfirstlane(before);
-        if (before != (uint32_t)(pr.nparts - 1)) return;
-        for (int hh = 0; hh < NH; hh++) {
-            float M = -INFINITY;
-            for (int pt = 0; pt < pr.nparts; pt++) {
-                const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)(slot_of(hh, pt) * 8), 0, kSc1);
-                M = fmaxf(M, ml[0]);
-            }
-            float den = 0.0f, a[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int pt = 0; pt < pr.nparts; pt++) {
-                const int64_t slot = slot_of(hh, pt);
-                const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)(slot * 8), 0, kSc1);
-                const f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)((slot * HD + d0) * 4), 0, kSc1);
-                const float w = ml[0] == -INFINITY ? 0.0f : exp2f(ml[0] - M);
-                den += w * ml[1];
-#pragma unroll
-                for (int e = 0; e < 4; e++) a[e] += w * v[e];
-            }
-            const float inv = 1.0f / den;
-#pragma unroll
-            for (int e = 0; e < 4; e++) a[e] *= inv;
-            store4<QT>(out + (c.out_row * H + h0 + hh) * (int64_t)HD + d0, a);
-        }
-    }
+    valu_body<KV, QT, NH>(p, lanes_per_row);
 }
 
-// ------------------------------------------------------------------ split-context reduce
-// O = sum_p 2^{m_p - M} O_p / sum_p 2^{m_p - M} l_p over the row's partitions.
-// Split-context reduce: one wave per (row, head), four per workgroup.  The
-// partials' maxima and sums are reduced across lanes (one partition per lane),
-// then lane groups of HD/4 lanes each accumulate a share of the partitions'
-// weighted outputs and the groups are summed with shuffles.
 template <typename QT>
 __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnParams p) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r = blockIdx.y, h = blockIdx.x * 4 + wave;
-    if (h >= p.num_heads) return;
-    const RowCtx c = row_ctx(p, r);
-    const PartRange pr = part_range(c, 0, p.part_tokens);
-    const int np = pr.nparts;
-    if (np <= 1) return;
-    const int HD = p.head_dim, H = p.num_heads;
-    const int64_t base = ((int64_t)r * H + h) * p.max_parts;
-    // one pass over (m, l): each lane folds its partitions, then the lanes merge
-    float Ml = -INFINITY, dl = 0.0f;
-    for (int i = lane; i < np; i += 64) {
-        const float mi = p.part_ml[(base + i) * 2], li = p.part_ml[(base + i) * 2 + 1];
-        const float Mn = fmaxf(Ml, mi);
-        if (Mn != -INFINITY) dl = dl * exp2f(Ml - Mn) + li * exp2f(mi - Mn);
-        Ml = Mn;
-    }
-    const float M = wave_max_xor(Ml, 1, 64);
-    float den = Ml == -INFINITY ? 0.0f : dl * exp2f(Ml - M);
-    den = wave_sum_xor(den, 1, 64);
-    // lanes per group: HD/4 rounded up to a power of two (<= 64)
-    int lpg = 1;
-    while (lpg * 4 < HD) lpg <<= 1;
-    const int ng = 64 / lpg, g = lane / lpg, d0 = (lane % lpg) * 4;
-    float a[4] = {0.f, 0.f, 0.f, 0.f};
-    if (d0 < HD) {
-#pragma unroll 4
-        for (int i = g; i < np; i += ng) {
-            const float w = exp2f(p.part_ml[(base + i) * 2] - M);
-            float v[4];
-            load4<float>(p.part_o + (base + i) * HD + d0, v);
-#pragma unroll
-            for (int e = 0; e < 4; e++) a[e] += w * v[e];
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; e++) a[e] = wave_sum_xor(a[e], lpg, 64);
-    if (g == 0 && d0 < HD) {
-        const float inv = 1.0f / den;
-#pragma unroll
-        for (int e = 0; e < 4; e++) a[e] *= inv;
-        store4<QT>(static_cast<QT *>(p.out) + (c.out_row * H + h) * (int64_t)HD + d0, a);
-    }
+    reduce_body<QT>(p);
 }
 
 // ------------------------------------------------------------------ launchers
@@ -374,10 +100,10 @@ static hipError_t launch_mfma_blk(const AttnParams &p, hipStream_t stream, const
         int grid = 0;
         const hipError_t e = streamk_grid<KV, HD, BLK>(&grid);
         if (e != hipSuccess) return e;
-        if (kt && HD == 128 && BLK == kBlkTile) {
-            const hipFunction_t f = kt->streamk[sizeof(KV) == 1][p.fused_layers > 1];
-            if (f) return module_launch(f, dim3(grid), block, p, stream);
-        }
+        hipError_t me;
+        if (via_module(kt, kt && HD == 128 && BLK == kBlkTile ? kt->streamk[sizeof(KV) == 1][p.fused_layers > 1] : nullptr,
+                       &me, dim3(grid), block, stream, p))
+            return me;
         // fused layers run on the same grid (the partial slots are planned for it;
         // no wave waits on another, so residency is a matter of speed only)
         if (p.fused_layers > 1)
@@ -387,6 +113,10 @@ static hipError_t launch_mfma_blk(const AttnParams &p, hipStream_t stream, const
         return hipGetLastError();
     }
     const dim3 grid(p.max_parts, p.num_kv_heads, p.rows);
+    hipError_t me;
+    if (via_module(kt, kt && HD == 128 && BLK == kBlkTile ? kt->mfma_wg[sizeof(KV) == 1] : nullptr, &me, grid, block,
+                   stream, p))
+        return me;
     hipLaunchKernelGGL((attn_mfma_kernel<KV, HD, BLK>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
@@ -442,12 +172,17 @@ bool mfma_streamk_plan(const AttnParams &p, int32_t dtype, int64_t *part_slots, 
 }
 
 template <typename KV, typename QT>
-static hipError_t launch_valu(const AttnParams &p, hipStream_t stream) {
+static hipError_t launch_valu(const AttnParams &p, hipStream_t stream, const KernelTable *kt) {
     int lpr = 1;
     while (lpr * 4 < p.head_dim) lpr <<= 1;
     if (lpr > 64 || p.head_dim % 4 != 0) return hipErrorInvalidValue;
     const int nh = p.heads_per_wave;
     dim3 grid(p.max_parts, p.num_heads / nh, p.rows);
+    const int slot = nh == 1 ? 0 : (nh == 2 ? 1 : (nh == 4 ? 2 : (nh == 8 ? 3 : -1)));
+    if (slot < 0) return hipErrorInvalidValue;
+    const int kvi = sizeof(KV) == 4 ? 0 : (sizeof(KV) == 2 ? 1 : 2);
+    hipError_t me;
+    if (via_module(kt, kt ? kt->valu[kvi][slot] : nullptr, &me, grid, dim3(64), stream, p, lpr)) return me;
     switch (nh) {
         case 1: hipLaunchKernelGGL((attn_valu_kernel<KV, QT, 1>), grid, dim3(64), 0, stream, p, lpr); break;
         case 2: hipLaunchKernelGGL((attn_valu_kernel<KV, QT, 2>), grid, dim3(64), 0, stream, p, lpr); break;
@@ -471,9 +206,9 @@ hipError_t launch_attention(const AttnParams &p_in, int32_t dtype, bool use_mfma
         e = dtype == kF16 ? launch_mfma<f16>(p, stream, kt) : launch_mfma<uint8_t>(p, stream, kt);
     } else {
         switch (dtype) {
-            case kF32: e = launch_valu<float, float>(p, stream); break;
-            case kF16: e = launch_valu<f16, f16>(p, stream); break;
-            case kFP8: e = launch_valu<uint8_t, f16>(p, stream); break;
+            case kF32: e = launch_valu<float, float>(p, stream, kt); break;
+            case kF16: e = launch_valu<f16, f16>(p, stream, kt); break;
+            case kFP8: e = launch_valu<uint8_t, f16>(p, stream, kt); break;
             default: return hipErrorInvalidValue;
         }
     }
@@ -482,6 +217,7 @@ hipError_t launch_attention(const AttnParams &p_in, int32_t dtype, bool use_mfma
     // stream-K (MFMA) and the VALU kernel with counters merge in the kernel
     if (p.max_parts <= 1 || p.seg_count != nullptr) return e;
     dim3 grid((p.num_heads + 3) / 4, p.rows);
+    if (via_module(kt, kt ? kt->reduce[dtype != kF32] : nullptr, &e, grid, dim3(256), stream, p)) return e;
     if (dtype == kF32)
         hipLaunchKernelGGL((attn_reduce_kernel<float>), grid, dim3(256), 0, stream, p);
     else

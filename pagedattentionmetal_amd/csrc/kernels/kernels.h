@@ -85,18 +85,45 @@ struct AttnParams {
 
 // Entry points of a loaded code object (libpam_kernels.hsaco, module_entry.hip).
 // A launcher given a table launches a configuration the table holds through
-// hipModuleLaunchKernel and any other through the library's own kernel; both
-// run the same kernel body.
+// hipModuleLaunchKernel, and any other through the library's own kernel (or
+// refuses it with hipErrorNotFound when the table is strict); both run the same
+// kernel body.
 struct KernelTable {
     hipFunction_t streamk[2][2];  // decode stream-K, d = 128, blocks >= 16: [f16, e4m3][one layer, fused layers]
+    hipFunction_t mfma_wg[2];     // decode, workgroup form (rows > 2048), d = 128, blocks >= 16: f16, e4m3
     hipFunction_t prefill[3];     // dense prefill, d = 128: f16, f16 with fused append, e4m3
+    hipFunction_t mixed[2];       // one-launch mixed step: f16, e4m3
+    hipFunction_t valu[3][4];     // VALU rows: [f32, f16, e4m3 KV][1, 2, 4, 8 heads per wave]
+    hipFunction_t reduce[2];      // split-context reduce: f32, f16 outputs
+    hipFunction_t append[3];      // append copy in 16-, 4- or 2-byte pieces
+    hipFunction_t append_batch[3];
+    hipFunction_t append_fp8;     // FP8 quantize-on-append (single sequence and batched)
+    hipFunction_t stage;          // staging copy
+    bool strict;                  // refuse configurations the table lacks
 };
-// hipModuleLaunchKernel of `f` with the parameter block as its kernel arguments.
-inline hipError_t module_launch(hipFunction_t f, dim3 grid, dim3 block, const AttnParams &p, hipStream_t stream) {
-    size_t bytes = sizeof(AttnParams);
-    void *config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<AttnParams *>(&p), HIP_LAUNCH_PARAM_BUFFER_SIZE,
-                      &bytes, HIP_LAUNCH_PARAM_END};
-    return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, nullptr, config);
+// hipModuleLaunchKernel of `f` with the kernel arguments `a...` (each passed by
+// address, as the kernel declares them).
+template <class... A>
+inline hipError_t module_launch(hipFunction_t f, dim3 grid, dim3 block, hipStream_t stream, A... a) {
+    void *args[] = {static_cast<void *>(&a)...};
+    return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, args, nullptr);
+}
+// The code-object side of a launcher: with a table, launches its entry `f`
+// (or, strict and without one, refuses) and returns true with the status in
+// *e; false: launch the library's kernel.
+template <class... A>
+inline bool via_module(const KernelTable *kt, hipFunction_t f, hipError_t *e, dim3 grid, dim3 block,
+                       hipStream_t stream, A... a) {
+    if (!kt) return false;
+    if (f) {
+        *e = module_launch(f, grid, block, stream, a...);
+        return true;
+    }
+    if (kt->strict) {
+        *e = hipErrorNotFound;
+        return true;
+    }
+    return false;
 }
 // Resident workgroups per CU of the library's stream-K kernel (dtype f16 / fp8,
 // d = 128, blocks >= 16, one layer or fused layers), for checking a code
@@ -151,7 +178,7 @@ struct AppendParams {
     int32_t num_tokens;
     int32_t num_kv_heads, head_dim, block_size;
 };
-hipError_t launch_append(const AppendParams &p, int32_t dtype, hipStream_t stream);
+hipError_t launch_append(const AppendParams &p, int32_t dtype, hipStream_t stream, const KernelTable *kt = nullptr);
 
 // Batched append for a mixed step.  f32/f16: token t goes to position
 // token_pos[t].y of sequence token_pos[t].x through that sequence's block-table
@@ -174,7 +201,8 @@ struct AppendBatchParams {
     int32_t seqs, bt_stride, total_tokens;
     int32_t num_kv_heads, head_dim, block_size;
 };
-hipError_t launch_append_batch(const AppendBatchParams &p, int32_t dtype, hipStream_t stream);
+hipError_t launch_append_batch(const AppendBatchParams &p, int32_t dtype, hipStream_t stream,
+                               const KernelTable *kt = nullptr);
 
 // Attention gradients of one sequence (training path): non-causal rows
 // 0 .. seq_len-1 over keys [window_start, seq_len); m, l are the forward's row max
@@ -200,7 +228,8 @@ hipError_t launch_fp8_dequant(const uint8_t *codes, const uint16_t *scales, uint
 
 // Copy `bytes` from mapped pinned host memory to the device, as a kernel on
 // `stream` (both pointers 16-byte aligned).
-hipError_t launch_stage_copy(const void *host_mapped, void *dst, size_t bytes, hipStream_t stream);
+hipError_t launch_stage_copy(const void *host_mapped, void *dst, size_t bytes, hipStream_t stream,
+                             const KernelTable *kt = nullptr);
 
 // Calibration streams of known size (achievable HBM rates, counter scaling).
 hipError_t launch_stream_read(const void *src, size_t bytes, uint32_t *sink, int blocks, hipStream_t stream);
@@ -238,6 +267,7 @@ constexpr int kMixedMaxRows = 1024;  // decode rows one mixed launch takes
 bool mixed_launch_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size, int32_t rows);
 // partial slots (d + 2 floats each) and merge counters of the decode part
 void mixed_decode_slots(const AttnParams &p, int32_t decode_groups, int64_t *part_slots, int64_t *counters);
-hipError_t launch_mixed_step(const AttnParams &p, int32_t dtype, int32_t decode_groups, hipStream_t stream);
+hipError_t launch_mixed_step(const AttnParams &p, int32_t dtype, int32_t decode_groups, hipStream_t stream,
+                             const KernelTable *kt = nullptr);
 
 }  // namespace pam

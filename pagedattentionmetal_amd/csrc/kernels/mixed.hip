@@ -13,22 +13,15 @@
 // Neither part waits on the other: both merge their split work with their own
 // epoch-tagged counters (pf_count, seg_count), and the K/V they read was
 // written by an earlier launch (the step's append).
-#include "attention_body.h"
-#include "prefill_body.h"
+#include "mixed_body.h"
 
 namespace pam {
 
-static_assert(kPrefillWaves % kMfmaWaves == 0, "the decode part runs whole stream-K units");
-static_assert(kMixedMaxRows <= kStreamKMaxRows, "decode rows of a mixed launch");
 
+// the kernel (the fat binary's entry); mixed_body also backs the code object's
 template <typename KV>
 __global__ __launch_bounds__(64 * kPrefillWaves, 1) void mixed_step_kernel(AttnParams p) {
-    const int b = blockIdx.x;  // workgroup-uniform branch: every barrier below is reached by all waves
-    if (b < p.pf_groups)
-        prefill_body<128, kPrefillRB, false, KV>(p);
-    else
-        streamk_body<KV, 128, kBlkTile, false, kPrefillWaves, kMixedMaxRows>(p, b - p.pf_groups,
-                                                                             (int)gridDim.x - p.pf_groups);
+    mixed_body<KV>(p);
 }
 
 bool mixed_launch_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size, int32_t rows) {
@@ -45,7 +38,8 @@ void mixed_decode_slots(const AttnParams &p, int32_t decode_groups, int64_t *par
     *counters = (int64_t)p.rows * Hkv;
 }
 
-hipError_t launch_mixed_step(const AttnParams &p_in, int32_t dtype, int32_t decode_groups, hipStream_t stream) {
+hipError_t launch_mixed_step(const AttnParams &p_in, int32_t dtype, int32_t decode_groups, hipStream_t stream,
+                             const KernelTable *kt) {
     AttnParams p = p_in;
     p.epoch = next_launch_epoch();
     const int G = p.num_heads / p.num_kv_heads;
@@ -54,6 +48,8 @@ hipError_t launch_mixed_step(const AttnParams &p_in, int32_t dtype, int32_t deco
     if (p.seg_count == nullptr || p.part_o == nullptr || p.zero_page == nullptr) return hipErrorInvalidValue;
     if ((int64_t)p.pf_groups + decode_groups > INT32_MAX) return hipErrorInvalidValue;
     const dim3 grid(p.pf_groups + decode_groups), block(64 * kPrefillWaves);
+    hipError_t e;
+    if (via_module(kt, kt ? kt->mixed[dtype == kFP8] : nullptr, &e, grid, block, stream, p)) return e;
     if (dtype == kFP8)
         hipLaunchKernelGGL((mixed_step_kernel<uint8_t>), grid, block, 0, stream, p);
     else

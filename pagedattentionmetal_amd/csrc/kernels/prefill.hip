@@ -59,10 +59,10 @@ hipError_t launch_prefill_mfma(const AttnParams &p_in, int32_t dtype, hipStream_
     const dim3 grid(p.pf_groups), block(64 * kPrefillWaves);
     if (dtype == kFP8 && (p.fuse_k != nullptr || p.k_scale == nullptr || p.v_scale == nullptr))
         return hipErrorInvalidValue;
-    if (kt) {  // the code object's entry of this configuration, when it has one
-        const hipFunction_t f = kt->prefill[dtype == kFP8 ? 2 : (p.fuse_k != nullptr ? 1 : 0)];
-        if (f) return module_launch(f, grid, block, p, stream);
-    }
+    hipError_t e;  // the code object's entry of this configuration, when it has one
+    if (via_module(kt, kt ? kt->prefill[dtype == kFP8 ? 2 : (p.fuse_k != nullptr ? 1 : 0)] : nullptr, &e, grid, block,
+                   stream, p))
+        return e;
     if (dtype == kFP8) {
         hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, false, uint8_t>), grid, block, 0, stream, p);
     } else if (p.fuse_k != nullptr) {

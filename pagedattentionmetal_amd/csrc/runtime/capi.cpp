@@ -313,6 +313,10 @@ PAM_API int32_t pam_module_load(void *context, const char *path) {
     return guarded(context, [&](Context *ctx) { ctx->module_load(path); });
 }
 
+PAM_API int32_t pam_module_set_strict(void *context, int32_t strict) {
+    return guarded(context, [&](Context *ctx) { ctx->module_set_strict(strict != 0); });
+}
+
 PAM_API int32_t pam_module_unload(void *context) {
     return guarded(context, [&](Context *ctx) { ctx->module_unload(); });
 }

@@ -197,7 +197,7 @@ void *Context::stage_into(void *dst, const void *host, size_t bytes) {
     const char *src_dev = static_cast<const char *>(pinned_dev_) + off;
     pinned_used_ += need;
     if (((uintptr_t)dst & 15) == 0)
-        hip_check(launch_stage_copy(src_dev, dst, bytes, stream()), "staging copy");
+        hip_check(launch_stage_copy(src_dev, dst, bytes, stream(), ktab()), "staging copy");
     else
         hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream()), "hipMemcpyAsync staging");
     hip_check(hipEventRecord(seg_event_[cur_seg_], stream()), "hipEventRecord");
@@ -492,6 +492,25 @@ void Context::module_load(const char *path) {
     t.prefill[0] = get("pam_prefill_f16_d128");
     t.prefill[1] = get("pam_prefill_fused_f16_d128");
     t.prefill[2] = get("pam_prefill_e4m3_d128");
+    t.mfma_wg[0] = get("pam_decode_wg_f16_d128");
+    t.mfma_wg[1] = get("pam_decode_wg_e4m3_d128");
+    t.mixed[0] = get("pam_mixed_step_f16_d128");
+    t.mixed[1] = get("pam_mixed_step_e4m3_d128");
+    static const char *kv_names[3] = {"f32", "f16", "e4m3"};
+    static const int heads[4] = {1, 2, 4, 8};
+    for (int k = 0; k < 3; k++)
+        for (int h = 0; h < 4; h++)
+            t.valu[k][h] = get(("pam_decode_valu_" + std::string(kv_names[k]) + "_h" + std::to_string(heads[h])).c_str());
+    t.reduce[0] = get("pam_reduce_f32");
+    t.reduce[1] = get("pam_reduce_f16");
+    static const char *piece[3] = {"16", "4", "2"};
+    for (int w = 0; w < 3; w++) {
+        t.append[w] = get(("pam_append_b" + std::string(piece[w])).c_str());
+        t.append_batch[w] = get(("pam_append_batch_b" + std::string(piece[w])).c_str());
+    }
+    t.append_fp8 = get("pam_append_fp8");
+    t.stage = get("pam_stage_copy");
+    t.strict = module_strict_;
     // a stream-K launch is planned for the library kernel's resident grid: an
     // entry with another occupancy would not fit the plan's partial slots
     for (int dt = 0; dt < 2; dt++)
@@ -873,7 +892,7 @@ void Context::append_layers(const pam_append_layers_request &r) {
             mark(ev0_);
             for (const auto &a : reqs) {
                 const AppendParams ap = append_params(a);
-                check_launch([&] { return launch_append(ap, a.layer.data_type, stream()); }, "appendLayers");
+                check_launch([&] { return launch_append(ap, a.layer.data_type, stream(), ktab()); }, "appendLayers");
             }
             mark(ev1_);
             finish("appendLayers");
@@ -1108,7 +1127,7 @@ void Context::fused_prefill_gpu(const pam_fused_prefill_request &r) {
     }
     with_retry("fusedPrefill", [&] {
         mark(ev0_);
-        if (!one_kernel) check_launch([&] { return launch_append(ap, l.data_type, stream()); }, "fused prefill append");
+        if (!one_kernel) check_launch([&] { return launch_append(ap, l.data_type, stream(), ktab()); }, "fused prefill append");
         launch_prefill_plan(pl, l.data_type);
         mark(ev1_);
         finish("fusedPrefill");
@@ -1156,6 +1175,8 @@ void Context::backward(const pam_backward_request &r) {
     p.row_c = p.row_d + (int64_t)r.seq_len * l.num_heads;
     with_retry("backward", [&] {
         mark(ev0_);
+        if (ktab() && ktab()->strict)
+            throw PamError("Unsupported paged attention path: the backward kernels are not in the code object.");
         check_launch([&] { return launch_backward(p, l.data_type, stream()); }, "backward");
         mark(ev1_);
         finish("backward");
@@ -1225,7 +1246,7 @@ void Context::append_gpu(const pam_append_request &r) {
     const AppendParams p = append_params(r);
     with_retry(l.data_type == kFP8 ? "appendToCacheCheckedFP8" : "appendToCacheFlat", [&] {
         mark(ev0_);
-        check_launch([&] { return launch_append(p, l.data_type, stream()); }, "append");
+        check_launch([&] { return launch_append(p, l.data_type, stream(), ktab()); }, "append");
         mark(ev1_);
         finish("append");
     });
@@ -1423,9 +1444,9 @@ void Context::mixed_step(const pam_mixed_request &r) {
     }
     with_retry("mixedStep", [&] {
         mark(ev0_);
-        if (ab.keys) check_launch([&] { return launch_append_batch(ab, l.data_type, stream()); }, "mixed append");
+        if (ab.keys) check_launch([&] { return launch_append_batch(ab, l.data_type, stream(), ktab()); }, "mixed append");
         if (one_launch) {
-            check_launch([&] { return launch_mixed_step(p, l.data_type, mix_dec_groups, stream()); }, "mixed attention");
+            check_launch([&] { return launch_mixed_step(p, l.data_type, mix_dec_groups, stream(), ktab()); }, "mixed attention");
             mark(evmid_);
             mark(ev1_);
             finish("mixed step");

@@ -160,6 +160,12 @@ class Context {
     void module_launch_raw(void *function, const uint32_t grid[3], const uint32_t block[3], uint32_t shared_bytes,
                            void *args, size_t args_bytes);
     const KernelTable *ktab() const { return module_ ? &ktab_ : nullptr; }
+    // strict: launches the code object has no entry for fail instead of
+    // running the library's kernel
+    void module_set_strict(bool strict) {
+        module_strict_ = strict;
+        ktab_.strict = strict;
+    }
 
     // --- scratch
     void reserve_workspace(size_t bytes);
@@ -227,6 +233,7 @@ class Context {
     int cur_seg_ = 0;
     void *zero_page_ = nullptr;
     hipModule_t module_ = nullptr;
+    bool module_strict_ = false;
     KernelTable ktab_{};
     bool stats_pending_ = false;
     bool stats_has_mid_ = false;

@@ -86,3 +86,103 @@ def test_module_launch_named_entry_with_packed_arguments():
     torch.zeros(4, device="cuda").add_(1)
     torch.cuda.synchronize()
     e.close()
+
+
+def _c3_step(torch, e, w, pools, mode, fp8):
+    """One c3 mixed step (append of the new tokens included) on fresh copies of
+    the pools; returns the output and the pools' bytes afterwards."""
+    from pagedattentionmetal_amd import api
+    kp0, vp0, q, nk, nv, ks0, vs0 = pools
+    kp, vp = kp0.clone(), vp0.clone()
+    ks = ks0.clone() if ks0 is not None else None
+    vs = vs0.clone() if vs0 is not None else None
+    bt = torch.from_numpy(w.block_tables).cuda()
+    out = torch.zeros_like(q)
+    e.set_mixed_launch(mode)
+    lay = api.PagedLayerSpec(w.head_dim, w.num_heads, w.num_kv_heads, w.block_size, 2 if fp8 else 1)
+    e.mixed_step(q, out, kp, vp, bt, w.context_lens, w.query_lens, lay, new_keys=nk, new_values=nv, k_scale=ks,
+                 v_scale=vs)
+    torch.cuda.synchronize()
+    res = [to_host(out), to_host(kp), to_host(vp)]
+    if fp8:
+        res += [to_host(ks), to_host(vs)]
+    return res
+
+
+def test_module_strict_runs_c1_and_c3_from_the_code_object():
+    """A strict module-bound engine (no library kernel may run) decodes c1 (f32,
+    VALU rows), a 2100-row GQA decode (workgroup form + reduce kernel) and the c3
+    mixed step with its append (f16 in both launch forms, and over e4m3 pools
+    quantised by the FP8 append), bit for bit as the library's kernels do."""
+    import torch
+    from pagedattentionmetal_amd import api, workloads
+    from pagedattentionmetal_amd.api import PagedAttentionError
+    w1 = workloads.config(1)
+    q1, kp1, vp1 = workloads.device_pools(w1)
+    bt1 = torch.from_numpy(w1.block_tables).cuda()
+    l1 = torch.from_numpy(w1.seq_lens.view("int32")).cuda()
+    lay1 = api.PagedLayerSpec(w1.head_dim, w1.num_heads, w1.num_kv_heads, w1.block_size, w1.data_type, w1.window)
+    # more rows than the stream-K form takes: the workgroup form and the reduce kernel
+    rng = np.random.default_rng(2100)
+    lens = rng.integers(1, 400, 2100).tolist()
+    qw, kw, vw, btw, lw = make_case(rng, len(lens), 16, 4, 128, 16, 1, lens)
+    dw = [to_dev(a) for a in (qw, kw, vw, btw, lw)]
+    w3 = workloads.mixed_config()
+    kp3, vp3, q3, nk3, nv3 = workloads.mixed_pools(w3)
+    # e4m3 pools: the c3 context quantised through the FP8 append kernel (one
+    # sequence at a time), by the engine under test
+    res = []
+    for module in (False, True):
+        e = _engine(module)
+        if module:
+            e.set_module_strict(True)
+        out = {}
+        o = torch.zeros_like(q1)
+        e.set_partition_tokens(0)
+        e.decode(q1, kp1, vp1, bt1, l1, o, w1.batch, w1.max_num_blocks, lay1)
+        out["c1"] = to_host(o)
+        e.set_partition_tokens(64)  # split rows: partitions merged by the reduce kernel
+        o = torch.zeros(qw.shape, dtype=torch.float16, device="cuda")
+        e.decode(*dw[:5], o, len(lens), btw.shape[1], _spec(16, 4, 128, 16, 1))
+        out["wg"] = to_host(o)
+        e.set_partition_tokens(0)
+        for mode in (0, 2):
+            out[f"c3_{mode}"] = _c3_step(torch, e, w3, (kp3, vp3, q3, nk3, nv3, None, None), mode, False)
+        k8 = torch.zeros(kp3.shape, dtype=torch.uint8, device="cuda")
+        v8 = torch.zeros_like(k8)
+        s8k = torch.zeros(kp3.shape[0], dtype=torch.float16, device="cuda")
+        s8v = torch.zeros_like(s8k)
+        bt3 = torch.from_numpy(w3.block_tables).cuda()
+        lay8 = api.PagedLayerSpec(w3.head_dim, w3.num_kv_heads, w3.num_kv_heads, w3.block_size, 2)
+        for b in range(len(w3.context_lens)):
+            L = int(w3.context_lens[b])
+            if L == 0:
+                continue
+            tok = torch.arange(L, device="cuda")
+            phys = bt3[b][tok // w3.block_size].long()
+            e.append_to_cache(kp3[phys, tok % w3.block_size].contiguous(), vp3[phys, tok % w3.block_size].contiguous(),
+                              k8, v8, bt3[b].contiguous(), 0, L, lay8, k_scale=s8k, v_scale=s8v)
+        out["c3_fp8"] = _c3_step(torch, e, w3, (k8, v8, q3, nk3, nv3, s8k, s8v), 0, True)
+        if module:
+            # the backward kernels are not in the code object: refused, not run
+            with pytest.raises(PagedAttentionError, match="code object"):
+                T = 16
+                qb = torch.zeros((T, 32, 128), dtype=torch.float16, device="cuda")
+                kb = torch.zeros((1, 16, 8, 128), dtype=torch.float16, device="cuda")
+                m = torch.zeros((T, 32), dtype=torch.float32, device="cuda")
+                e.backward(qb, kb, kb, torch.zeros(1, dtype=torch.int32, device="cuda"), qb, m, m + 1,
+                           torch.empty_like(qb), torch.zeros_like(kb), torch.zeros_like(kb), T,
+                           _spec(32, 8, 128, 16, 1))
+        res.append(out)
+        e.close()
+    lib_, mod = res
+    assert np.array_equal(lib_["c1"].view(np.uint32), mod["c1"].view(np.uint32))
+    assert np.array_equal(lib_["wg"].view(np.uint16), mod["wg"].view(np.uint16))
+    for key in ("c3_0", "c3_2", "c3_fp8"):
+        for i, (a, b) in enumerate(zip(lib_[key], mod[key])):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (key, i)
+    ref = oracle.decode(0, to_host(q1), to_host(kp1), to_host(vp1), w1.block_tables, w1.seq_lens, w1.num_heads,
+                        n_threads=8)
+    assert row_rel_err(mod["c1"].astype(np.float64), ref) <= TOL[0]
+    ref = oracle.decode(1, qw, kw, vw, btw, lw, 16, n_threads=8)
+    assert row_rel_err(mod["wg"].astype(np.float64), ref) <= TOL[1]
