@@ -173,10 +173,12 @@ def _gather(torch, pool, tables):
 
 @pytest.mark.gpu
 def test_c5_shape_trace_step_against_oracle():
-    """A short serving trace at BASELINE c5's layer shape (64 q / 8 kv heads, d 128,
-    bs 16, fp16, 4096-token window; prompts U[64, 8192], outputs U[16, 512]): one
-    mid-trace step that has both prompts and decode rows is checked against the
-    oracle - every decode row, and the last 16 rows of one prompt."""
+    """A serving trace at BASELINE c5's layer shape (64 q / 8 kv heads, d 128,
+    bs 16, fp16, 4096-token window; prompts U[64, 8192], outputs U[16, 512]):
+    an early, a middle and a late step of a 40-step trace (the first step with
+    both prompts and decode rows at or after steps 4, 20 and 36) are checked
+    against the oracle - every decode row, and the last 16 rows of the longest
+    prompt."""
     import torch
     import oracle
     from helpers import TOL, row_rel_err
@@ -186,14 +188,16 @@ def test_c5_shape_trace_step_against_oracle():
                                 layer_kw=dict(num_heads=64, num_kv_heads=8, window=W))
     eng = inf.engine
     orig = eng.mixed_step
-    seen = {"checked": 0, "steps": 0}
+    targets = [4, 20, 36]
+    seen = {"checked": [], "steps": 0}
 
     def checked_step(q, out, k_pool, v_pool, bt, ctx, ql, layer, **kw):
         orig(q, out, k_pool, v_pool, bt, ctx, ql, layer, **kw)
         seen["steps"] += 1
         dec = np.nonzero(ql == 1)[0]
         pre = np.nonzero(ql > 1)[0]
-        if seen["checked"] or seen["steps"] < 4 or len(dec) == 0 or len(pre) == 0:
+        due = [t for t in targets if t <= seen["steps"]]
+        if len(due) <= len(seen["checked"]) or len(dec) == 0 or len(pre) == 0:
             return
         torch.cuda.synchronize()
         bs, H, d = layer.block_size, layer.num_heads, layer.head_dim
@@ -217,12 +221,13 @@ def test_c5_shape_trace_step_against_oracle():
         qp = q[rows].cpu().numpy()
         refp = oracle.prefill(1, qp, kh, vh, btp[0], P - 16, causal=True, window=W, n_threads=8)
         gotp = out[rows].cpu().numpy().astype(np.float64)
-        assert row_rel_err(gotp, refp) <= TOL[1], f"prompt of {P} tokens"
-        seen["checked"] += 1
+        assert row_rel_err(gotp, refp) <= TOL[1], f"step {seen['steps']}: prompt of {P} tokens"
+        seen["checked"].append((seen["steps"], len(dec), P))
 
     eng.mixed_step = checked_step
-    poisson_trace(inf, steps=14, rate=2.0, prompt_range=(64, 8192), output_range=(16, 512), seed=0x5EED0005)
-    assert seen["checked"] == 1, seen
+    poisson_trace(inf, steps=40, rate=2.0, prompt_range=(64, 8192), output_range=(16, 512), seed=0x5EED0005)
+    assert len(seen["checked"]) == 3, seen
+    print("checked (step, decode rows, prompt tokens):", seen["checked"])
 
 
 @pytest.mark.gpu
