@@ -480,6 +480,16 @@ int32_t pam_module_launch(void *context, void *function, uint32_t grid_x, uint32
                           size_t args_bytes);
 const char *pam_module_default_path(void);
 
+/* One decode step of a sequence through the framework adapter (PagedMetalKVCache
+ * pagedAttention at seqLen 1, PagedMetalKVCache.swift:94-129): appendTokens(1)
+ * on the cache's bookkeeping, the token's K/V ([numKVHeads][headDim]) written
+ * into the pools and its query ([numHeads][headDim]) decoded into output.  The
+ * sequence's block table and length stay in HBM between steps, patched by the
+ * append kernel, so a step is two launches and no host-to-device staging.
+ * f32 and f16 caches; pam_free_sequence releases the device table. */
+int32_t pam_decode_step(void *context, void *cache, int64_t sequenceID, const void *keys, const void *values,
+                        const void *query, void *output, int32_t numHeads);
+
 /* Allocation-free decode.  No counterpart in the reference: it is for callers
  * that cannot allocate device memory (tight serving loops, harnesses that
  * forbid hipMalloc).  Not for HIP graph capture: the host picks each launch's

@@ -182,6 +182,7 @@ SIGNATURES = {
     "pam_module_load": (I32, [P, C.c_char_p]),
     "pam_module_unload": (I32, [P]),
     "pam_module_set_strict": (I32, [P, I32]),
+    "pam_decode_step": (I32, [P, P, I64, P, P, P, P, I32]),
     "pam_module_function": (I32, [P, C.c_char_p, C.POINTER(C.c_void_p)]),
     "pam_module_launch": (I32, [P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                 C.c_uint32, P, SZ]),

@@ -75,6 +75,7 @@ class PagedTorchKVCache:
             engine = api.PagedAttentionEngine()
             engine.set_stream(torch.cuda.current_stream())
             engine.synchronous = False
+            engine.set_gpu_timing(False)  # a serving loop: no per-call timing events
             self._stream = torch.cuda.current_stream().cuda_stream
         self._own_engine = owns
         self.engine = engine
@@ -84,6 +85,7 @@ class PagedTorchKVCache:
                                                 layer.num_kv_heads, layer.data_type)
         self.cache_manager.allocate_sequence(self.sequence_id)
         self.offset = 0
+        self._step = api.lib().pam_decode_step
 
     # metaState (PagedMetalKVCache.swift:158-167)
     @property
@@ -136,10 +138,26 @@ class PagedTorchKVCache:
         io = torch.float32 if L.data_type == PagedAttentionDataType.float32 else torch.float16
         cm = self.cache_manager
         cur = self.offset
+        if S == 1 and L.data_type != PagedAttentionDataType.float8:
+            # a decode step in one library call (pam_decode_step): bookkeeping,
+            # the token's K/V append and the decode; the block table and length
+            # stay on the device between steps
+            def flat(t, rows):
+                if t.dtype == io and t.is_contiguous():
+                    return t.view(rows, d)
+                return t[0, :, 0].to(io).contiguous()
+            k, v, q = flat(keys, L.num_kv_heads), flat(values, L.num_kv_heads), flat(queries, H)
+            out = torch.empty((H, d), dtype=io, device=queries.device)
+            rc = self._step(self.engine.handle, cm.handle, self.sequence_id, k.data_ptr(), v.data_ptr(),
+                            q.data_ptr(), out.data_ptr(), H)
+            if rc != 0:
+                self.engine._check(rc)
+            self.offset += 1
+            out = out.view(1, H, 1, d)
+            return out if out.dtype == queries.dtype else out.to(queries.dtype)
         cm.append_tokens(self.sequence_id, S)
         if S == 1:
-            # a decode step through the cache's own calls (pam_append_kv, pam_decode):
-            # the library stages the table and length, no tensor is built per step
+            # FP8 caches: the cache's own calls (pam_append_kv, pam_decode)
             k = keys[0, :, 0].to(io).contiguous()    # [Hkv, d]
             v = values[0, :, 0].to(io).contiguous()
             q = queries[0, :, 0].to(io).contiguous()  # [H, d]

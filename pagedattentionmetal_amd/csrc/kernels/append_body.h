@@ -11,6 +11,10 @@ namespace pam {
 
 template <typename CH>
 __device__ __forceinline__ void append_body(const AppendParams &p, int64_t chunks_per_row, int64_t total) {
+    if (p.length_patch && blockIdx.x == 0 && threadIdx.x == 0) {
+        if (p.table_patch) p.table_patch[p.patch_index] = p.patch_block;
+        *p.length_patch = p.length_value;
+    }
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
         const int64_t t = i / chunks_per_row, c = i % chunks_per_row;
@@ -18,6 +22,8 @@ __device__ __forceinline__ void append_body(const AppendParams &p, int64_t chunk
         if (p.slot_mapping) {
             slot = p.slot_mapping[t];
             if (slot < 0) continue;  // padding token
+        } else if (p.fixed_slot >= 0) {
+            slot = p.fixed_slot;  // one token
         } else {
             const int64_t pos = (int64_t)p.token_offset + t;
             slot = (int64_t)p.block_table[pos / p.block_size] * p.block_size + pos % p.block_size;

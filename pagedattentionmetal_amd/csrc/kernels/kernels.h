@@ -177,6 +177,16 @@ struct AppendParams {
     int32_t token_offset;
     int32_t num_tokens;
     int32_t num_kv_heads, head_dim, block_size;
+    // one-token appends of a sequence whose table lives on the device (the
+    // decode step): fixed_slot >= 0 is token 0's pool slot, computed by the
+    // host, and the kernel also writes table_patch[patch_index] = patch_block
+    // (when table_patch is set) and *length_patch = length_value, the table
+    // and length the decode launched after it reads
+    int64_t fixed_slot = -1;
+    int32_t *table_patch = nullptr;
+    uint32_t *length_patch = nullptr;
+    int32_t patch_index = 0, patch_block = 0;
+    uint32_t length_value = 0;
 };
 hipError_t launch_append(const AppendParams &p, int32_t dtype, hipStream_t stream, const KernelTable *kt = nullptr);
 

@@ -138,6 +138,7 @@ PAM_API void pam_free_sequence(void *cache, int64_t sequenceID) {
     if (!c) return;
     std::lock_guard<std::mutex> g(c->mu);
     c->alloc.free_sequence(sequenceID);
+    c->drop_device_table(sequenceID);
 }
 
 PAM_API int32_t pam_available_blocks(void *cache) {
@@ -248,6 +249,101 @@ PAM_API int32_t pam_decode(void *context, void *cache, const int64_t *batchIDs, 
         r.layer = layer_of(c, numHeads);
         r.k_pool_bytes = r.v_pool_bytes = c->pool_bytes;
         ctx->decode(r);
+    });
+}
+
+// The adapter's decode step (PagedMetalKVCache.swift:94-129 at seqLen 1):
+// appendTokens(count: 1), appendToCache of the token's K/V, decode of its query.
+// The sequence's table and length stay in HBM between steps (KVCache::
+// DeviceTable): the append kernel writes the token at a slot the host computes,
+// patches a new last table entry and the length, and the decode reads them, so
+// a step is two launches and no staging.  Any other table change (a first step,
+// copy-on-write, a prefix hit) re-stages the table first.
+PAM_API int32_t pam_decode_step(void *context, void *cache, int64_t sequenceID, const void *keys, const void *values,
+                                const void *query, void *output, int32_t numHeads) {
+    KVCache *c = cache_of(cache);
+    if (!c || !keys || !values || !query || !output) return -1;
+    return guarded(context, [&](Context *ctx) {
+        std::lock_guard<std::mutex> g(c->mu);
+        require_device(c);
+        if (c->dtype == kFP8) throw invalid_configuration("the decode step appends one f32 or f16 token.");
+        BlockCopies copies;
+        try {
+            c->alloc.append_tokens(sequenceID, 1, nullptr, 0, &copies);
+        } catch (...) {
+            c->copy_blocks(copies, ctx->stream());  // CoW done before an OOM stays done
+            throw;
+        }
+        c->copy_blocks(copies, ctx->stream());
+        const LogicalSequence &s = c->alloc.sequence(sequenceID);
+        const std::vector<int32_t> &t = s.block_table;
+        const int32_t nb = (int32_t)t.size(), bs = c->alloc.block_size();
+        KVCache::DeviceTable &m = c->device_tables[sequenceID];
+        if (m.cap < nb) {
+            int32_t cap = 64;
+            while (cap < nb) cap *= 2;
+            int32_t *p = nullptr;
+            hip_check(hipMalloc(&p, ((size_t)cap + 1) * 4), "hipMalloc decode-step table");
+            if (m.ptr) {
+                (void)hipStreamSynchronize(ctx->stream());
+                (void)hipFree(m.ptr);
+            }
+            m.ptr = p;
+            m.cap = cap;
+            m.shadow.clear();
+        }
+        AppendParams ap{};
+        ap.keys = keys;
+        ap.values = values;
+        ap.k_pool = c->k_pool;
+        ap.v_pool = c->v_pool;
+        ap.token_offset = (int32_t)s.length - 1;
+        ap.num_tokens = 1;
+        ap.num_kv_heads = c->num_kv_heads;
+        ap.head_dim = c->head_dim;
+        ap.block_size = bs;
+        const int64_t pos = s.length - 1;
+        ap.fixed_slot = (int64_t)t[(size_t)(pos / bs)] * bs + pos % bs;
+        ap.length_patch = reinterpret_cast<uint32_t *>(m.ptr);
+        ap.length_value = (uint32_t)s.length;
+        const bool grew_by_one = m.shadow.size() + 1 == t.size() && std::equal(m.shadow.begin(), m.shadow.end(), t.begin());
+        const bool same = m.shadow.size() == t.size() && std::equal(m.shadow.begin(), m.shadow.end(), t.begin());
+        if (grew_by_one) {
+            ap.table_patch = m.ptr + 1;
+            ap.patch_index = nb - 1;
+            ap.patch_block = t.back();
+        } else if (!same) {
+            std::vector<int32_t> img((size_t)nb + 1);
+            img[0] = (int32_t)s.length;
+            std::copy(t.begin(), t.end(), img.begin() + 1);
+            ctx->stage_into(m.ptr, img.data(), img.size() * 4);
+        }
+        m.shadow.clear();  // unknown until the step's work is enqueued
+        pam_append_request a{};
+        a.keys = keys;
+        a.values = values;
+        a.k_pool = c->k_pool;
+        a.v_pool = c->v_pool;
+        a.block_table = m.ptr + 1;
+        a.block_table_bytes = (size_t)nb * 4;
+        a.token_offset = ap.token_offset;
+        a.num_new_tokens = 1;
+        a.layer = layer_of(c, c->num_kv_heads);
+        a.k_pool_bytes = a.v_pool_bytes = c->pool_bytes;
+        pam_decode_request d{};
+        d.q = query;
+        d.output = output;
+        d.k_pool = c->k_pool;
+        d.v_pool = c->v_pool;
+        d.block_tables = m.ptr + 1;
+        d.seq_lengths = reinterpret_cast<const uint32_t *>(m.ptr);
+        d.block_tables_bytes = (size_t)nb * 4;
+        d.seq_lengths_bytes = 4;
+        d.batch_size = 1;
+        d.max_num_blocks = nb;
+        d.layer = layer_of(c, numHeads);
+        d.k_pool_bytes = d.v_pool_bytes = c->pool_bytes;
+        if (ctx->decode_step(a, ap, d)) m.shadow = t;
     });
 }
 

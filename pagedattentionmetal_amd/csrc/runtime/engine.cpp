@@ -1222,6 +1222,40 @@ void Context::validate_append(const pam_append_request &r) {
         throw invalid_configuration("append request has a null buffer.");
 }
 
+bool Context::decode_step(const pam_append_request &a, const AppendParams &ap, const pam_decode_request &d) {
+    validate_append(a);
+    validate_decode(d);
+    if (a.num_new_tokens != 1 || a.layer.data_type == kFP8)
+        throw invalid_configuration("the decode step appends one f32 or f16 token.");
+    ensure_device();
+    auto run = [&] {
+        const DecodePlan dp = plan_decode(d, nullptr, 1, nullptr, nullptr);
+        with_retry("decodeStep", [&] {
+            mark(ev0_);
+            check_launch([&] { return launch_append(ap, a.layer.data_type, stream(), ktab()); }, "decode step append");
+            check_launch([&] { return launch_attention(dp.p, d.layer.data_type, dp.use_mfma, stream(),
+                                                       gpu_timing ? evmid_ : nullptr, ktab()); },
+                         "decode step");
+            mark(ev1_);
+            finish("decode step");
+        });
+        record_stats(PAM_OP_DECODE, 1, 0, d.max_num_blocks, dp.tmp, dp.p.max_parts > 1 || dp.p.seg_count != nullptr,
+                     true);
+    };
+    if (graceful_degradation) {
+        try {
+            run();
+        } catch (const PamError &e) {
+            std::fprintf(stderr, "[pam] decode step failed: %s\n", e.what());
+            zero_output(d.output, (size_t)q_bytes_per_token(d.layer));
+            return false;
+        }
+    } else {
+        run();
+    }
+    return true;
+}
+
 AppendParams Context::append_params(const pam_append_request &r) {
     const pam_layer_spec &l = r.layer;
     AppendParams p{};
@@ -1238,6 +1272,7 @@ AppendParams Context::append_params(const pam_append_request &r) {
     p.num_kv_heads = l.num_kv_heads;
     p.head_dim = l.head_dim;
     p.block_size = l.block_size;
+    p.fixed_slot = -1;
     return p;
 }
 

@@ -48,10 +48,22 @@ KVCache::~KVCache() {
     if (!has_device) return;
     (void)hipSetDevice(device);
     (void)hipDeviceSynchronize();
+    for (auto &t : device_tables)
+        if (t.second.ptr) (void)hipFree(t.second.ptr);
     if (k_pool) (void)hipFree(k_pool);
     if (v_pool) (void)hipFree(v_pool);
     if (k_scale) (void)hipFree(k_scale);
     if (v_scale) (void)hipFree(v_scale);
+}
+
+void KVCache::drop_device_table(int64_t id) {
+    auto it = device_tables.find(id);
+    if (it == device_tables.end()) return;
+    if (it->second.ptr) {
+        (void)hipSetDevice(device);
+        (void)hipFree(it->second.ptr);  // waits for the work that reads it
+    }
+    device_tables.erase(it);
 }
 
 size_t KVCache::bytes_per_block() const {

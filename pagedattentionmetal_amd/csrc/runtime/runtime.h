@@ -13,6 +13,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../../include/pam.h"
@@ -62,6 +63,20 @@ class KVCache {
     size_t bytes_per_block() const;  // one pool (K or V)
     // perform copy-on-write block copies in HBM on the given stream
     void copy_blocks(const BlockCopies &copies, hipStream_t stream);
+
+    // A sequence's block table and length kept in HBM for the decode step
+    // (pam_decode_step): [length | table entries ...], capacity `cap` entries.
+    // `shadow` is what the device copy holds; a step whose table only grew by
+    // its last entry patches that entry in the append kernel, any other change
+    // re-stages the whole table.
+    struct DeviceTable {
+        int32_t *ptr = nullptr;
+        int32_t cap = 0;
+        std::vector<int32_t> shadow;
+        uint32_t length = 0;
+    };
+    std::unordered_map<int64_t, DeviceTable> device_tables;
+    void drop_device_table(int64_t id);
 };
 
 class Context {
@@ -111,6 +126,11 @@ class Context {
     void setup_noalloc();
     void prefill(const pam_prefill_request &r);
     void append(const pam_append_request &r);
+    // one decode step of a sequence: the append of its new token (`ap`, one
+    // token, with its table and length patches) then the decode of `d`, which
+    // reads the table and length the append wrote; validated as append + decode.
+    // False: the work failed and graceful degradation zeroed the output
+    bool decode_step(const pam_append_request &a, const AppendParams &ap, const pam_decode_request &d);
     void mixed_step(const pam_mixed_request &r);
     void fused_prefill(const pam_fused_prefill_request &r);
     void backward(const pam_backward_request &r);

@@ -109,3 +109,63 @@ def test_paged_cache_refusals_and_fallback():
     assert calls == ["array", "causal"] and cache.offset == 0
     out = paged_attention_with_cache_update(q, k, k, cache, 64 ** -0.5, "causal", fallback=native)
     assert torch.is_tensor(out) and cache.offset == 4 and len(calls) == 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,H,hkv,d,bs", [(1, 32, 8, 128, 16), (0, 8, 2, 64, 8)])
+def test_decode_step_matches_append_then_decode(dtype, H, hkv, d, bs):
+    """pam_decode_step (device-resident table and length, patched by the append
+    kernel) against pam_append_tokens + pam_append_kv + pam_decode on a twin
+    cache: two sequences sharing a hashed prefix whose partial tail block is
+    copied on the first step (a full re-stage), then 40 steps each across
+    several block boundaries.  Outputs, pools and bookkeeping are identical."""
+    import ctypes as C
+    import torch
+    from pagedattentionmetal_amd import api
+    L = api.lib()
+    tdt = torch.float32 if dtype == 0 else torch.float16
+    rng = np.random.default_rng(99 + dtype)
+    P = 2 * bs + bs // 4  # prompt: two full blocks and a partial third
+    hashes = (C.c_uint64 * 3)(11, 22, 33)
+    prompt_k = torch.from_numpy(rng.standard_normal((P, hkv, d)).astype(np.float32)).to("cuda", tdt)
+    prompt_v = torch.from_numpy(rng.standard_normal((P, hkv, d)).astype(np.float32)).to("cuda", tdt)
+    steps = [(sid, torch.from_numpy(rng.standard_normal((3, max(H, hkv), d)).astype(np.float32)).to("cuda", tdt))
+             for _ in range(40) for sid in (2, 1)]
+    res = []
+    for use_step in (True, False):
+        eng = api.PagedAttentionEngine()
+        eng.set_graceful_degradation(False)
+        cm = api.KVCacheManager(eng, 64, bs, d, hkv, dtype)
+        for sid in (1, 2):
+            cm.allocate_sequence(sid)
+            assert L.pam_append_tokens_hashed(eng.handle, cm.handle, sid, P, hashes, 3) == 0
+        # sequence 2 shares all three blocks of sequence 1 (prefix hits)
+        assert cm.get_block_table(1) == cm.get_block_table(2)
+        eng._check(L.pam_append_kv(eng.handle, cm.handle, 1, prompt_k.data_ptr(), prompt_v.data_ptr(), 0, P, hkv))
+        outs = []
+        for sid, x in steps:
+            k, v, q = x[0, :hkv].contiguous(), x[1, :hkv].contiguous(), x[2, :H].contiguous()
+            out = torch.empty((H, d), dtype=tdt, device="cuda")
+            if use_step:
+                eng._check(L.pam_decode_step(eng.handle, cm.handle, sid, k.data_ptr(), v.data_ptr(), q.data_ptr(),
+                                             out.data_ptr(), H))
+            else:
+                pos = cm.get_sequence_length(sid)
+                cm.append_tokens(sid, 1)
+                eng._check(L.pam_append_kv(eng.handle, cm.handle, sid, k.data_ptr(), v.data_ptr(), pos, 1, hkv))
+                ids = (C.c_int64 * 1)(sid)
+                eng._check(L.pam_decode(eng.handle, cm.handle, ids, 1, q.data_ptr(), out.data_ptr(), H))
+            outs.append(out)
+        torch.cuda.synchronize()
+        res.append(([o.cpu() for o in outs], cm.k_pool().cpu(), cm.v_pool().cpu(), cm.get_block_table(1),
+                    cm.get_block_table(2), cm.get_sequence_length(2)))
+        L.pam_free_sequence(cm.handle, 1)  # releases the device table
+        cm.close()
+        eng.close()
+    a, b = res
+    assert a[3:] == b[3:] and a[5] == P + 40
+    assert a[3] != a[4]  # the shared tail was copied on write
+    for i, (x, y) in enumerate(zip(a[0], b[0])):
+        assert torch.equal(x, y), f"step {i}"
+    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+    assert all(torch.isfinite(o.float()).all() for o in a[0])
