@@ -612,6 +612,9 @@ def main():
                                 "U[0,3584], causal) + 56 decodes (context U[256,4096]), 32 q / 8 kv heads, "
                                 "d=128, bs=16, fp16, append of the new K/V included in the step",
                     "mixed_step_ms": round(ms3, 5),
+                    "mixed_step_form": "automatic: one launch with the prefill and the decode rows side by side "
+                                       "on CUs of their own when its estimate wins (c3: it does), else separate",
+                    "step_tflops": round(pflops / (ms3 * 1e-3) / 1e12, 2),
                     "tokens_per_s": round(w3.total_rows / (ms3 * 1e-3), 1),
                     "prefill_kernel": "prefill_mfma_kernel<128>", "prefill_kernel_ms": round(pk_ms, 5),
                     "flops_per_launch": pflops, "tflops": round(tflops, 2), "peak_tflops": FP16_PEAK_TFLOPS,

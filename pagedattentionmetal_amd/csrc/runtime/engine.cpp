@@ -1390,16 +1390,52 @@ void Context::mixed_step(const pam_mixed_request &r) {
     pf.num_kv_heads = l.num_kv_heads;
     pf.window = W;
     pf.causal = 1;
-    // One launch for the chunks and the decode rows (mixed.hip), on request: the
-    // prefill's workgroups first, the decode's after them.  The automatic choice
-    // is separate launches (c3 measured 1.6% faster that way with the decode's
-    // one-workgroup-per-CU grid).  The prefill is planned for every CU and the
-    // decode's grid follows it.
-    const bool one_launch = mixed_launch_mode == 2 && !chunks.empty() && ragged_rows > 0 && use_mfma &&
-                            part_tokens_override == 0 &&
-                            mixed_launch_supported(l.data_type, l.head_dim, G, bs, ragged_rows);
-    const int32_t mix_pf_groups = mixed_prefill_groups > 0 ? mixed_prefill_groups : cus_;
-    const int32_t mix_dec_groups = mixed_decode_groups > 0 ? mixed_decode_groups : cus_;
+    // One launch for the chunks and the decode rows (mixed.hip): the prefill's
+    // workgroups first, the decode's after them, on CUs of their own (a
+    // workgroup of either part fills a CU).  The split follows a cost estimate:
+    // the prefill's key tiles (plus the per-item cost of the planner) at
+    // kPfUnitUs per tile per CU, the decode rows' K/V bytes at kDecodeCuGBs per
+    // CU; the decode gets the CUs (a multiple of 8, one per XCD in turn) that
+    // balance the two.  Automatic mode takes it when its estimate beats
+    // separate launches (prefill on every CU, then the decode at the chip's
+    // rate) by 5%.  c3 measured 0.224-0.227 ms with 64-72 decode CUs against
+    // 0.258 ms for separate launches.
+    const bool one_ok = !chunks.empty() && ragged_rows > 0 && use_mfma && part_tokens_override == 0 &&
+                        mixed_launch_supported(l.data_type, l.head_dim, G, bs, ragged_rows);
+    bool one_launch = false;
+    int32_t mix_pf_groups = mixed_prefill_groups, mix_dec_groups = mixed_decode_groups;
+    if (one_ok && mixed_launch_mode != 1) {
+        constexpr double kPfUnitUs = 1.0, kDecodeCuGBs = 40.0, kChipGBs = 5800.0;
+        const int32_t tpw = 256 / G;  // a prefill item: 256 query rows (token, head) of one kv head
+        double units = 0.0;
+        for (const int4 &c : chunks) {
+            const int64_t kv_len = (int64_t)c.y + c.z;
+            const int64_t ws = W > 0 ? std::max<int64_t>(0, kv_len - W) : 0;
+            for (int32_t tok0 = 0; tok0 < c.z; tok0 += tpw) {
+                const int64_t key_end = (int64_t)c.y + std::min(c.z, tok0 + tpw);
+                units += (double)(ceil_div(key_end, 32) - ws / 32 + 12) * l.num_kv_heads;
+            }
+        }
+        double dec_bytes = 0.0;
+        const double row_bytes = (double)l.num_kv_heads * l.head_dim * (l.data_type == kFP8 ? 1 : 2) * 2;
+        for (const int4 &ri : rows) dec_bytes += (double)(ri.z - ri.y) * row_bytes;
+        auto est_one = [&](int32_t dec) {
+            return std::max(units * kPfUnitUs / (cus_ - dec), dec_bytes / (dec * kDecodeCuGBs * 1e3)) + 13.0;
+        };
+        int32_t best = 0;
+        double best_t = 1e300;
+        for (int32_t dec = 8; dec + 8 <= cus_; dec += 8) {
+            const double t = est_one(dec);
+            if (t < best_t) best_t = t, best = dec;
+        }
+        const double t_sep = units * kPfUnitUs / cus_ + dec_bytes / (kChipGBs * 1e3) + 17.0;
+        if (best > 0 && (mixed_launch_mode == 2 || best_t < 0.95 * t_sep)) {
+            one_launch = true;
+            if (mix_dec_groups <= 0) mix_dec_groups = best;
+            if (mix_pf_groups <= 0) mix_pf_groups = cus_ - mix_dec_groups;
+        }
+    }
+    if (one_launch && (mix_pf_groups <= 0 || mix_dec_groups <= 0)) one_launch = false;
     DensePlan dense_plan;
     if (!chunks.empty())
         dense_plan = plan_dense_prefill(pf, chunks.data(), (int32_t)chunks.size(), sl, one_launch ? mix_pf_groups : 0);
