@@ -460,7 +460,8 @@ int32_t pam_engine_mixed_step(void *context, const pam_mixed_request *request);
  *   prefill  pam_prefill_f16_d128, pam_prefill_fused_f16_d128, pam_prefill_e4m3_d128,
  *            pam_mixed_step_{f16,e4m3}_d128
  *   append   pam_append_b{16,4,2}, pam_append_batch_b{16,4,2}, pam_append_fp8
- *   staging  pam_stage_copy;  and pam_fill_u32 for callers' own launches.
+ *   staging  pam_stage_copy;  copy-on-write  pam_block_copy;
+ *   and pam_fill_u32 for callers' own launches.
  * pam_module_load loads one with hipModuleLoad; while it is loaded the context
  * launches every configuration the object holds through hipModuleLaunchKernel
  * (same kernel bodies: the same results bit for bit) and all others (MFMA

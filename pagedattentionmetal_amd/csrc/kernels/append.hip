@@ -121,6 +121,24 @@ hipError_t launch_append_batch(const AppendBatchParams &p, int32_t dtype, hipStr
     return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void block_copy_kernel(uint4 *k_pool, uint4 *v_pool, uint16_t *k_scale,
+                                                         uint16_t *v_scale, int64_t n16, int32_t src, int32_t dst) {
+    block_copy_body(k_pool, v_pool, k_scale, v_scale, n16, src, dst);
+}
+
+hipError_t launch_block_copy(void *k_pool, void *v_pool, uint16_t *k_scale, uint16_t *v_scale, size_t block_bytes,
+                             int32_t src, int32_t dst, hipStream_t stream, const KernelTable *kt) {
+    if (block_bytes % 16 || (((uintptr_t)k_pool | (uintptr_t)v_pool) & 15)) return hipErrorInvalidValue;
+    const int64_t n16 = (int64_t)(block_bytes / 16);
+    const dim3 grid((unsigned)((n16 + 255) / 256));
+    uint4 *k = static_cast<uint4 *>(k_pool), *v = static_cast<uint4 *>(v_pool);
+    hipError_t e;
+    if (via_module(kt, kt ? kt->block_copy : nullptr, &e, grid, dim3(256), stream, k, v, k_scale, v_scale, n16, src, dst))
+        return e;
+    hipLaunchKernelGGL(block_copy_kernel, grid, dim3(256), 0, stream, k, v, k_scale, v_scale, n16, src, dst);
+    return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ codec kernels
 
 __global__ void fp8_quantize_kernel(const uint16_t *values, const uint16_t *scales, uint8_t *out, int64_t n) {

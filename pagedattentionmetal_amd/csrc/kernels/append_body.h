@@ -149,4 +149,20 @@ __device__ __forceinline__ void append_batch_body(const AppendBatchParams &p, in
     }
 }
 
+// Copy-on-write of one physical block: its K and V bytes (n16 16-byte pieces
+// each) from block `src` to block `dst` of the pools, and its FP8 half scales
+// when the pools have them.
+__device__ __forceinline__ void block_copy_body(uint4 *k_pool, uint4 *v_pool, uint16_t *k_scale, uint16_t *v_scale,
+                                                int64_t n16, int32_t src, int32_t dst) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n16) {
+        k_pool[(int64_t)dst * n16 + i] = k_pool[(int64_t)src * n16 + i];
+        v_pool[(int64_t)dst * n16 + i] = v_pool[(int64_t)src * n16 + i];
+    }
+    if (i == 0 && k_scale) {
+        k_scale[dst] = k_scale[src];
+        v_scale[dst] = v_scale[src];
+    }
+}
+
 }  // namespace pam

@@ -99,6 +99,7 @@ struct KernelTable {
     hipFunction_t append_batch[3];
     hipFunction_t append_fp8;     // FP8 quantize-on-append (single sequence and batched)
     hipFunction_t stage;          // staging copy
+    hipFunction_t block_copy;     // copy-on-write of one block
     bool strict;                  // refuse configurations the table lacks
 };
 // hipModuleLaunchKernel of `f` with the kernel arguments `a...` (each passed by
@@ -211,6 +212,11 @@ struct AppendBatchParams {
     int32_t seqs, bt_stride, total_tokens;
     int32_t num_kv_heads, head_dim, block_size;
 };
+// Copy-on-write of one block (block_bytes per pool, a multiple of 16): K and V
+// bytes and, when the scale pointers are set, the FP8 scales, src -> dst.
+// hipErrorInvalidValue for sizes or pools it cannot copy in 16-byte pieces.
+hipError_t launch_block_copy(void *k_pool, void *v_pool, uint16_t *k_scale, uint16_t *v_scale, size_t block_bytes,
+                             int32_t src, int32_t dst, hipStream_t stream, const KernelTable *kt = nullptr);
 hipError_t launch_append_batch(const AppendBatchParams &p, int32_t dtype, hipStream_t stream,
                                const KernelTable *kt = nullptr);
 

@@ -96,6 +96,12 @@ extern "C" __global__ __launch_bounds__(256) void pam_append_fp8(AppendBatchPara
                                                                  int32_t single_offset) {
     append_fp8_body(p, first_lb, single_offset);
 }
+// copy-on-write of one block
+extern "C" __global__ __launch_bounds__(256) void pam_block_copy(uint4 *k_pool, uint4 *v_pool, uint16_t *k_scale,
+                                                                 uint16_t *v_scale, int64_t n16, int32_t src,
+                                                                 int32_t dst) {
+    block_copy_body(k_pool, v_pool, k_scale, v_scale, n16, src, dst);
+}
 // staging copy of per-call metadata from mapped pinned host memory
 extern "C" __global__ __launch_bounds__(256) void pam_stage_copy(const uint4 *__restrict__ src,
                                                                  uint4 *__restrict__ dst, size_t n16,

@@ -271,10 +271,10 @@ PAM_API int32_t pam_decode_step(void *context, void *cache, int64_t sequenceID, 
         try {
             c->alloc.append_tokens(sequenceID, 1, nullptr, 0, &copies);
         } catch (...) {
-            c->copy_blocks(copies, ctx->stream());  // CoW done before an OOM stays done
+            c->copy_blocks(copies, ctx->stream(), ctx->ktab());  // CoW done before an OOM stays done
             throw;
         }
-        c->copy_blocks(copies, ctx->stream());
+        c->copy_blocks(copies, ctx->stream(), ctx->ktab());
         const LogicalSequence &s = c->alloc.sequence(sequenceID);
         const std::vector<int32_t> &t = s.block_table;
         const int32_t nb = (int32_t)t.size(), bs = c->alloc.block_size();
@@ -499,11 +499,11 @@ PAM_API int32_t pam_append_tokens_hashed(void *context, void *cache, int64_t seq
         try {
             c->alloc.append_tokens(sequenceID, count, blockHashes, numHashes, &copies);
         } catch (...) {
-            if (c->has_device) c->copy_blocks(copies, ctx->stream());  // CoW done before an OOM stays done
+            if (c->has_device) c->copy_blocks(copies, ctx->stream(), ctx->ktab());  // CoW done before an OOM stays done
             throw;
         }
         if (c->has_device && !copies.empty()) {
-            c->copy_blocks(copies, ctx->stream());
+            c->copy_blocks(copies, ctx->stream(), ctx->ktab());
             ctx->finish("copy-on-write");
         }
     });
@@ -517,7 +517,7 @@ PAM_API int32_t pam_ensure_exclusive(void *context, void *cache, int64_t sequenc
         BlockCopies copies;
         c->alloc.ensure_exclusive(sequenceID, logicalBlock, &copies);
         if (c->has_device && !copies.empty()) {
-            c->copy_blocks(copies, ctx->stream());
+            c->copy_blocks(copies, ctx->stream(), ctx->ktab());
             ctx->finish("copy-on-write");
         }
     });

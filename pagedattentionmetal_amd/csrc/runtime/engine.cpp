@@ -510,6 +510,7 @@ void Context::module_load(const char *path) {
     }
     t.append_fp8 = get("pam_append_fp8");
     t.stage = get("pam_stage_copy");
+    t.block_copy = get("pam_block_copy");
     t.strict = module_strict_;
     // a stream-K launch is planned for the library kernel's resident grid: an
     // entry with another occupancy would not fit the plan's partial slots

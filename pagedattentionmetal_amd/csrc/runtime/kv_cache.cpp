@@ -70,10 +70,17 @@ size_t KVCache::bytes_per_block() const {
     return (size_t)alloc.block_size() * num_kv_heads * head_dim * elem_size(dtype);
 }
 
-void KVCache::copy_blocks(const BlockCopies &copies, hipStream_t stream) {
+void KVCache::copy_blocks(const BlockCopies &copies, hipStream_t stream, const KernelTable *kt) {
     if (!has_device || copies.empty()) return;
     const size_t bpb = bytes_per_block();
     for (const auto &c : copies) {
+        // one kernel for K, V and the scales; a block whose bytes are not
+        // whole 16-byte pieces goes through the copy engine
+        const hipError_t e = launch_block_copy(k_pool, v_pool, dtype == kFP8 ? k_scale : nullptr,
+                                               dtype == kFP8 ? v_scale : nullptr, bpb, c.first, c.second, stream, kt);
+        if (e == hipSuccess) continue;
+        if (e != hipErrorInvalidValue) hip_check(e, "copy-on-write");
+        (void)hipGetLastError();
         char *k = static_cast<char *>(k_pool), *v = static_cast<char *>(v_pool);
         hip_check(hipMemcpyAsync(k + (size_t)c.second * bpb, k + (size_t)c.first * bpb, bpb, hipMemcpyDeviceToDevice,
                                  stream),

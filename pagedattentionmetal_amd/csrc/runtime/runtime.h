@@ -62,7 +62,7 @@ class KVCache {
 
     size_t bytes_per_block() const;  // one pool (K or V)
     // perform copy-on-write block copies in HBM on the given stream
-    void copy_blocks(const BlockCopies &copies, hipStream_t stream);
+    void copy_blocks(const BlockCopies &copies, hipStream_t stream, const KernelTable *kt = nullptr);
 
     // A sequence's block table and length kept in HBM for the decode step
     // (pam_decode_step): [length | table entries ...], capacity `cap` entries.
