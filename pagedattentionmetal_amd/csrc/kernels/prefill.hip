@@ -96,6 +96,9 @@ constexpr int kSplitCost = 4;
 constexpr int kMinPiece = 8;
 constexpr int kPrefetchCost = 4;  // start-up tiles an item saves when its descriptors were prefetched
 
+// the paired deal is taken when its estimate is at most this times the others'
+constexpr double kPairedSlack = 1.0;
+
 struct PfItem {
     int4 chunk;
     int32_t kvh, tok0, t_lo, t_hi;
@@ -267,12 +270,82 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
             }
             return worst;
         };
-        std::vector<std::vector<int64_t>> sorted_items;
+        // Paired groups: a (chunk, kv head)'s token blocks run side by side, each
+        // on its own workgroup of the XCD, so its K/V streams from HBM about
+        // once for all of them.  Groups are sorted by cost and the heaviest is
+        // paired with the lightest, block i of one with block n - 1 - i of the
+        // other (its heaviest with the other's lightest) on one workgroup, and
+        // each pair's blocks go to the least-loaded workgroups of the XCD.
+        auto deal_paired = [&](std::vector<std::vector<int64_t>> &lists) -> int64_t {
+            lists.assign(groups, {});
+            std::vector<int64_t> load(groups, 0);
+            int64_t worst = 0;
+            for (int32_t x = 0; x < kXcds; x++) {
+                // this XCD's groups: runs of items of one (chunk, kv head), in grid order
+                std::vector<std::vector<int64_t>> grp;
+                for (int64_t it : by_xcd[x]) {
+                    if (grp.empty() || items[grp.back()[0]].chunk.x != items[it].chunk.x ||
+                        items[grp.back()[0]].kvh != items[it].kvh)
+                        grp.emplace_back();
+                    grp.back().push_back(it);
+                }
+                auto gcost = [&](const std::vector<int64_t> &g) {
+                    int64_t c = 0;
+                    for (int64_t it : g) c += cost(it);
+                    return c;
+                };
+                std::stable_sort(grp.begin(), grp.end(),
+                                 [&](const std::vector<int64_t> &a, const std::vector<int64_t> &b) { return gcost(a) > gcost(b); });
+                for (size_t lo = 0, hi = grp.size(); lo < hi; lo++) {
+                    // the pair (lo, hi - 1), or group lo alone when it is the last
+                    std::vector<std::vector<int64_t>> slots(grp[lo].size());
+                    for (size_t i = 0; i < grp[lo].size(); i++) slots[i].push_back(grp[lo][i]);
+                    if (hi - 1 > lo) {
+                        const std::vector<int64_t> &b = grp[--hi];
+                        for (size_t i = 0; i < b.size(); i++) {
+                            const size_t k = slots.size() - 1 - (i % slots.size());
+                            slots[k].push_back(b[i]);
+                        }
+                    }
+                    // the pair's slots onto the least-loaded workgroups of this XCD,
+                    // heaviest slot first
+                    std::stable_sort(slots.begin(), slots.end(), [&](const std::vector<int64_t> &u, const std::vector<int64_t> &v) {
+                        int64_t cu = 0, cv = 0;
+                        for (int64_t it : u) cu += cost(it);
+                        for (int64_t it : v) cv += cost(it);
+                        return cu > cv;
+                    });
+                    for (const auto &sl : slots) {
+                        int32_t best = -1;
+                        for (int32_t i = 0; i < per_xcd; i++) {
+                            const int32_t wgi = i * kXcds + x;
+                            if (best < 0 || load[wgi] < load[best]) best = wgi;
+                        }
+                        for (int64_t it : sl) {
+                            load[best] += cost(it) - (lists[best].empty() ? 0 : kPrefetchCost);
+                            lists[best].push_back(it);
+                        }
+                        worst = std::max(worst, load[best]);
+                    }
+                }
+            }
+            return worst;
+        };
+        std::vector<std::vector<int64_t>> sorted_items, paired_items;
         static_makespan = deal(false, static_items);
         const int64_t sorted_makespan = deal(true, sorted_items);
-        if ((double)sorted_makespan < 0.99 * (double)static_makespan) {
+        const int64_t paired_makespan = deal_paired(paired_items);
+        int deal_pick = 0;  // 0 grid order, 1 longest first, 2 paired groups
+        if ((double)sorted_makespan < 0.99 * (double)static_makespan) deal_pick = 1;
+        const int64_t best_other = deal_pick == 1 ? sorted_makespan : static_makespan;
+        // paired groups keep their L2 sharing: taken when its estimate is no longer
+        if ((double)paired_makespan <= kPairedSlack * (double)best_other) deal_pick = 2;
+        if (deal_pick == 1) {
             static_items.swap(sorted_items);
             static_makespan = sorted_makespan;
+        } else if (deal_pick == 2) {
+            static_items.swap(paired_items);
+            static_makespan = paired_makespan;
         }
     }
 
