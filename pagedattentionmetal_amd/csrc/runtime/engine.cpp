@@ -1430,13 +1430,14 @@ void Context::mixed_step(const pam_mixed_request &r) {
             if (t < best_t) best_t = t, best = dec;
         }
         const double t_sep = units * kPfUnitUs / cus_ + dec_bytes / (kChipGBs * 1e3) + 17.0;
-        if (best > 0 && (mixed_launch_mode == 2 || best_t < 0.95 * t_sep)) {
+        if (mixed_launch_mode == 2 || (best > 0 && best_t < 0.95 * t_sep)) {
             one_launch = true;
-            if (mix_dec_groups <= 0) mix_dec_groups = best;
-            if (mix_pf_groups <= 0) mix_pf_groups = cus_ - mix_dec_groups;
+            // groups not set by the caller: the estimate's split, or (a device
+            // too small to split) every CU for each part, the decode after the prefill
+            if (mix_dec_groups <= 0) mix_dec_groups = best > 0 ? best : cus_;
+            if (mix_pf_groups <= 0) mix_pf_groups = best > 0 ? cus_ - mix_dec_groups : cus_;
         }
     }
-    if (one_launch && (mix_pf_groups <= 0 || mix_dec_groups <= 0)) one_launch = false;
     DensePlan dense_plan;
     if (!chunks.empty())
         dense_plan = plan_dense_prefill(pf, chunks.data(), (int32_t)chunks.size(), sl, one_launch ? mix_pf_groups : 0);
