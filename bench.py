@@ -552,6 +552,12 @@ def main():
     pflops = w3.prefill_flops()
     tflops = pflops / (pk_ms * 1e-3) / 1e12
     log(f"bench: c3 mixed step {ms3:.4f} ms; prefill kernel {pk_ms:.4f} ms = {tflops:.1f} TFLOP/s")
+    # the dense f16 MFMA rate this part sustains at its power-limited clock
+    # (pam_calib_mfma: MFMAs only, one 8-wave workgroup per CU), beside the
+    # published peak the roofline uses
+    e3.calib_mfma(20000)  # untimed: clocks settle over the first milliseconds
+    mfma_ceiling = e3.calib_mfma(60000)
+    log(f"bench: MFMA-only loop {mfma_ceiling:.0f} TFLOP/s")
     cpu3 = None
     if not args.no_cpu:
         threads = max(1, min(16, os.cpu_count() or 1))
@@ -618,7 +624,10 @@ def main():
                     "tokens_per_s": round(w3.total_rows / (ms3 * 1e-3), 1),
                     "prefill_kernel": "prefill_mfma_kernel<128>", "prefill_kernel_ms": round(pk_ms, 5),
                     "flops_per_launch": pflops, "tflops": round(tflops, 2), "peak_tflops": FP16_PEAK_TFLOPS,
-                    "frac": round(tflops / FP16_PEAK_TFLOPS, 4), "cpu_baseline": cpu3},
+                    "frac": round(tflops / FP16_PEAK_TFLOPS, 4),
+                    "mfma_loop_tflops": round(mfma_ceiling, 1),
+                    "frac_of_mfma_loop": round(tflops / mfma_ceiling, 4) if mfma_ceiling > 0 else None,
+                    "cpu_baseline": cpu3},
     }
 
     if args.calibrate:

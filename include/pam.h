@@ -517,6 +517,11 @@ int32_t pam_fp8_dequant(void *context, const uint8_t *codes, const uint16_t *sca
  * accesses by `blocks` workgroups of 256 threads (0 = 4 per CU).  bytes % 16 == 0. */
 int32_t pam_calib_stream_read(void *context, const void *src, size_t bytes, int32_t blocks, float *ms);
 int32_t pam_calib_stream_copy(void *context, const void *src, void *dst, size_t bytes, int32_t blocks, float *ms);
+/* Dense f16 MFMA rate the device sustains (TFLOP/s written to *tflops): one
+ * 8-wave workgroup per CU, each wave iters x 4 v_mfma_f32_32x32x16_f16 on
+ * independent accumulators and nothing else, timed with hipEvents after one
+ * untimed launch.  The power-limited ceiling a matrix-bound kernel is set against. */
+int32_t pam_calib_mfma(void *context, int32_t iters, double *tflops);
 
 /* Synthetic data of the measured workloads (no reference counterpart): n
  * normals N(0, stddev^2) into dst (PAM_FLOAT32 or PAM_FLOAT16), element i from

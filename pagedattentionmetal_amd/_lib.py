@@ -193,6 +193,7 @@ SIGNATURES = {
     "pam_fp8_dequant": (I32, [P, P, P, P, I64]),
     "pam_calib_stream_read": (I32, [P, P, SZ, I32, P]),
     "pam_calib_stream_copy": (I32, [P, P, P, SZ, I32, P]),
+    "pam_calib_mfma": (I32, [P, I32, P]),
     "pam_synth_normal": (I32, [P, P, I32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, C.c_int64, C.c_float]),
     "pam_debug_fail_next_launches": (I32, [P, I32]),
     "pam_debug_dirty_counters": (I32, [P, I32]),

@@ -435,6 +435,12 @@ class PagedAttentionEngine:
         self._check(lib().pam_calib_stream_read(self._ctx, _ptr(src), _nbytes(src), int(blocks), C.byref(ms)))
         return ms.value
 
+    def calib_mfma(self, iters: int = 60000) -> float:
+        """Dense f16 MFMA TFLOP/s the device sustains (pam_calib_mfma)."""
+        t = C.c_double()
+        self._check(lib().pam_calib_mfma(self._ctx, int(iters), C.byref(t)))
+        return t.value
+
     def synth_normal(self, dst, seed: int, stream: int, stddev: float = 1.0, outlier_stream: int = -1,
                      outlier_frac: float = 0.0):
         """Fill a float32 / float16 device tensor with the counter-based normals of

@@ -250,6 +250,9 @@ hipError_t launch_stage_copy(const void *host_mapped, void *dst, size_t bytes, h
 // Calibration streams of known size (achievable HBM rates, counter scaling).
 hipError_t launch_stream_read(const void *src, size_t bytes, uint32_t *sink, int blocks, hipStream_t stream);
 hipError_t launch_stream_copy(const void *src, void *dst, size_t bytes, int blocks, hipStream_t stream);
+// Dense f16 MFMA loop: `blocks` workgroups of 8 waves, each wave `iters` x 4
+// v_mfma_f32_32x32x16_f16 (32768 flops each); sink never written in practice.
+hipError_t launch_mfma_loop(int blocks, int iters, float *sink, hipStream_t stream);
 // Counter-based synthetic normals (synth.hip).
 hipError_t launch_synth_normal(void *dst, int32_t dtype, uint64_t n, uint64_t seed, uint64_t stream, float stddev,
                                int64_t outlier_stream, float outlier_frac, hipStream_t s);

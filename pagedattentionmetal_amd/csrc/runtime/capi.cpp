@@ -848,6 +848,21 @@ struct TimedSpan {
     TimedSpan &operator=(const TimedSpan &) = delete;
 };
 
+PAM_API int32_t pam_calib_mfma(void *context, int32_t iters, double *tflops) {
+    return guarded(context, [&](Context *ctx) {
+        if (iters <= 0 || !tflops) throw invalid_configuration("the MFMA calibration needs iters > 0 and an output.");
+        ctx->ensure_device();
+        const int32_t nb = calib_blocks(0) / 4;  // one 8-wave workgroup per CU
+        float *sink = static_cast<float *>(ctx->device_scratch(5, (size_t)nb * 4));
+        hip_check(launch_mfma_loop(nb, iters, sink, ctx->stream()), "MFMA calibration");  // warm-up
+        TimedSpan span(ctx->stream());
+        const hipError_t e = launch_mfma_loop(nb, iters, sink, ctx->stream());
+        const float t = span.end();
+        hip_check(e, "MFMA calibration");
+        *tflops = t > 0 ? (double)nb * 8 * iters * 4 * 32768.0 / (t * 1e-3) / 1e12 : -1.0;
+    });
+}
+
 PAM_API int32_t pam_calib_stream_read(void *context, const void *src, size_t bytes, int32_t blocks, float *ms) {
     return guarded(context, [&](Context *ctx) {
         ctx->ensure_device();

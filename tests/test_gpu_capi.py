@@ -301,3 +301,15 @@ def test_calibration_streams(torch):
     assert eng.calib_stream_copy(src, dst) > 0
     torch.cuda.synchronize()
     assert torch.equal(src, dst)
+
+
+def test_calibration_mfma_loop(torch):
+    """pam_calib_mfma: the MFMA-only loop's rate is positive and no more than the
+    part's published dense f16 peak (2.5 PFLOP/s); bad arguments are refused."""
+    from pagedattentionmetal_amd import PagedAttentionEngine
+    from pagedattentionmetal_amd.api import PagedAttentionError
+    eng = PagedAttentionEngine()
+    t = eng.calib_mfma(500)
+    assert 100.0 < t <= 2500.0, t
+    with pytest.raises(PagedAttentionError, match="iters"):
+        eng.calib_mfma(0)
