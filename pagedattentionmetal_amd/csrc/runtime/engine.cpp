@@ -1152,6 +1152,9 @@ void Context::backward(const pam_backward_request &r) {
         !r.d_v_pool)
         throw invalid_configuration("backward request has a null buffer.");
     ensure_device();
+    // refused before any work or retry: the same request would be refused again
+    if (ktab() && ktab()->strict)
+        throw PamError("Unsupported paged attention path: the backward kernels are not in the code object.");
     BackwardParams p{};
     p.q = r.q;
     p.k_pool = r.k_pool;
@@ -1176,8 +1179,6 @@ void Context::backward(const pam_backward_request &r) {
     p.row_c = p.row_d + (int64_t)r.seq_len * l.num_heads;
     with_retry("backward", [&] {
         mark(ev0_);
-        if (ktab() && ktab()->strict)
-            throw PamError("Unsupported paged attention path: the backward kernels are not in the code object.");
         check_launch([&] { return launch_backward(p, l.data_type, stream()); }, "backward");
         mark(ev1_);
         finish("backward");
