@@ -5,6 +5,7 @@
 // pool (kernels.metal:693-917 semantics: scale 1/sqrt(d), GQA head h reads kv
 // head h / G, a fixed window start max(0, kv_len - W) for every row).
 //
+// Head sizes 64 and 128 (f16 or e4m3 pools); the layouts are in prefill_body.h.
 // Matrix work runs on v_mfma_f32_32x32x16_f16, which on gfx950 retires twice
 // the flops per cycle of the 16x16 shapes.  A workgroup (8 waves, two per SIMD)
 // owns 256 query rows of one kv head: the (token, head) pairs of 256 / G
@@ -46,7 +47,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void prefill_mfma_kernel(Att
 }
 
 bool prefill_mfma_supported(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size) {
-    return (dtype == kF16 || dtype == kFP8) && head_dim == 128 && group >= 1 && group <= 32 &&
+    return (dtype == kF16 || dtype == kFP8) && (head_dim == 128 || head_dim == 64) && group >= 1 && group <= 32 &&
            (kPrefillRows % group) == 0 && block_size > 0 && (block_size & (block_size - 1)) == 0;
 }
 
@@ -59,11 +60,17 @@ hipError_t launch_prefill_mfma(const AttnParams &p_in, int32_t dtype, hipStream_
     const dim3 grid(p.pf_groups), block(64 * kPrefillWaves);
     if (dtype == kFP8 && (p.fuse_k != nullptr || p.k_scale == nullptr || p.v_scale == nullptr))
         return hipErrorInvalidValue;
-    hipError_t e;  // the code object's entry of this configuration, when it has one
-    if (via_module(kt, kt ? kt->prefill[dtype == kFP8 ? 2 : (p.fuse_k != nullptr ? 1 : 0)] : nullptr, &e, grid, block,
-                   stream, p))
-        return e;
-    if (dtype == kFP8) {
+    hipError_t e;  // the code object's entry of this configuration, when it has one (d = 128 only)
+    hipFunction_t f = kt && p.head_dim == 128 ? kt->prefill[dtype == kFP8 ? 2 : (p.fuse_k != nullptr ? 1 : 0)] : nullptr;
+    if (via_module(kt, f, &e, grid, block, stream, p)) return e;
+    if (p.head_dim == 64) {
+        if (dtype == kFP8)
+            hipLaunchKernelGGL((prefill_mfma_kernel<64, kPrefillRB, false, uint8_t>), grid, block, 0, stream, p);
+        else if (p.fuse_k != nullptr)
+            hipLaunchKernelGGL((prefill_mfma_kernel<64, kPrefillRB, true, f16>), grid, block, 0, stream, p);
+        else
+            hipLaunchKernelGGL((prefill_mfma_kernel<64, kPrefillRB, false, f16>), grid, block, 0, stream, p);
+    } else if (dtype == kFP8) {
         hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, false, uint8_t>), grid, block, 0, stream, p);
     } else if (p.fuse_k != nullptr) {
         hipLaunchKernelGGL((prefill_mfma_kernel<128, kPrefillRB, true, f16>), grid, block, 0, stream, p);

@@ -21,16 +21,24 @@ constexpr int kBtCache = 2048;                 // block-table entries a workgrou
 constexpr int kXcds = 8;                       // accelerator dies (each with its own L2)
 
 
-// LDS tiles (layouts checked against SQ_LDS_BANK_CONFLICT on gfx950).
-// K: rows of 128 + 8 halves, so the 16 consecutive rows one 16-lane pass of an
-// operand load touches fall on 16 distinct 16-byte bank groups.
-// V: rows of 128 halves, 16-byte piece p of row r stored at p ^ 4*(r%4): the 4
-// rows x 64 bytes of each 32-lane pass of a transposed load cover all banks once.
-constexpr int kPrefillKL = 128 + 8;
-constexpr int kPrefillVL = 128;
-__device__ __forceinline__ int k_lds_at(int key, int piece) { return key * kPrefillKL + (piece << 3); }
+// LDS tiles for head size HD (layouts checked against SQ_LDS_BANK_CONFLICT on
+// gfx950 at d = 128).
+// K: rows of HD + 8 halves (an odd number of 16-byte units), so the 16
+// consecutive rows one 16-lane pass of an operand load touches fall on 16
+// distinct 16-byte bank groups.
+// V: rows of HD halves with 16-byte piece p of row r stored at p ^ s(r), so the
+// 4 rows x 64 bytes of each 32-lane pass of a transposed load cover all banks
+// once: s(r) = 4 (r % 4) for 256-byte rows (d = 128); for 128-byte rows
+// (d = 64), rows r and r + 1 already fall on opposite bank halves and
+// s(r) = 4 ((r / 2) % 2) separates r from r + 2.
+template <int HD>
+constexpr int pf_kl() { return HD + 8; }
+template <int HD>
+__device__ __forceinline__ int k_lds_at(int key, int piece) { return key * pf_kl<HD>() + (piece << 3); }
+template <int HD>
 __device__ __forceinline__ int v_lds_at(int key, int piece) {
-    return key * kPrefillVL + ((piece ^ ((key & 3) << 2)) << 3);
+    const int sw = HD == 128 ? (key & 3) << 2 : ((key >> 1) & 1) << 2;
+    return key * HD + ((piece ^ sw) << 3);
 }
 
 // three-way maximum (v_maximum3_f32); scores are never NaN
@@ -43,23 +51,28 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
     // KV: f16 pools, or e4m3 codes (uint8_t) with a half scale per physical block
     constexpr bool FP8 = sizeof(KV) == 1;
     static_assert(!(FUSED && FP8), "the fused append is f16 only");
-    static_assert(HD == 128, "layouts assume d = 128");
+    static_assert(HD == 128 || HD == 64, "layouts for d = 64 and 128");
+    constexpr int KL = pf_kl<HD>(), VL = HD;
     constexpr int KT = kPrefillKT;
     constexpr int KH = KT / 32;       // 32-key score blocks per tile
     constexpr int DC = HD / 16;       // 16-wide d chunks (S operands)
     constexpr int DT = HD / 32;       // 32-wide output dim tiles
     constexpr int PIECES = HD / 8;    // 16-byte pieces per token row
     constexpr int THREADS = 64 * kPrefillWaves;
-    constexpr int KEYS_PER_PASS = THREADS / PIECES;  // 16 lanes per key row
+    // staging: a thread loads one 16-byte piece of K and of V for each of its
+    // keys (d = 128: 16 lanes per key row); at d = 64 the threads outnumber a
+    // tile's K pieces twice, so the first half stages K and the second V
+    constexpr bool SPLIT = THREADS / PIECES >= 2 * KT;
+    constexpr int KEYS_PER_PASS = SPLIT ? KT : THREADS / PIECES;
     constexpr int KPT = KT / KEYS_PER_PASS;          // keys per thread per tile
     constexpr int ROWS = 32 * RB * kPrefillWaves;
-    static_assert(KT % KEYS_PER_PASS == 0 && KPT <= 2, "whole keys per thread");
+    static_assert(KT % KEYS_PER_PASS == 0 && KPT <= 2 && (!SPLIT || THREADS / PIECES == 2 * KT), "whole keys per thread");
     // the K and V rings in one array: after a segment's tile loop the whole of
     // it holds the waves' output rows on their way to memory (finish, below)
-    constexpr int kRingK = kPrefillBufs * KT * kPrefillKL, kRingV = kPrefillBufs * KT * kPrefillVL;
+    constexpr int kRingK = kPrefillBufs * KT * KL, kRingV = kPrefillBufs * KT * VL;
     __shared__ __attribute__((aligned(16))) f16 ring_lds[kRingK + kRingV];
-    f16(*k_lds)[KT * kPrefillKL] = reinterpret_cast<f16(*)[KT * kPrefillKL]>(ring_lds);
-    f16(*v_lds)[KT * kPrefillVL] = reinterpret_cast<f16(*)[KT * kPrefillVL]>(ring_lds + kRingK);
+    f16(*k_lds)[KT * KL] = reinterpret_cast<f16(*)[KT * KL]>(ring_lds);
+    f16(*v_lds)[KT * VL] = reinterpret_cast<f16(*)[KT * VL]>(ring_lds + kRingK);
     static_assert(RB == 1 && kPrefillWaves * 32 * HD <= kRingK + kRingV, "one 32-row output tile per wave in the ring");
     __shared__ int32_t bt_lds[kBtCache];
 
@@ -158,17 +171,20 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
             for (int c = 0; c < DC; c++) qv[b][c] = *reinterpret_cast<const f16x8 *>(qp + 16 * c);
         }
 
-        // staging map: thread -> piece tid % 16 of keys tid / 16 (+ THREADS / 16)
-        // (16 lanes read one key row's 256 contiguous bytes)
-        const int my_piece = tid % PIECES, my_key = tid / PIECES;
+        // staging map: thread -> piece tid % PIECES of keys tid / PIECES (+
+        // THREADS / PIECES) (PIECES lanes read one key row's contiguous bytes);
+        // SPLIT: key (tid / PIECES) % KT of K (first half) or V (second half)
+        const bool vhalf = SPLIT && tid >= THREADS / 2;
+        const int my_piece = tid % PIECES, my_key = (tid / PIECES) % (SPLIT ? KT : THREADS);
         const uint32_t row_stride = (uint32_t)(p.num_kv_heads * HD);  // halves per pool row (< 2^32)
-        const KV *kpool = static_cast<const KV *>(p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
+        const KV *kpool = static_cast<const KV *>(vhalf ? p.v_pool : p.k_pool) + (int64_t)kvh * HD + my_piece * 8;
         const KV *vpool = static_cast<const KV *>(p.v_pool) + (int64_t)kvh * HD + my_piece * 8;
         // fused append: rows of the chunk's new tokens have the pools' row stride;
         // a load of one adds the (uniform) distance from the pool to the input
         // (in halves; both buffers hold f16, so the byte distance is even)
-        const int64_t kin_d = FUSED ? (int64_t)((uintptr_t)p.fuse_k - (uintptr_t)p.k_pool) / 2 : 0;
         const int64_t vin_d = FUSED ? (int64_t)((uintptr_t)p.fuse_v - (uintptr_t)p.v_pool) / 2 : 0;
+        const int64_t kin_d = FUSED ? (vhalf ? vin_d : (int64_t)((uintptr_t)p.fuse_k - (uintptr_t)p.k_pool) / 2) : 0;
+        const uint16_t *kscale = FP8 ? (vhalf ? p.v_scale : p.k_scale) : nullptr;
         // two register sets in flight: a tile's rows are loaded two iterations
         // before they are written to LDS.  A thread's piece of a row is 8
         // elements: 16 bytes of f16, or 8 e4m3 codes plus the block's scales.
@@ -181,6 +197,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
         int blk0 = 0;  // first block of the block-table segment held in bt_lds
         const int32_t *bt_seg = bt_lds;  // bt_lds - blk0: indexed by logical block
         // pool row of this thread's key(s) of a tile, then the loads from it
+        // (SPLIT: the thread's one piece, of K or of V, goes to r.k)
         auto lookup = [&](int tile, uint32_t(&slot)[KPT]) {
 #pragma unroll
             for (int i = 0; i < KPT; i++) {
@@ -202,6 +219,17 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
 #pragma unroll
             for (int i = 0; i < KPT; i++) {
                 const uint32_t row = slot[i] & 0x7FFFFFFFu;
+                if constexpr (SPLIT) {
+                    const uint64_t off = (uint64_t)row * row_stride;
+                    if constexpr (FP8) {
+                        r.k[i] = *reinterpret_cast<const uint2 *>(kpool + off);
+                        r.ks[i] = kscale[row >> bsh];
+                    } else {
+                        const bool in = FUSED && (slot[i] >> 31);
+                        r.k[i] = *reinterpret_cast<const f16x8 *>(kpool + off + (in ? kin_d : 0));
+                    }
+                    continue;
+                }
                 if constexpr (!FP8 && !FUSED) {
                     const char *ka = (const char *)kpool + (uint64_t)row * row_bytes;
                     r.k[i] = *reinterpret_cast<const f16x8 *>(ka);
@@ -229,12 +257,21 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
         int k_st[KPT], v_st[KPT];
 #pragma unroll
         for (int i = 0; i < KPT; i++) {
-            k_st[i] = k_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
-            v_st[i] = v_lds_at(my_key + i * KEYS_PER_PASS, my_piece);
+            k_st[i] = k_lds_at<HD>(my_key + i * KEYS_PER_PASS, my_piece);
+            v_st[i] = v_lds_at<HD>(my_key + i * KEYS_PER_PASS, my_piece);
         }
         auto stage = [&](int buf, const Regs &r) {
 #pragma unroll
             for (int i = 0; i < KPT; i++) {
+                if constexpr (SPLIT) {
+                    f16 *dst = ring_lds + (vhalf ? kRingK + buf * KT * VL + v_st[i] : buf * KT * KL + k_st[i]);
+                    if constexpr (FP8)
+                        *reinterpret_cast<f16x8 *>(dst) =
+                            e4m3x8_to_f16x8(r.k[i].x, r.k[i].y) * (f16x8)bits_to_f16((uint16_t)r.ks[i]);
+                    else
+                        *reinterpret_cast<f16x8 *>(dst) = r.k[i];
+                    continue;
+                }
                 if constexpr (FP8) {
                     // exact code values times the block scale in one binary16
                     // multiply: the reference's half dequantisation, as in decode
@@ -250,7 +287,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
         };
 
         // S^T: A operand of chunk c = K[key n][16c + 8h .. +7], shared by the row blocks
-        const int k_rd = k_lds_at(n, h);
+        const int k_rd = k_lds_at<HD>(n, h);
         auto score = [&](int buf, f32x16(&sc)[RB][KH]) {
             const f16 *kt = k_lds[buf];
 #pragma unroll
@@ -259,7 +296,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                 for (int b = 0; b < RB; b++) sc[b][e] = (f32x16)0.0f;
 #pragma unroll
                 for (int c = 0; c < DC; c++) {
-                    const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * kPrefillKL + 16 * c]);
+                    const f16x8 ka = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * KL + 16 * c]);
 #pragma unroll
                     for (int b = 0; b < RB; b++)
                         sc[b][e] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[b][c], sc[b][e], 0, 0, 0);
@@ -276,7 +313,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
             const int row = 4 * h + (o >> 2);
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
-                v_rd[dt] = v_lds_at(row, 4 * dt + 2 * hh + ((o & 3) >> 1)) + 4 * (o & 1);
+                v_rd[dt] = v_lds_at<HD>(row, 4 * dt + 2 * hh + ((o & 3) >> 1)) + 4 * (o & 1);
         }
 
         // lmax: the tile's raw row max (score units); m_thr: the score above which
@@ -418,7 +455,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                     for (int e = 0; e < KH; e++)
 #pragma unroll
                         for (int c = 0; c < DC; c++)
-                            ka[e][c] = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * kPrefillKL + 16 * c]);
+                            ka[e][c] = *reinterpret_cast<const f16x8 *>(&kt[k_rd + 32 * e * KL + 16 * c]);
                 }
                 lookup(min(seg + t + 4, seg_end - 1), nslot);
                 if (__any(prepare(seg + t, sacc))) rescale();
@@ -462,8 +499,8 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                 for (int c = 0; c < 2 * KH; c++)
 #pragma unroll
                     for (int dt = 0; dt < DT; dt++) {
-                        const f16x4 lo = lds_read_tr16(vt + v_rd[dt] + 16 * c * kPrefillVL);
-                        const f16x4 hi = lds_read_tr16(vt + v_rd[dt] + (16 * c + 8) * kPrefillVL);
+                        const f16x4 lo = lds_read_tr16(vt + v_rd[dt] + 16 * c * VL);
+                        const f16x4 hi = lds_read_tr16(vt + v_rd[dt] + (16 * c + 8) * VL);
                         va[c][dt] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                     }
                 if (t + 1 < T) {
@@ -545,7 +582,7 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
         // and writes the rows.  The counter carries the launch's epoch
         // (arrive_count), so it is never reset.
         if (wb.z > 1) {
-            static_assert(kPrefillSlotBytes == (int64_t)kPrefillWaves * 64 * RB * (16 * DT + 2) * 4, "slot size");
+            static_assert(kPrefillSlotBytes >= (int64_t)kPrefillWaves * 64 * RB * (16 * DT + 2) * 4, "slot size");
             const __amdgpu_buffer_rsrc_t prs =
                 __builtin_amdgcn_make_buffer_rsrc(p.pf_part, 0, (int)p.pf_part_bytes, 0x00020000);
             constexpr int NQ = RB * DT * 4;  // 16-byte pieces of O^T per lane
@@ -605,10 +642,10 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
 
         // finish: O / l (l summed over the two lane halves) into the wave's
         // 32-row slice of the ring, idle since every wave left the tile loop
-        // (the barrier after it), then out as whole rows: 16 lanes store one
-        // 256-byte row with 16-byte stores, where the accumulator layout would
-        // have each store instruction touch 32 rows.  Row r's 16-byte piece p
-        // sits at p ^ (r % 16), so neither side's LDS accesses conflict.
+        // (the barrier after it), then out as whole rows: PIECES lanes store one
+        // row with 16-byte stores, where the accumulator layout would have each
+        // store instruction touch 32 rows.  Row r's 16-byte piece p sits at
+        // p ^ (r % PIECES), so neither side's LDS accesses conflict.
         // A row with no key in range (window past the row) is 0/0, as the
         // reference's m/l bookkeeping gives.
         {
@@ -628,12 +665,13 @@ __device__ __forceinline__ void prefill_body(const AttnParams &p) {
                     f16x4 v;
 #pragma unroll
                     for (int r2 = 0; r2 < 4; r2++) v[r2] = (f16)(o[0][dt][4 * q + r2] * inv);
-                    *reinterpret_cast<f16x4 *>(ot + on * HD + (((4 * dt + q) ^ (on & 15)) << 3) + 4 * oh) = v;
+                    *reinterpret_cast<f16x4 *>(ot + on * HD + (((4 * dt + q) ^ (on & (PIECES - 1))) << 3) + 4 * oh) = v;
                 }
+            constexpr int RPP = 64 / PIECES;  // rows per 64-lane pass
 #pragma unroll
-            for (int i = 0; i < 32 / 4; i++) {
-                const int rl = 4 * i + (ln >> 4), pc = ln & 15;
-                const f16x8 v = *reinterpret_cast<const f16x8 *>(ot + rl * HD + ((pc ^ (rl & 15)) << 3));
+            for (int i = 0; i < 32 / RPP; i++) {
+                const int rl = RPP * i + ln / PIECES, pc = ln % PIECES;
+                const f16x8 v = *reinterpret_cast<const f16x8 *>(ot + rl * HD + ((pc ^ (rl & (PIECES - 1))) << 3));
                 const int rr = wave * 32 + rl, tk = tok0 + rr / G;
                 if (tk < tok_end)
                     *reinterpret_cast<f16x8 *>(static_cast<f16 *>(p.out) +

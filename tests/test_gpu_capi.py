@@ -189,7 +189,8 @@ def test_gpu_timing_switch(torch):
     (1, 32, 8, 128, 16, 200, True, 64),  # fixed window start
     (1, 32, 16, 128, 32, 1000, True, 0),  # one-kernel fused path, items split over workgroups
     (1, 8, 8, 128, 16, 150, False, 0),   # one-kernel fused path, G = 1, full attention
-    (1, 16, 4, 64, 8, 77, True, 0),      # row kernels, bs 8
+    (1, 16, 4, 64, 8, 77, True, 0),      # d = 64 dense kernel, bs 8
+    (1, 32, 8, 64, 16, 300, True, 0),    # d = 64 dense kernel, one-kernel fused path
     (2, 32, 8, 128, 16, 100, True, 0),   # FP8: quantise on append, dequantise in attention
 ])
 def test_fused_prefill_equals_append_then_prefill(torch, dtype, H, hkv, d, bs, T, causal, window):

@@ -302,6 +302,14 @@ PREFILL_CASES = [
     (200, 64, 64, 8, 128, 32, 2, True, 100),  # G = 8, window cuts inside the chunk
     (130, 0, 16, 1, 128, 8, 2, True, 0),      # G = 16, bs 8
     (77, 5, 8, 8, 128, 16, 2, False, 0),      # G = 1, full attention
+    # the same dense kernel at d = 64 (f16 and e4m3; K and V staged by separate thread halves)
+    (300, 1000, 32, 8, 64, 16, 1, True, 0),
+    (130, 0, 16, 1, 64, 16, 1, True, 0),      # G = 16
+    (77, 5, 8, 8, 64, 16, 1, False, 0),       # G = 1, full attention
+    (200, 64, 64, 8, 64, 32, 1, True, 100),   # G = 8, window cuts inside the chunk
+    (40, 9000, 8, 2, 64, 4, 1, True, 0),      # bs 4: block table in segments
+    (300, 1000, 32, 8, 64, 16, 2, True, 0),
+    (130, 0, 16, 1, 64, 8, 2, True, 0),       # G = 16, bs 8
 ]
 
 
@@ -333,13 +341,14 @@ def test_prefill_parity(engine, case):
 
 
 @pytest.mark.gpu
-def test_dense_prefill_split_repeatable(engine):
+@pytest.mark.parametrize("d", [128, 64])
+def test_dense_prefill_split_repeatable(engine, d):
     """The dense prefill kernel cuts long items into pieces merged in the kernel
     (partial slots and counters): the merge order is fixed, so repeated calls give
     the same bits, and a call of another shape in between changes nothing."""
     import torch
     rng = np.random.default_rng(77)
-    H, hkv, d, bs, T, off = 32, 8, 128, 16, 700, 2500
+    H, hkv, bs, T, off = 32, 8, 16, 700, 2500
     q, k, v, bt, _ = make_case(rng, 1, H, hkv, d, bs, 1, [off + T])
     q = rng.standard_normal((T, H, d)).astype(np.float16)
     kd, vd, qd, btd = to_dev(k), to_dev(v), to_dev(q), to_dev(bt[0])
