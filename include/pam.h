@@ -217,7 +217,7 @@ int32_t pam_engine_prefill(void *context, const pam_prefill_request *request);
 /* PagedAttentionEngine.appendToCache(_:) (PagedAttentionEngine.swift:585-597) */
 int32_t pam_engine_append(void *context, const pam_append_request *request);
 /* PagedAttentionEngine.fusedPrefill(_:) (PagedAttentionEngine.swift:633-710): append
- * and prefill as one call on the context's stream.  f16 caches with head_dim 128
+ * and prefill as one call on the context's stream.  f16 caches with head_dim 64 or 128
  * run one kernel that reads the new keys and values from raw_k / raw_v and writes
  * them into the pools; other shapes and dtypes append first, then attend.  The
  * pools end up equal to a separate append in every case. */
@@ -457,7 +457,7 @@ int32_t pam_engine_mixed_step(void *context, const pam_mixed_request *request);
  *   decode   pam_decode_streamk_{f16,e4m3}_d128, pam_decode_layers_streamk_{f16,e4m3}_d128,
  *            pam_decode_wg_{f16,e4m3}_d128, pam_decode_valu_{f32,f16,e4m3}_h{1,2,4,8},
  *            pam_reduce_{f32,f16}
- *   prefill  pam_prefill_f16_d128, pam_prefill_fused_f16_d128, pam_prefill_e4m3_d128,
+ *   prefill  pam_prefill_{f16,fused_f16,e4m3}_d128, pam_prefill_{f16,fused_f16,e4m3}_d64,
  *            pam_mixed_step_{f16,e4m3}_d128
  *   append   pam_append_b{16,4,2}, pam_append_batch_b{16,4,2}, pam_append_fp8
  *   staging  pam_stage_copy;  copy-on-write  pam_block_copy;

@@ -91,7 +91,7 @@ struct AttnParams {
 struct KernelTable {
     hipFunction_t streamk[2][2];  // decode stream-K, d = 128, blocks >= 16: [f16, e4m3][one layer, fused layers]
     hipFunction_t mfma_wg[2];     // decode, workgroup form (rows > 2048), d = 128, blocks >= 16: f16, e4m3
-    hipFunction_t prefill[3];     // dense prefill, d = 128: f16, f16 with fused append, e4m3
+    hipFunction_t prefill[2][3];  // dense prefill, [d = 128, d = 64][f16, f16 with fused append, e4m3]
     hipFunction_t mixed[2];       // one-launch mixed step: f16, e4m3
     hipFunction_t valu[3][4];     // VALU rows: [f32, f16, e4m3 KV][1, 2, 4, 8 heads per wave]
     hipFunction_t reduce[2];      // split-context reduce: f32, f16 outputs

@@ -60,8 +60,9 @@ hipError_t launch_prefill_mfma(const AttnParams &p_in, int32_t dtype, hipStream_
     const dim3 grid(p.pf_groups), block(64 * kPrefillWaves);
     if (dtype == kFP8 && (p.fuse_k != nullptr || p.k_scale == nullptr || p.v_scale == nullptr))
         return hipErrorInvalidValue;
-    hipError_t e;  // the code object's entry of this configuration, when it has one (d = 128 only)
-    hipFunction_t f = kt && p.head_dim == 128 ? kt->prefill[dtype == kFP8 ? 2 : (p.fuse_k != nullptr ? 1 : 0)] : nullptr;
+    hipError_t e;  // the code object's entry of this configuration, when it has one
+    hipFunction_t f =
+        kt ? kt->prefill[p.head_dim == 64 ? 1 : 0][dtype == kFP8 ? 2 : (p.fuse_k != nullptr ? 1 : 0)] : nullptr;
     if (via_module(kt, f, &e, grid, block, stream, p)) return e;
     if (p.head_dim == 64) {
         if (dtype == kFP8)

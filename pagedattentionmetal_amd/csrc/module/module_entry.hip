@@ -29,9 +29,9 @@ namespace pam {
         __shared__ float sm_ml[kMfmaWaves][16][2];                                                    \
         mfma_item<KV, 128, kBlkTile>(p, blockIdx.z, blockIdx.x, blockIdx.y, smem, sm_ml);             \
     }
-#define PAM_PREFILL_ENTRY(NAME, FUSED, KV)                                                   \
+#define PAM_PREFILL_ENTRY(NAME, HD, FUSED, KV)                                               \
     extern "C" __global__ __launch_bounds__(64 * kPrefillWaves, 1) void NAME(AttnParams p) { \
-        prefill_body<128, kPrefillRB, FUSED, KV>(p);                                          \
+        prefill_body<HD, kPrefillRB, FUSED, KV>(p);                                           \
     }
 #define PAM_MIXED_ENTRY(NAME, KV)                                                            \
     extern "C" __global__ __launch_bounds__(64 * kPrefillWaves, 1) void NAME(AttnParams p) { \
@@ -77,10 +77,13 @@ PAM_VALU_ENTRY(pam_decode_valu_e4m3_h8, uint8_t, f16, 8)
 // split-context reduce, by output type
 extern "C" __global__ __launch_bounds__(256) void pam_reduce_f32(AttnParams p) { reduce_body<float>(p); }
 extern "C" __global__ __launch_bounds__(256) void pam_reduce_f16(AttnParams p) { reduce_body<f16>(p); }
-// dense chunked prefill, d = 128
-PAM_PREFILL_ENTRY(pam_prefill_f16_d128, false, f16)
-PAM_PREFILL_ENTRY(pam_prefill_fused_f16_d128, true, f16)
-PAM_PREFILL_ENTRY(pam_prefill_e4m3_d128, false, uint8_t)
+// dense chunked prefill, d = 128 and d = 64
+PAM_PREFILL_ENTRY(pam_prefill_f16_d128, 128, false, f16)
+PAM_PREFILL_ENTRY(pam_prefill_fused_f16_d128, 128, true, f16)
+PAM_PREFILL_ENTRY(pam_prefill_e4m3_d128, 128, false, uint8_t)
+PAM_PREFILL_ENTRY(pam_prefill_f16_d64, 64, false, f16)
+PAM_PREFILL_ENTRY(pam_prefill_fused_f16_d64, 64, true, f16)
+PAM_PREFILL_ENTRY(pam_prefill_e4m3_d64, 64, false, uint8_t)
 // one-launch mixed step
 PAM_MIXED_ENTRY(pam_mixed_step_f16_d128, f16)
 PAM_MIXED_ENTRY(pam_mixed_step_e4m3_d128, uint8_t)

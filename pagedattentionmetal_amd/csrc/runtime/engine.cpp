@@ -489,9 +489,12 @@ void Context::module_load(const char *path) {
     t.streamk[1][0] = get("pam_decode_streamk_e4m3_d128");
     t.streamk[0][1] = get("pam_decode_layers_streamk_f16_d128");
     t.streamk[1][1] = get("pam_decode_layers_streamk_e4m3_d128");
-    t.prefill[0] = get("pam_prefill_f16_d128");
-    t.prefill[1] = get("pam_prefill_fused_f16_d128");
-    t.prefill[2] = get("pam_prefill_e4m3_d128");
+    t.prefill[0][0] = get("pam_prefill_f16_d128");
+    t.prefill[0][1] = get("pam_prefill_fused_f16_d128");
+    t.prefill[0][2] = get("pam_prefill_e4m3_d128");
+    t.prefill[1][0] = get("pam_prefill_f16_d64");
+    t.prefill[1][1] = get("pam_prefill_fused_f16_d64");
+    t.prefill[1][2] = get("pam_prefill_e4m3_d64");
     t.mfma_wg[0] = get("pam_decode_wg_f16_d128");
     t.mfma_wg[1] = get("pam_decode_wg_e4m3_d128");
     t.mixed[0] = get("pam_mixed_step_f16_d128");

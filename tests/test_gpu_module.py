@@ -186,3 +186,41 @@ def test_module_strict_runs_c1_and_c3_from_the_code_object():
     assert row_rel_err(mod["c1"].astype(np.float64), ref) <= TOL[0]
     ref = oracle.decode(1, qw, kw, vw, btw, lw, 16, n_threads=8)
     assert row_rel_err(mod["wg"].astype(np.float64), ref) <= TOL[1]
+
+
+def test_module_strict_d64_prefill_bit_identical():
+    """The code object's d = 64 prefill entries (f16, e4m3) give the library
+    kernel's bits in a strict module-bound engine."""
+    import torch
+    rng = np.random.default_rng(6464)
+    H, hkv, d, bs, T, off = 16, 4, 64, 16, 300, 700
+    for dtype in (1, 2):
+        q, k, v, bt, _ = make_case(rng, 1, H, hkv, d, bs, 1, [off + T])
+        qp = to_dev(rng.standard_normal((T, H, d)).astype(np.float16))
+        outs = []
+        for module in (False, True):
+            e = _engine(module)
+            if module:
+                e.set_module_strict(True)
+            kd, vd, ks, vs = to_dev(k), to_dev(v), None, None
+            if dtype == 2:
+                # quantise the same f16 rows into e4m3 pools through the append
+                nb = k.shape[0]
+                kd = torch.zeros((nb, bs, hkv, d), dtype=torch.uint8, device="cuda")
+                vd = torch.zeros_like(kd)
+                ks = torch.zeros(nb, dtype=torch.float16, device="cuda")
+                vs = torch.zeros_like(ks)
+                tok = np.arange(off + T)
+                kr = to_dev(k[bt[0, tok // bs], tok % bs])
+                vr = to_dev(v[bt[0, tok // bs], tok % bs])
+                e.append_to_cache(kr, vr, kd, vd, to_dev(bt[0]), 0, off + T, _spec(hkv, hkv, d, bs, 2), k_scale=ks,
+                                  v_scale=vs)
+            o = torch.zeros((T, H, d), dtype=torch.float16, device="cuda")
+            e.prefill(qp, kd, vd, to_dev(bt[0]), o, T, _spec(H, hkv, d, bs, dtype), causal=True, q_offset=off,
+                      k_scale=ks, v_scale=vs)
+            outs.append(to_host(o))
+            e.close()
+        assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16)), dtype
+        if dtype == 1:
+            ref = oracle.prefill(1, to_host(qp), k, v, bt[0], off, causal=True, n_threads=8)
+            assert row_rel_err(outs[0].astype(np.float64), ref) <= TOL[1]
