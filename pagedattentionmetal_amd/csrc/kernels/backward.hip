@@ -229,24 +229,6 @@ __device__ __forceinline__ void to_chunks(const bw_f32x16 &v, f16x8 (&out)[2]) {
     for (int r = 0; r < 16; r++) out[r >> 3][r & 7] = (f16)v[r];
 }
 
-// 16 bytes per lane from global memory straight into LDS: lane L of the wave
-// writes lds_base + 16 L (global_load_lds_dwordx4, counted by vmcnt).  With 4
-// bytes, lane L writes lds_base + 4 L; inactive lanes write nothing.  Issued
-// as inline assembly so that the compiler, which does not see these LDS writes,
-// adds no wait for them before unrelated LDS reads: the rings below order them
-// with explicit vmcnt waits and barriers (ring_barrier).
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p);
-}
-__device__ __forceinline__ void lds_dma16(const void *g, const void *lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr(lds_base)), "v"(g)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void lds_dma4(const void *g, const void *lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_addr(lds_base)), "v"(g)
-                 : "memory", "m0");
-}
-
 // Workgroup barrier for the LDS rings: this wave's LDS reads and all but its
 // last `N` loads are complete, then every wave arrives.  A __syncthreads would
 // not do: the compiler does not count the inline-assembly loads, so it emits

@@ -33,6 +33,24 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
     return __builtin_bit_cast(f16x4, v);
 }
 
+// 16 bytes per lane from global memory straight into LDS: lane L of the wave
+// writes lds_base + 16 L (global_load_lds_dwordx4, counted by vmcnt).  With 4
+// bytes, lane L writes lds_base + 4 L; inactive lanes write nothing.  Issued
+// as inline assembly so that the compiler, which does not see these LDS writes,
+// adds no wait for them before unrelated LDS reads: their users order them with
+// explicit vmcnt waits and barriers.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p);
+}
+__device__ __forceinline__ void lds_dma16(const void *g, const void *lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr(lds_base)), "v"(g)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void *g, const void *lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_addr(lds_base)), "v"(g)
+                 : "memory", "m0");
+}
+
 __device__ __forceinline__ f16 bits_to_f16(uint16_t b) { return __builtin_bit_cast(f16, b); }
 __device__ __forceinline__ uint16_t f16_to_bits(f16 h) { return __builtin_bit_cast(uint16_t, h); }
 
