@@ -332,8 +332,18 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
                         "-byte scratch.");
     };
     // a partition length set through pam_set_partition_tokens selects the
-    // partitioned form
-    if (use_mfma && part_tokens_override == 0 && mfma_streamk_plan(p, dtype, &slots, &counters)) {
+    // partitioned form.  So do few (row, kv head) pairs with long contexts:
+    // there the stream-K form's last unit of a pair merges many partials one
+    // batch after another, where fixed partitions, split over a workgroup's
+    // waves and merged by the reduce kernel, keep every step short.  Measured
+    // on gfx950 (32/8 heads, f16, µs per call, stream-K -> partitions):
+    //   1 row:  2K tokens 20.8 -> 14.5, 4K 23.8 -> 15.1, 16K 43.5 -> 27.2, 64K 87.6 -> 65.9
+    //   2 rows: 4K 24.3 -> 16.3, 16K 49.2 -> 44.0, 64K 99.1 -> 103.2
+    //   4 rows: 2K 22.1 -> 16.3, 4K 27.6 -> 25.1, 16K 56.6 -> 58.9, 64K 168 -> 201
+    const int64_t pairs = (int64_t)p.rows * p.num_kv_heads;
+    const bool few_pairs = p.fused_layers <= 1 && max_tiles >= 128 &&
+                           (pairs <= 8 || (pairs <= 16 && max_tiles <= 2048) || (pairs <= 32 && max_tiles <= 256));
+    if (use_mfma && part_tokens_override == 0 && !few_pairs && mfma_streamk_plan(p, dtype, &slots, &counters)) {
         p.part_tokens = (int32_t)(max_tiles * 16);
         p.max_parts = 1;
         const int64_t bytes = slots * ((int64_t)p.head_dim + 2) * 4;

@@ -230,6 +230,30 @@ def test_decode_streamk_repeatable(engine):
                 assert np.array_equal(got.view(np.uint16), first[i].view(np.uint16)), f"shape {i} not repeatable"
 
 
+@pytest.mark.parametrize("dtype,B,lens", [(1, 1, [4096]), (1, 2, [2500, 7000]), (2, 1, [3000]), (1, 4, [900, 4000, 17, 2048])])
+def test_decode_few_rows_long_context_partitions(engine, dtype, B, lens):
+    """Few (row, kv head) pairs with long contexts run as fixed partitions split
+    over a workgroup's waves plus the reduce kernel (the stream-K form's merge
+    would serialise): parity with the oracle, f16 and e4m3."""
+    import torch
+    rng = np.random.default_rng(93 + B + dtype)
+    H, hkv, d, bs = 32, 8, 128, 16
+    q, k, v, bt, lens = make_case(rng, B, H, hkv, d, bs, dtype, lens)
+    ks = vs = None
+    if dtype == 2:
+        kd, vd, ksd, vsd, kp, vp, ks, vs = build_fp8(engine, rng, k, v, bt, lens, hkv, d, bs)
+    else:
+        kd, vd, ksd, vsd = to_dev(k), to_dev(v), None, None
+        kp, vp = k, v
+    out = torch.zeros((B, H, d), dtype=torch.float16, device="cuda")
+    engine.decode(to_dev(q), kd, vd, to_dev(bt), to_dev(lens), out, B, bt.shape[1], layer(H, hkv, d, bs, dtype),
+                  k_scale=ksd, v_scale=vsd)
+    ref = oracle.decode(dtype, q, kp, vp, bt, lens, H, k_scale=None if ks is None else ks.view(np.uint16),
+                        v_scale=None if vs is None else vs.view(np.uint16), n_threads=8)
+    err = row_rel_err(to_host(out), ref)
+    assert err <= TOL[dtype], f"rel err {err:.3e}"
+
+
 def test_decode_mfma_many_rows_workgroup_form(engine):
     """More rows than the stream-K form indexes: the workgroup form plus reduce."""
     import torch
