@@ -502,15 +502,16 @@ def test_mixed_step_parity(engine, dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("seed,H,hkv,bs,window", [(1, 32, 8, 16, 0), (2, 16, 8, 8, 0), (3, 32, 4, 16, 700),
-                                                  (4, 64, 8, 32, 0)])
-def test_mixed_step_random_ragged_chunks(engine, seed, H, hkv, bs, window):
+@pytest.mark.parametrize("seed,H,hkv,bs,window,d", [(1, 32, 8, 16, 0, 128), (2, 16, 8, 8, 0, 128),
+                                                    (3, 32, 4, 16, 700, 128), (4, 64, 8, 32, 0, 128),
+                                                    (5, 32, 8, 16, 0, 64), (6, 16, 4, 8, 300, 64)])
+def test_mixed_step_random_ragged_chunks(engine, seed, H, hkv, bs, window, d):
     """Many ragged f16 prefill chunks (2..600 new tokens after 0..2500 cached ones)
     beside decode rows: the dense prefill's work list cuts the larger items into
-    pieces merged in the kernel.  Every row is checked against the oracle."""
+    pieces merged in the kernel (d = 128 and d = 64).  Every row is checked
+    against the oracle."""
     import torch
     rng = np.random.default_rng(900 + seed)
-    d = 128
     nch, ndec = 10, 5
     ctx = np.concatenate([rng.integers(0, 2501, nch), rng.integers(1, 2000, ndec)]).astype(np.int32)
     ql = np.concatenate([rng.integers(2, 601, nch), np.ones(ndec)]).astype(np.int32)
