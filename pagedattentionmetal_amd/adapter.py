@@ -86,6 +86,14 @@ class PagedTorchKVCache:
         self.cache_manager.allocate_sequence(self.sequence_id)
         self.offset = 0
         self._step = api.lib().pam_decode_step
+        # the decode step's shapes and type ([1, H, 1, d] queries, [1, Hkv, 1, d]
+        # keys and values): calls with exactly these take the short path of
+        # paged_attention
+        import torch
+        self._io = torch.float32 if layer.data_type == PagedAttentionDataType.float32 else torch.float16
+        self._q1 = torch.Size([1, layer.num_heads, 1, layer.head_dim])
+        self._kv1 = torch.Size([1, layer.num_kv_heads, 1, layer.head_dim])
+        self._short = layer.data_type != PagedAttentionDataType.float8
 
     # metaState (PagedMetalKVCache.swift:158-167)
     @property
@@ -116,6 +124,22 @@ class PagedTorchKVCache:
             if cur_stream != self._stream:
                 self.engine.set_stream(cur_stream)
                 self._stream = cur_stream
+        io = self._io
+        if (self._short and isinstance(mask, str) and (mask == "none" or mask == "causal") and
+                queries.shape == self._q1 and keys.shape == self._kv1 and values.shape == self._kv1 and
+                queries.dtype == io and keys.dtype == io and values.dtype == io and queries.is_contiguous() and
+                keys.is_contiguous() and values.is_contiguous()):
+            # a decode step in one library call (pam_decode_step): bookkeeping,
+            # the token's K/V append and the decode; the block table and length
+            # stay on the device between steps.  [1, heads, 1, d] holds the same
+            # bytes as [heads, d].
+            out = torch.empty(self._q1, dtype=io, device=queries.device)
+            rc = self._step(self.engine.handle, self.cache_manager.handle, self.sequence_id, keys.data_ptr(),
+                            values.data_ptr(), queries.data_ptr(), out.data_ptr(), self.layer.num_heads)
+            if rc != 0:
+                self.engine._check(rc)
+            self.offset += 1
+            return out
         if _is_tensor_mask(mask):
             raise UnsupportedMask("materialized masks fall back to native attention")
         if mask not in ("none", "causal"):
@@ -135,7 +159,6 @@ class PagedTorchKVCache:
             if t.shape[1] != L.num_kv_heads or t.shape[2] != S or t.shape[3] != L.head_dim:
                 raise UnsupportedShape(f"keys/values must match seqLen={S}, kvHeads={L.num_kv_heads}, "
                                        f"headDim={L.head_dim}.")
-        io = torch.float32 if L.data_type == PagedAttentionDataType.float32 else torch.float16
         cm = self.cache_manager
         cur = self.offset
         if S == 1 and L.data_type != PagedAttentionDataType.float8:
