@@ -33,7 +33,6 @@
 // to the MFMA in f16; the common case needs no cross-lane reduction.
 #include <algorithm>
 #include <functional>
-#include <queue>
 
 #include "prefill_body.h"
 
@@ -176,6 +175,9 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
     constexpr int KT = kPrefillKT;
     const int32_t G = p.num_heads / p.num_kv_heads, tpw = kPrefillRows / G;
     std::vector<PfItem> items;
+    int64_t n_items = 0;
+    for (int32_t c = 0; c < n; c++) n_items += (int64_t)p.num_kv_heads * ((chunks[c].z + tpw - 1) / tpw);
+    items.reserve(n_items);
     int64_t total = 0;
     for (int32_t c = 0; c < n; c++) {
         const int4 ch = chunks[c];
@@ -216,8 +218,8 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
     std::vector<int64_t> grid_item(grid_ids, -1);
     int64_t grid_makespan = 0;
     {
-        std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> cu;
-        for (int32_t i = 0; i < groups; i++) cu.push(0);
+        // each CU's finish time, a binary min-heap (all 0 to start)
+        std::vector<int64_t> cu(groups, 0);
         for (int64_t b = 0; b < grid_ids; b++) {
             const int64_t xcd = b % kXcds, r = b / kXcds;
             const int64_t grp = xcd + kXcds * (r / nx);
@@ -227,10 +229,19 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
             if (tb >= nb) continue;
             const int64_t it = item_base[c] + (int64_t)kvh * nb + tb;
             grid_item[b] = it;
-            const int64_t t = cu.top() + items[it].t_hi - items[it].t_lo + kSegCost;
-            cu.pop();
-            cu.push(t);
+            const int64_t t = cu[0] + items[it].t_hi - items[it].t_lo + kSegCost;
             grid_makespan = std::max(grid_makespan, t);
+            for (int32_t i = 0;;) {  // the earliest CU takes it: sift its new time down
+                const int32_t l = 2 * i + 1, r = l + 1;
+                int32_t m = l < groups && cu[l] < t ? l : -1;
+                if (r < groups && cu[r] < t && cu[r] < cu[l]) m = r;
+                if (m < 0) {
+                    cu[i] = t;
+                    break;
+                }
+                cu[i] = cu[m];
+                i = m;
+            }
         }
     }
 
@@ -248,32 +259,64 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
     //    group's blocks end up apart and lose their shared L2 (measured 12%
     //    slower on 64 chunks of one context length), so it is taken only when
     //    its estimate is at least 1% shorter.
-    std::vector<std::vector<int64_t>> static_items;
+    // the chosen deal's items, workgroup by workgroup in the order dealt:
+    // workgroup b's are static_items[static_off[b] .. static_off[b + 1])
+    std::vector<int64_t> static_items;
+    std::vector<int32_t> static_off;
     int64_t static_makespan = INT64_MAX;
     if (groups % kXcds == 0 && grid_ids <= INT32_MAX) {
         const int32_t per_xcd = groups / kXcds;
         std::vector<std::vector<int64_t>> by_xcd(kXcds);
         for (int64_t b = 0; b < grid_ids; b++)
             if (grid_item[b] >= 0) by_xcd[b % kXcds].push_back(grid_item[b]);
-        auto cost = [&](int64_t it) { return (int64_t)items[it].t_hi - items[it].t_lo + kSegCost; };
-        auto deal = [&](bool sorted, std::vector<std::vector<int64_t>> &lists) -> int64_t {
-            lists.assign(groups, {});
+        std::vector<int64_t> icost(items.size());
+        for (size_t i = 0; i < items.size(); i++) icost[i] = (int64_t)items[i].t_hi - items[i].t_lo + kSegCost;
+        // The deals below return their estimated makespan; with `trace` they
+        // also record each (workgroup, item) in the order dealt (workgroup i of
+        // XCD x is i * 8 + x).
+        // A deal onto the least-loaded workgroup takes the lowest index among
+        // equals.
+        std::vector<int64_t> load(groups);
+        std::vector<int32_t> cnt(groups);
+        // the XCD's workgroups in a binary min-heap on (load, workgroup)
+        std::vector<int32_t> heap(per_xcd);
+        auto before = [&](int32_t a, int32_t b) { return load[a] < load[b] || (load[a] == load[b] && a < b); };
+        auto heap_init = [&](int32_t x) {
+            for (int32_t i = 0; i < per_xcd; i++) heap[i] = i * kXcds + x;  // all loads 0: already a heap
+        };
+        auto sift_down = [&]() {  // the top's load grew
+            int32_t i = 0;
+            for (;;) {
+                const int32_t l = 2 * i + 1, r = l + 1;
+                int32_t m = i;
+                if (l < per_xcd && before(heap[l], heap[m])) m = l;
+                if (r < per_xcd && before(heap[r], heap[m])) m = r;
+                if (m == i) return;
+                std::swap(heap[i], heap[m]);
+                i = m;
+            }
+        };
+        std::vector<std::pair<int32_t, int64_t>> dealt;
+        auto put = [&](int32_t wg, int64_t it, bool trace) {
+            load[wg] += icost[it] - (cnt[wg] ? kPrefetchCost : 0);
+            cnt[wg]++;
+            if (trace) dealt.emplace_back(wg, it);
+        };
+        std::vector<int64_t> seq;
+        auto deal = [&](bool sorted, bool trace) -> int64_t {
+            std::fill(load.begin(), load.end(), 0);
+            std::fill(cnt.begin(), cnt.end(), 0);
             int64_t worst = 0;
             for (int32_t x = 0; x < kXcds; x++) {
-                std::vector<int64_t> seq = by_xcd[x];
+                seq = by_xcd[x];
                 if (sorted)
-                    std::stable_sort(seq.begin(), seq.end(), [&](int64_t a, int64_t b) { return cost(a) > cost(b); });
-                using Load = std::pair<int64_t, int32_t>;  // (estimated load, workgroup on this XCD)
-                std::priority_queue<Load, std::vector<Load>, std::greater<Load>> wg;
-                for (int32_t i = 0; i < per_xcd; i++) wg.push({0, i});
+                    std::stable_sort(seq.begin(), seq.end(), [&](int64_t a, int64_t b) { return icost[a] > icost[b]; });
+                heap_init(x);
                 for (int64_t it : seq) {
-                    Load l = wg.top();
-                    wg.pop();
-                    std::vector<int64_t> &list = lists[(int64_t)l.second * kXcds + x];
-                    l.first += cost(it) - (list.empty() ? 0 : kPrefetchCost);
-                    list.push_back(it);
-                    worst = std::max(worst, l.first);
-                    wg.push(l);
+                    const int32_t wg = heap[0];
+                    put(wg, it, trace);
+                    sift_down();
+                    worst = std::max(worst, load[wg]);
                 }
             }
             return worst;
@@ -284,77 +327,74 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
         // paired with the lightest, block i of one with block n - 1 - i of the
         // other (its heaviest with the other's lightest) on one workgroup, and
         // each pair's blocks go to the least-loaded workgroups of the XCD.
-        auto deal_paired = [&](std::vector<std::vector<int64_t>> &lists) -> int64_t {
-            lists.assign(groups, {});
-            std::vector<int64_t> load(groups, 0);
+        std::vector<int32_t> gstart, gorder, sorder;
+        std::vector<int64_t> gcost, scost;
+        auto deal_paired = [&](bool trace) -> int64_t {
+            std::fill(load.begin(), load.end(), 0);
+            std::fill(cnt.begin(), cnt.end(), 0);
             int64_t worst = 0;
             for (int32_t x = 0; x < kXcds; x++) {
                 // this XCD's groups: runs of items of one (chunk, kv head), in grid order
-                std::vector<std::vector<int64_t>> grp;
-                for (int64_t it : by_xcd[x]) {
-                    if (grp.empty() || items[grp.back()[0]].chunk.x != items[it].chunk.x ||
-                        items[grp.back()[0]].kvh != items[it].kvh)
-                        grp.emplace_back();
-                    grp.back().push_back(it);
-                }
-                auto gcost = [&](const std::vector<int64_t> &g) {
-                    int64_t c = 0;
-                    for (int64_t it : g) c += cost(it);
-                    return c;
-                };
-                std::stable_sort(grp.begin(), grp.end(),
-                                 [&](const std::vector<int64_t> &a, const std::vector<int64_t> &b) { return gcost(a) > gcost(b); });
-                for (size_t lo = 0, hi = grp.size(); lo < hi; lo++) {
-                    // the pair (lo, hi - 1), or group lo alone when it is the last
-                    std::vector<std::vector<int64_t>> slots(grp[lo].size());
-                    for (size_t i = 0; i < grp[lo].size(); i++) slots[i].push_back(grp[lo][i]);
-                    if (hi - 1 > lo) {
-                        const std::vector<int64_t> &b = grp[--hi];
-                        for (size_t i = 0; i < b.size(); i++) {
-                            const size_t k = slots.size() - 1 - (i % slots.size());
-                            slots[k].push_back(b[i]);
-                        }
+                const std::vector<int64_t> &xs = by_xcd[x];
+                gstart.clear();
+                gcost.clear();
+                for (size_t i = 0; i < xs.size(); i++) {
+                    if (i == 0 || items[xs[i - 1]].chunk.x != items[xs[i]].chunk.x ||
+                        items[xs[i - 1]].kvh != items[xs[i]].kvh) {
+                        gstart.push_back((int32_t)i);
+                        gcost.push_back(0);
                     }
+                    gcost.back() += icost[xs[i]];
+                }
+                const int32_t ng = (int32_t)gstart.size();
+                heap_init(x);
+                gstart.push_back((int32_t)xs.size());
+                gorder.resize(ng);
+                for (int32_t g = 0; g < ng; g++) gorder[g] = g;
+                std::stable_sort(gorder.begin(), gorder.end(), [&](int32_t a, int32_t b) { return gcost[a] > gcost[b]; });
+                for (int32_t lo = 0, hi = ng; lo < hi; lo++) {
+                    // the pair (lo, hi - 1), or group lo alone when it is the last;
+                    // slot k holds block k of group lo, then the blocks i of the
+                    // other with n - 1 - (i mod n) = k
+                    const int32_t ga = gorder[lo], na = gstart[ga + 1] - gstart[ga];
+                    const int32_t gb = hi - 1 > lo ? gorder[--hi] : -1;
+                    const int32_t nb = gb < 0 ? 0 : gstart[gb + 1] - gstart[gb];
+                    scost.assign(na, 0);
+                    for (int32_t k = 0; k < na; k++) scost[k] = icost[xs[gstart[ga] + k]];
+                    for (int32_t i = 0; i < nb; i++) scost[na - 1 - (i % na)] += icost[xs[gstart[gb] + i]];
                     // the pair's slots onto the least-loaded workgroups of this XCD,
                     // heaviest slot first
-                    std::stable_sort(slots.begin(), slots.end(), [&](const std::vector<int64_t> &u, const std::vector<int64_t> &v) {
-                        int64_t cu = 0, cv = 0;
-                        for (int64_t it : u) cu += cost(it);
-                        for (int64_t it : v) cv += cost(it);
-                        return cu > cv;
-                    });
-                    for (const auto &sl : slots) {
-                        int32_t best = -1;
-                        for (int32_t i = 0; i < per_xcd; i++) {
-                            const int32_t wgi = i * kXcds + x;
-                            if (best < 0 || load[wgi] < load[best]) best = wgi;
-                        }
-                        for (int64_t it : sl) {
-                            load[best] += cost(it) - (lists[best].empty() ? 0 : kPrefetchCost);
-                            lists[best].push_back(it);
-                        }
-                        worst = std::max(worst, load[best]);
+                    sorder.resize(na);
+                    for (int32_t k = 0; k < na; k++) sorder[k] = k;
+                    std::stable_sort(sorder.begin(), sorder.end(), [&](int32_t u, int32_t v) { return scost[u] > scost[v]; });
+                    for (int32_t k : sorder) {
+                        const int32_t wg = heap[0];
+                        put(wg, xs[gstart[ga] + k], trace);
+                        for (int32_t i = na - 1 - k; i < nb; i += na) put(wg, xs[gstart[gb] + i], trace);
+                        sift_down();
+                        worst = std::max(worst, load[wg]);
                     }
                 }
             }
             return worst;
         };
-        std::vector<std::vector<int64_t>> sorted_items, paired_items;
-        static_makespan = deal(false, static_items);
-        const int64_t sorted_makespan = deal(true, sorted_items);
-        const int64_t paired_makespan = deal_paired(paired_items);
+        static_makespan = deal(false, false);
+        const int64_t sorted_makespan = deal(true, false);
+        const int64_t paired_makespan = deal_paired(false);
         int deal_pick = 0;  // 0 grid order, 1 longest first, 2 paired groups
         if ((double)sorted_makespan < 0.99 * (double)static_makespan) deal_pick = 1;
         const int64_t best_other = deal_pick == 1 ? sorted_makespan : static_makespan;
         // paired groups keep their L2 sharing: taken when its estimate is no longer
         if ((double)paired_makespan <= kPairedSlack * (double)best_other) deal_pick = 2;
-        if (deal_pick == 1) {
-            static_items.swap(sorted_items);
-            static_makespan = sorted_makespan;
-        } else if (deal_pick == 2) {
-            static_items.swap(paired_items);
-            static_makespan = paired_makespan;
-        }
+        // the chosen deal again, recording it, then its items grouped by
+        // workgroup (a counting sort keeps each workgroup's order dealt)
+        dealt.reserve(items.size());
+        static_makespan = deal_pick == 2 ? deal_paired(true) : deal(deal_pick == 1, true);
+        static_off.assign(groups + 1, 0);
+        for (int32_t b = 0; b < groups; b++) static_off[b + 1] = static_off[b] + cnt[b];
+        static_items.resize(dealt.size());
+        std::vector<int32_t> fill(static_off.begin(), static_off.end() - 1);
+        for (const auto &d : dealt) static_items[fill[d.first]++] = d.second;
     }
 
     // smallest capacity that fits the line into `groups` workgroups
@@ -372,8 +412,8 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
         out.range.assign(groups, make_int2(0, 0));
         for (int32_t b = 0; b < groups; b++) {
             const int32_t first = (int32_t)(out.work.size() / 3);
-            for (int64_t i : static_items[b]) {
-                const PfItem &it = items[i];
+            for (int32_t k = static_off[b]; k < static_off[b + 1]; k++) {
+                const PfItem &it = items[static_items[k]];
                 out.work.push_back(it.chunk);
                 out.work.push_back(make_int4(it.kvh, it.tok0, it.t_lo, it.t_hi));
                 out.work.push_back(make_int4(0, 0, 1, 0));
