@@ -167,10 +167,11 @@ __device__ __forceinline__ uint32_t arrive_count(uint64_t *counter, uint32_t epo
     using g64 = __attribute__((address_space(1))) uint64_t;
     g64 *c = (g64 *)counter;
     const uint64_t tag = (uint64_t)epoch << 32;
-    // raise a stale counter to (epoch, 0); a current one is already above tag
-    const uint64_t seen = __hip_atomic_fetch_max(c, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the maximum has returned (it is applied) before the add is issued
-    asm volatile("s_waitcnt vmcnt(0)" ::"v"(seen) : "memory");
+    // raise a stale counter to (epoch, 0); a current one is already above tag.
+    // The add is issued without waiting for the maximum: two atomics of one
+    // thread on one location are applied in program order (same-location
+    // coherence; a wave's requests to one address share one L2 channel queue).
+    (void)__hip_atomic_fetch_max(c, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t old = __hip_atomic_fetch_add(c, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // no load of the published data may be moved above the count
     __atomic_signal_fence(__ATOMIC_SEQ_CST);

@@ -63,12 +63,28 @@ __device__ __forceinline__ void valu_body(const AttnParams &p, int lanes_per_row
     const int G = H / p.num_kv_heads;
     const int h0 = hg * NH;
     const int kvh = h0 / G;
+    const int LPR = lanes_per_row, TPI = 64 / lanes_per_row;
+    const int sub = lane / LPR;
+    constexpr int UB = kValuBatch;
+    // A decode row without a window starts its keys at token 0, so the first
+    // batch's block-table entries are known before the row's length: they are
+    // requested beside it.  The index is clamped into the row's max_num_blocks
+    // entries; only entries of tokens below the length are used, and those lie
+    // below the clamp.
+    const bool early_bt = p.mode == kRowDecode && p.window <= 0 && p.max_num_blocks > 0;
+    int32_t bt_first[UB];
+    if (early_bt) {
+        const int32_t *bt_row = p.block_tables + (int64_t)r * p.bt_stride;
+#pragma unroll
+        for (int u = 0; u < UB; u++) {
+            const int idx = (part * p.part_tokens + u * TPI + sub) / p.block_size;
+            bt_first[u] = bt_row[idx < p.max_num_blocks ? idx : p.max_num_blocks - 1];
+        }
+    }
     const RowCtx c = row_ctx(p, r);
     const PartRange pr = part_range(c, part, p.part_tokens);
     if (part >= (pr.nparts > 1 ? pr.nparts : 1)) return;
 
-    const int LPR = lanes_per_row, TPI = 64 / lanes_per_row;
-    const int sub = lane / LPR;
     const int d0 = (lane % LPR) * 4;
     const bool dim_ok = d0 < HD;
     QT *out = static_cast<QT *>(p.out);
@@ -104,15 +120,15 @@ __device__ __forceinline__ void valu_body(const AttnParams &p, int lanes_per_row
     // Tokens go in batches of kValuBatch steps of TPI tokens: the block-table
     // entries of a batch are requested together, then its K/V slices, so a batch
     // waits on two memory latencies; one online-softmax update covers the batch.
-    constexpr int UB = kValuBatch;
-    for (int j0 = pr.t_begin * 16; j0 < pr.t_end * 16; j0 += UB * TPI) {
+    // one batch at token j0; bte: the block-table entries of its steps
+    auto batch = [&](const int j0, const int32_t (&bte)[UB]) {
         bool ok[UB];
         int64_t phys[UB];
 #pragma unroll
         for (int u = 0; u < UB; u++) {
             const int j = j0 + u * TPI + sub;
             ok[u] = j >= c.k_lo && j < c.k_hi && j < pr.t_end * 16;
-            phys[u] = ok[u] ? (int64_t)c.bt[j / bs] : 0;
+            phys[u] = ok[u] ? (int64_t)bte[u] : 0;
         }
         float kv[UB][4], vv[UB][4];
 #pragma unroll
@@ -163,6 +179,20 @@ __device__ __forceinline__ void valu_body(const AttnParams &p, int lanes_per_row
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[hh][e] = a4[e];
         }
+    };
+    int j0 = pr.t_begin * 16;
+    if (early_bt && j0 < pr.t_end * 16) {
+        batch(j0, bt_first);
+        j0 += UB * TPI;
+    }
+    for (; j0 < pr.t_end * 16; j0 += UB * TPI) {
+        int32_t bte[UB];
+#pragma unroll
+        for (int u = 0; u < UB; u++) {
+            const int j = j0 + u * TPI + sub;
+            bte[u] = j >= c.k_lo && j < c.k_hi && j < pr.t_end * 16 ? c.bt[j / bs] : 0;
+        }
+        batch(j0, bte);
     }
 
 #pragma unroll
@@ -216,21 +246,42 @@ __device__ __forceinline__ void valu_body(const AttnParams &p, int lanes_per_row
             before = arrive_count(p.seg_count + (int64_t)r * (H / NH) + hg, p.epoch);
         before = __builtin_amdgcn_readfirstlane(before);
         if (before != (uint32_t)(pr.nparts - 1)) return;
+        // the first kMergeCache partitions' partials are loaded with the maxima,
+        // so a short row's merge waits on one memory latency, not two
+        constexpr int kMergeCache = 16;
         for (int hh = 0; hh < NH; hh++) {
             float M = -INFINITY;
-            for (int pt = 0; pt < pr.nparts; pt++) {
+            f32x2 mlc[kMergeCache];
+            f32x4 vc[kMergeCache];
+#pragma unroll
+            for (int pt = 0; pt < kMergeCache; pt++) {
+                if (pt < pr.nparts) {
+                    const int64_t slot = slot_of(hh, pt);
+                    mlc[pt] = __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)(slot * 8), 0, kSc1);
+                    vc[pt] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)((slot * HD + d0) * 4), 0, kSc1);
+                }
+            }
+#pragma unroll
+            for (int pt = 0; pt < kMergeCache; pt++)
+                if (pt < pr.nparts) M = fmaxf(M, mlc[pt][0]);
+            for (int pt = kMergeCache; pt < pr.nparts; pt++) {
                 const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)(slot_of(hh, pt) * 8), 0, kSc1);
                 M = fmaxf(M, ml[0]);
             }
             float den = 0.0f, a[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int pt = 0; pt < pr.nparts; pt++) {
-                const int64_t slot = slot_of(hh, pt);
-                const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)(slot * 8), 0, kSc1);
-                const f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)((slot * HD + d0) * 4), 0, kSc1);
+            auto fold = [&](const f32x2 ml, const f32x4 v) {
                 const float w = ml[0] == -INFINITY ? 0.0f : exp2f(ml[0] - M);
                 den += w * ml[1];
 #pragma unroll
                 for (int e = 0; e < 4; e++) a[e] += w * v[e];
+            };
+#pragma unroll
+            for (int pt = 0; pt < kMergeCache; pt++)
+                if (pt < pr.nparts) fold(mlc[pt], vc[pt]);
+            for (int pt = kMergeCache; pt < pr.nparts; pt++) {
+                const int64_t slot = slot_of(hh, pt);
+                fold(__builtin_amdgcn_raw_buffer_load_b64(prs, ml_off + (int)(slot * 8), 0, kSc1),
+                     __builtin_amdgcn_raw_buffer_load_b128(prs, (int)((slot * HD + d0) * 4), 0, kSc1));
             }
             const float inv = 1.0f / den;
 #pragma unroll
