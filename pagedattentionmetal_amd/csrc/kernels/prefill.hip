@@ -102,6 +102,7 @@ constexpr int kSegCost = 12;
 constexpr int kSplitCost = 4;
 constexpr int kMinPiece = 8;
 constexpr int kPrefetchCost = 4;  // start-up tiles an item saves when its descriptors were prefetched
+static_assert(kSegCost > kPrefetchCost, "every item costs more than its prefetch credit");
 
 // the paired deal is taken when its estimate is at most this times the others'
 constexpr double kPairedSlack = 1.0;
@@ -395,6 +396,80 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
         static_items.resize(dealt.size());
         std::vector<int32_t> fill(static_off.begin(), static_off.end() - 1);
         for (const auto &d : dealt) static_items[fill[d.first]++] = d.second;
+        // With few items per workgroup (at most 4 on average) dealing onto the
+        // least-loaded workgroup leaves slack, so a local search follows: the
+        // most-loaded workgroup of an XCD gives one of its items to another
+        // workgroup of the XCD, or swaps it for a shorter one there, taking the
+        // change that lowers the larger of the two loads the most, until no
+        // change lowers it.  Items stay on their XCD.
+        // Lists are kept at most kCap items per workgroup (no move into a full one).
+        constexpr int32_t kCap = 16;
+        bool fits = (int64_t)dealt.size() <= 4 * (int64_t)groups && per_xcd > 1;
+        for (int32_t b = 0; fits && b < groups; b++) fits = cnt[b] <= kCap;
+        if (fits) {
+            std::vector<int64_t> wl((size_t)groups * kCap);
+            std::vector<int32_t> wn(groups);
+            for (int32_t b = 0; b < groups; b++) {
+                wn[b] = cnt[b];
+                std::copy(static_items.begin() + static_off[b], static_items.begin() + static_off[b + 1], wl.begin() + (size_t)b * kCap);
+            }
+            auto at = [&](int32_t b, int32_t k) -> int64_t & { return wl[(size_t)b * kCap + k]; };
+            bool moved = false;
+            for (int32_t x = 0; x < kXcds; x++) {
+                for (int32_t iter = 0; iter < 4 * per_xcd; iter++) {
+                    int32_t A = x;
+                    for (int32_t b = x + kXcds; b < groups; b += kXcds)
+                        if (load[b] > load[A]) A = b;
+                    const int64_t LA = load[A];
+                    int64_t best = LA;
+                    int32_t bk = -1, bB = -1, bj = -1;  // item k of A to workgroup B (for its item j; -1: a move)
+                    for (int32_t k = 0; k < wn[A]; k++) {
+                        const int64_t a = icost[at(A, k)];
+                        const int64_t la_mv = LA - a + (wn[A] > 1 ? kPrefetchCost : 0);
+                        for (int32_t B = x; B < groups; B += kXcds) {
+                            const int64_t LB = load[B];
+                            // a move or swap leaves B above LB (items cost more than
+                            // the prefetch credit; a swap takes a shorter item)
+                            if (B == A || LB + 1 >= best) continue;
+                            if (wn[B] < kCap) {
+                                const int64_t mv = std::max(la_mv, LB + a - (wn[B] ? kPrefetchCost : 0));
+                                if (mv < best) best = mv, bk = k, bB = B, bj = -1;
+                            }
+                            for (int32_t j = 0; j < wn[B]; j++) {
+                                const int64_t c = icost[at(B, j)];
+                                if (c >= a) continue;
+                                const int64_t sw = std::max(LA - a + c, LB - c + a);
+                                if (sw < best) best = sw, bk = k, bB = B, bj = j;
+                            }
+                        }
+                    }
+                    if (bk < 0) break;
+                    const int64_t it = at(A, bk);
+                    if (bj < 0) {  // A's items close up; the item joins B's end
+                        for (int32_t k = bk; k + 1 < wn[A]; k++) at(A, k) = at(A, k + 1);
+                        wn[A]--;
+                        load[A] -= icost[it] - (wn[A] ? kPrefetchCost : 0);
+                        load[bB] += icost[it] - (wn[bB] ? kPrefetchCost : 0);
+                        at(bB, wn[bB]++) = it;
+                    } else {  // the two items trade places
+                        const int64_t other = at(bB, bj);
+                        at(A, bk) = other;
+                        at(bB, bj) = it;
+                        load[A] += icost[other] - icost[it];
+                        load[bB] += icost[it] - icost[other];
+                    }
+                    moved = true;
+                }
+            }
+            if (moved) {
+                static_makespan = 0;
+                for (int32_t b = 0; b < groups; b++) {
+                    static_off[b + 1] = static_off[b] + wn[b];
+                    std::copy(wl.begin() + (size_t)b * kCap, wl.begin() + (size_t)b * kCap + wn[b], static_items.begin() + static_off[b]);
+                    static_makespan = std::max(static_makespan, load[b]);
+                }
+            }
+        }
     }
 
     // smallest capacity that fits the line into `groups` workgroups
