@@ -110,6 +110,32 @@ int main() {
         for (const int2 &r : ps.range) several |= r.y - r.x > 1;
         multi_plans += ps.slots == 0 && several;  // static grid, or a balanced split that cut nothing
     }
+    // c3's chunks on 192 workgroups (the one-launch mixed step's prefill part):
+    // 512 whole items, 2.7 per workgroup.  Dealt longest-first onto the
+    // least-loaded workgroup its largest load is 217 tiles (12 per item, less 4
+    // for each later item of a workgroup); the local search that follows the
+    // deal brings it to 197.
+    {
+        const int ctx[8] = {2412, 1645, 1012, 369, 1595, 2566, 2747, 1490};
+        std::vector<int4> ch;
+        for (int i = 0; i < 8; i++) ch.push_back(make_int4(i, ctx[i], 512, 512 * i));
+        const int rc = check(ch, 32, 8, 0, 1, 192);
+        AttnParams p{};
+        p.num_heads = 32;
+        p.num_kv_heads = 8;
+        p.causal = 1;
+        PrefillSplit ps;
+        prefill_split_plan(ch.data(), 8, p, 192, ps);
+        long worst = 0;
+        for (const int2 &r : ps.range) {
+            long load = 0;
+            for (int s = r.x; s < r.y; s++) load += ps.work[3 * s + 1].w - ps.work[3 * s + 1].z + 12 - (s > r.x ? 4 : 0);
+            worst = std::max(worst, load);
+        }
+        std::printf("c3 chunks on 192 workgroups: check %d, %zu workgroups, %d slots, largest load %ld tiles\n", rc,
+                    ps.range.size(), ps.slots, worst);
+        if (rc || ps.slots != 0 || ps.range.size() != 192 || worst > 197) failures++;
+    }
     std::printf("%d failures, %d of 3000 plans split items, %d run several whole items per workgroup\n", failures,
                 split_plans, multi_plans);
     return failures ? 1 : 0;
