@@ -254,6 +254,34 @@ def test_decode_few_rows_long_context_partitions(engine, dtype, B, lens):
     assert err <= TOL[dtype], f"rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("dtype,H,hkv", [(0, 8, 8), (1, 8, 8), (1, 32, 8)], ids=["f32-valu", "f16-valu", "f16-mfma"])
+def test_decode_ignores_table_entries_past_the_length(engine, dtype, H, hkv):
+    """Block-table entries past a row's length may be read early (the VALU
+    kernel requests a wave's first entries before the row's length arrives) but
+    never used: here they name a pool block of NaNs, which any use would spread
+    into the output.  c1-like short ragged rows, split into partitions."""
+    import torch
+    rng = np.random.default_rng(95 + dtype + H)
+    d, bs = 128, 16
+    q, k, v, bt, lens = make_case(rng, 4, H, hkv, d, bs, dtype, [17, 200, 64, 129])
+    poison = k.shape[0]
+    k = np.concatenate([k, np.full((1,) + k.shape[1:], np.nan, k.dtype)])
+    v = np.concatenate([v, np.full((1,) + v.shape[1:], np.nan, v.dtype)])
+    wide = np.full((bt.shape[0], bt.shape[1] + 5), poison, np.int32)
+    for b in range(bt.shape[0]):
+        n = (int(lens[b]) + bs - 1) // bs
+        wide[b, :n] = bt[b, :n]
+    dt = torch.float32 if dtype == 0 else torch.float16
+    out = torch.zeros((4, H, d), dtype=dt, device="cuda")
+    engine.decode(to_dev(q), to_dev(k), to_dev(v), to_dev(wide), to_dev(lens), out, 4, wide.shape[1],
+                  layer(H, hkv, d, bs, dtype))
+    ref = oracle.decode(dtype, q, k, v, wide, lens, H, n_threads=8)
+    got = to_host(out)
+    assert not np.isnan(got.astype(np.float64)).any()
+    err = row_rel_err(got, ref)
+    assert err <= TOL[dtype], f"rel err {err:.3e}"
+
+
 def test_decode_mfma_many_rows_workgroup_form(engine):
     """More rows than the stream-K form indexes: the workgroup form plus reduce."""
     import torch
