@@ -456,6 +456,7 @@ int32_t pam_engine_mixed_step(void *context, const pam_mixed_request *request);
  * path:
  *   decode   pam_decode_streamk_{f16,e4m3}_d128, pam_decode_layers_streamk_{f16,e4m3}_d128,
  *            pam_decode_wg_{f16,e4m3}_d128, pam_decode_valu_{f32,f16,e4m3}_h{1,2,4,8},
+ *            pam_decode_valu_wg_{f32,f16,e4m3}_h{1,2},
  *            pam_reduce_{f32,f16}
  *   prefill  pam_prefill_{f16,fused_f16,e4m3}_d128, pam_prefill_{f16,fused_f16,e4m3}_d64,
  *            pam_mixed_step_{f16,e4m3}_d128

@@ -47,6 +47,14 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnParams p, int lanes_p
     valu_body<KV, QT, NH>(p, lanes_per_row);
 }
 
+// One workgroup per (row, head group): wave w runs partition w, the waves merge
+// in LDS (AttnParams::valu_wg).
+template <typename KV, typename QT, int NH>
+__global__ __launch_bounds__(64 * kValuWgMaxParts) void attn_valu_wg_kernel(AttnParams p, int lanes_per_row) {
+    __shared__ float wg_lds[kValuWgLds<NH>];
+    valu_body<KV, QT, NH, true>(p, lanes_per_row, wg_lds);
+}
+
 template <typename QT>
 __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnParams p) {
     reduce_body<QT>(p);
@@ -177,6 +185,18 @@ static hipError_t launch_valu(const AttnParams &p, hipStream_t stream, const Ker
     while (lpr * 4 < p.head_dim) lpr <<= 1;
     if (lpr > 64 || p.head_dim % 4 != 0) return hipErrorInvalidValue;
     const int nh = p.heads_per_wave;
+    if (p.valu_wg) {
+        if ((nh != 1 && nh != 2) || p.max_parts < 2 || p.max_parts > kValuWgMaxParts) return hipErrorInvalidValue;
+        const dim3 wgrid(1, p.num_heads / nh, p.rows), wblock(64 * p.max_parts);
+        const int kvi = sizeof(KV) == 4 ? 0 : (sizeof(KV) == 2 ? 1 : 2);
+        hipError_t me;
+        if (via_module(kt, kt ? kt->valu_wg[kvi][nh - 1] : nullptr, &me, wgrid, wblock, stream, p, lpr)) return me;
+        if (nh == 1)
+            hipLaunchKernelGGL((attn_valu_wg_kernel<KV, QT, 1>), wgrid, wblock, 0, stream, p, lpr);
+        else
+            hipLaunchKernelGGL((attn_valu_wg_kernel<KV, QT, 2>), wgrid, wblock, 0, stream, p, lpr);
+        return hipGetLastError();
+    }
     dim3 grid(p.max_parts, p.num_heads / nh, p.rows);
     const int slot = nh == 1 ? 0 : (nh == 2 ? 1 : (nh == 4 ? 2 : (nh == 8 ? 3 : -1)));
     if (slot < 0) return hipErrorInvalidValue;
@@ -215,7 +235,7 @@ hipError_t launch_attention(const AttnParams &p_in, int32_t dtype, bool use_mfma
     if (e != hipSuccess) return e;
     if (after_main) (void)hipEventRecord(after_main, stream);
     // stream-K (MFMA) and the VALU kernel with counters merge in the kernel
-    if (p.max_parts <= 1 || p.seg_count != nullptr) return e;
+    if (p.max_parts <= 1 || p.seg_count != nullptr || p.valu_wg) return e;
     dim3 grid((p.num_heads + 3) / 4, p.rows);
     if (via_module(kt, kt ? kt->reduce[dtype != kF32] : nullptr, &e, grid, dim3(256), stream, p)) return e;
     if (dtype == kF32)

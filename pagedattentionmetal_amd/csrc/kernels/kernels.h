@@ -28,6 +28,9 @@ enum RowMode : int32_t {
 // MFMA decode holds up to 16 query heads per kv head; G >= 4).
 constexpr int kMaxFusedLayers = 4;
 
+// most partitions of the VALU kernel's workgroup form (one wave each)
+constexpr int kValuWgMaxParts = 16;
+
 struct AttnParams {
     const void *q;             // [rows][H][d] (f32 for f32 caches, f16 otherwise)
     void *out;                 // [rows][H][d] same type as q
@@ -81,6 +84,9 @@ struct AttnParams {
     // counts as zero arrivals, so counters need no reset.  The launchers set a
     // fresh nonzero epoch for every launch (a retried launch gets a new one).
     uint32_t epoch;
+    // VALU kernel: 1 runs a (row, head group)'s partitions as the waves of one
+    // workgroup (attn_valu_wg_kernel), merged in LDS
+    int32_t valu_wg;
 };
 
 // Entry points of a loaded code object (libpam_kernels.hsaco, module_entry.hip).
@@ -94,6 +100,7 @@ struct KernelTable {
     hipFunction_t prefill[2][3];  // dense prefill, [d = 128, d = 64][f16, f16 with fused append, e4m3]
     hipFunction_t mixed[2];       // one-launch mixed step: f16, e4m3
     hipFunction_t valu[3][4];     // VALU rows: [f32, f16, e4m3 KV][1, 2, 4, 8 heads per wave]
+    hipFunction_t valu_wg[3][2];  // their workgroup form: [KV][1, 2 heads per wave]
     hipFunction_t reduce[2];      // split-context reduce: f32, f16 outputs
     hipFunction_t append[3];      // append copy in 16-, 4- or 2-byte pieces
     hipFunction_t append_batch[3];

@@ -53,12 +53,19 @@ __device__ __forceinline__ void load_kv4<uint8_t>(const uint8_t *ptr, f16 scale,
 }
 
 constexpr int kValuBatch = 8;  // steps of the VALU kernel whose loads are in flight together
+// LDS of the workgroup form: every partition's (O, m, l) for NH heads at the
+// largest head size the VALU kernel takes (256: 64 lanes of 4 dims)
+template <int NH>
+constexpr int kValuWgLds = kValuWgMaxParts * NH * (256 + 2);
 
 // lanes_per_row: power of two >= head_dim / 4 (<= 64); heads NH share one kv head.
-template <typename KV, typename QT, int NH>
-__device__ __forceinline__ void valu_body(const AttnParams &p, int lanes_per_row) {
-    const int lane = threadIdx.x;
-    const int part = blockIdx.x, hg = blockIdx.y, r = blockIdx.z;
+// WG: the workgroup is one (row, head group) and wave w its partition w; the
+// partitions merge in wg_lds (kValuWgLds<NH> floats: max_parts * NH *
+// (head_dim + 2) of them are used).
+template <typename KV, typename QT, int NH, bool WG = false>
+__device__ __forceinline__ void valu_body(const AttnParams &p, int lanes_per_row, float *wg_lds = nullptr) {
+    const int lane = WG ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
+    const int part = WG ? (int)(threadIdx.x >> 6) : (int)blockIdx.x, hg = blockIdx.y, r = blockIdx.z;
     const int HD = p.head_dim, H = p.num_heads;
     const int G = H / p.num_kv_heads;
     const int h0 = hg * NH;
@@ -83,13 +90,15 @@ __device__ __forceinline__ void valu_body(const AttnParams &p, int lanes_per_row
     }
     const RowCtx c = row_ctx(p, r);
     const PartRange pr = part_range(c, part, p.part_tokens);
-    if (part >= (pr.nparts > 1 ? pr.nparts : 1)) return;
+    // a wave past the row's partitions has no tiles; in a workgroup it stays
+    // for the merge's barrier when there is one
+    if (part >= (pr.nparts > 1 ? pr.nparts : 1) && (!WG || pr.nparts <= 1)) return;
 
     const int d0 = (lane % LPR) * 4;
     const bool dim_ok = d0 < HD;
     QT *out = static_cast<QT *>(p.out);
     if (pr.nparts == 0) {
-        if (sub == 0 && dim_ok) {
+        if (sub == 0 && dim_ok && (!WG || part == 0)) {
             float nanv[4] = {__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
             for (int hh = 0; hh < NH; hh++) store4<QT>(out + (c.out_row * H + h0 + hh) * (int64_t)HD + d0, nanv);
         }
@@ -200,6 +209,46 @@ __device__ __forceinline__ void valu_body(const AttnParams &p, int lanes_per_row
         l[hh] = wave_sum_xor(l[hh], LPR, 64);
 #pragma unroll
         for (int e = 0; e < 4; e++) acc[hh][e] = wave_sum_xor(acc[hh][e], LPR, 64);
+    }
+    if constexpr (WG) {
+        if (pr.nparts > 1) {
+            // each wave's partial into LDS, then wave 0 folds the partitions in
+            // order, as the global merge below does (the same bits)
+            const int stride = NH * (HD + 2);
+            float *mine = wg_lds + part * stride;
+            if (part < pr.nparts && sub == 0 && dim_ok) {
+#pragma unroll
+                for (int hh = 0; hh < NH; hh++) {
+                    *reinterpret_cast<float4 *>(mine + hh * HD + d0) = make_float4(acc[hh][0], acc[hh][1], acc[hh][2], acc[hh][3]);
+                    if (d0 == 0) {
+                        mine[NH * HD + 2 * hh] = m[hh];
+                        mine[NH * HD + 2 * hh + 1] = l[hh];
+                    }
+                }
+            }
+            __syncthreads();
+            if (part == 0 && sub == 0 && dim_ok) {
+#pragma unroll
+                for (int hh = 0; hh < NH; hh++) {
+                    float M = -INFINITY;
+                    for (int pt = 0; pt < pr.nparts; pt++) M = fmaxf(M, wg_lds[pt * stride + NH * HD + 2 * hh]);
+                    float den = 0.0f, a[4] = {0.f, 0.f, 0.f, 0.f};
+                    for (int pt = 0; pt < pr.nparts; pt++) {
+                        const float *src = wg_lds + pt * stride;
+                        const float mp = src[NH * HD + 2 * hh], lp = src[NH * HD + 2 * hh + 1];
+                        const float4 v = *reinterpret_cast<const float4 *>(src + hh * HD + d0);
+                        const float w = mp == -INFINITY ? 0.0f : exp2f(mp - M);
+                        den += w * lp;
+                        a[0] += w * v.x, a[1] += w * v.y, a[2] += w * v.z, a[3] += w * v.w;
+                    }
+                    const float inv = 1.0f / den;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) a[e] *= inv;
+                    store4<QT>(out + (c.out_row * H + h0 + hh) * (int64_t)HD + d0, a);
+                }
+            }
+            return;
+        }
     }
     if (sub != 0 || !dim_ok) return;
     if (pr.nparts == 1) {

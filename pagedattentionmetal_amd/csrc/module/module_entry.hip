@@ -41,6 +41,11 @@ namespace pam {
     extern "C" __global__ __launch_bounds__(64) void NAME(AttnParams p, int lanes_per_row) {    \
         valu_body<KV, QT, NH>(p, lanes_per_row);                                                 \
     }
+#define PAM_VALU_WG_ENTRY(NAME, KV, QT, NH)                                                                  \
+    extern "C" __global__ __launch_bounds__(64 * kValuWgMaxParts) void NAME(AttnParams p, int lanes_per_row) { \
+        __shared__ float wg_lds[kValuWgLds<NH>];                                                             \
+        valu_body<KV, QT, NH, true>(p, lanes_per_row, wg_lds);                                              \
+    }
 #define PAM_APPEND_ENTRY(NAME, CH)                                                                          \
     extern "C" __global__ __launch_bounds__(256) void NAME(AppendParams p, int64_t chunks_per_row,        \
                                                            int64_t total) {                               \
@@ -74,6 +79,14 @@ PAM_VALU_ENTRY(pam_decode_valu_e4m3_h1, uint8_t, f16, 1)
 PAM_VALU_ENTRY(pam_decode_valu_e4m3_h2, uint8_t, f16, 2)
 PAM_VALU_ENTRY(pam_decode_valu_e4m3_h4, uint8_t, f16, 4)
 PAM_VALU_ENTRY(pam_decode_valu_e4m3_h8, uint8_t, f16, 8)
+// their workgroup form: a (row, head group)'s partitions as the waves of one
+// workgroup, merged in LDS
+PAM_VALU_WG_ENTRY(pam_decode_valu_wg_f32_h1, float, float, 1)
+PAM_VALU_WG_ENTRY(pam_decode_valu_wg_f32_h2, float, float, 2)
+PAM_VALU_WG_ENTRY(pam_decode_valu_wg_f16_h1, f16, f16, 1)
+PAM_VALU_WG_ENTRY(pam_decode_valu_wg_f16_h2, f16, f16, 2)
+PAM_VALU_WG_ENTRY(pam_decode_valu_wg_e4m3_h1, uint8_t, f16, 1)
+PAM_VALU_WG_ENTRY(pam_decode_valu_wg_e4m3_h2, uint8_t, f16, 2)
 // split-context reduce, by output type
 extern "C" __global__ __launch_bounds__(256) void pam_reduce_f32(AttnParams p) { reduce_body<float>(p); }
 extern "C" __global__ __launch_bounds__(256) void pam_reduce_f16(AttnParams p) { reduce_body<f16>(p); }

@@ -322,6 +322,7 @@ int32_t Context::choose_part_tokens(int64_t items_per_part, int64_t max_tiles, b
 int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t max_tiles, int64_t waves,
                             char *fixed) {
     p.seg_count = nullptr;
+    p.valu_wg = 0;
     int64_t slots = 0, counters = 0;
     // `fixed`: the allocation-free scratch (kNoAllocScratchBytes, laid out as
     // zero page | counters | partials); requests that do not fit it are refused
@@ -367,6 +368,13 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
     p.part_tokens = choose_part_tokens(waves, max_tiles, use_mfma);
     p.max_parts = (int32_t)std::max<int64_t>(1, ceil_div(max_tiles, p.part_tokens / 16));
     if (p.max_parts <= 1) return 0;
+    // VALU rows of one or two heads per wave split into at most kValuWgMaxParts
+    // partitions: a (row, head group)'s partitions run as the waves of one
+    // workgroup and merge in LDS, with no partials in memory and no counters
+    if (!use_mfma && p.heads_per_wave <= 2 && p.max_parts <= kValuWgMaxParts) {
+        p.valu_wg = 1;
+        return 0;
+    }
     const int64_t slots_p = (int64_t)p.rows * p.num_heads * p.max_parts;
     const int64_t bytes = slots_p * ((int64_t)p.head_dim + 2) * 4;
     if (bytes >= ((int64_t)1 << 31)) throw PamError("split-context workspace exceeds 2 GiB");
@@ -514,6 +522,9 @@ void Context::module_load(const char *path) {
     for (int k = 0; k < 3; k++)
         for (int h = 0; h < 4; h++)
             t.valu[k][h] = get(("pam_decode_valu_" + std::string(kv_names[k]) + "_h" + std::to_string(heads[h])).c_str());
+    for (int k = 0; k < 3; k++)
+        for (int h = 0; h < 2; h++)
+            t.valu_wg[k][h] = get(("pam_decode_valu_wg_" + std::string(kv_names[k]) + "_h" + std::to_string(heads[h])).c_str());
     t.reduce[0] = get("pam_reduce_f32");
     t.reduce[1] = get("pam_reduce_f16");
     static const char *piece[3] = {"16", "4", "2"};

@@ -144,6 +144,11 @@ DECODE_CASES = [
     (4, 32, 8, 128, 16, 1, [0, 20, 0, 300], 0, 0, 0),
     (3, 32, 8, 128, 16, 2, [3, 200, 1500], 0, 0, 128),
     (2, 32, 8, 64, 8, 2, [900, 40], 0, 0, 0),                      # fp8, bs 8
+    # VALU rows split into at most 16 partitions run as one workgroup per (row,
+    # head group) merged in LDS; more partitions merge through memory
+    (3, 16, 8, 128, 16, 1, [30, 160, 250], 0, 1, 0),              # 2 heads per wave, workgroup form
+    (2, 8, 8, 128, 16, 0, [3000, 900], 0, 0, 0),                  # fp32, 188 partitions: global merge
+    (2, 8, 8, 128, 16, 2, [40, 230], 0, 0, 0),                    # fp8 MHA: VALU workgroup form
 ]
 
 

@@ -474,7 +474,8 @@ def test_code_object_is_built_beside_the_library(pam, ctx):
     assert head == b"\x7fELF"
     for name in (b"pam_decode_streamk_f16_d128", b"pam_decode_streamk_e4m3_d128", b"pam_decode_layers_streamk_f16_d128",
                  b"pam_prefill_f16_d128", b"pam_prefill_fused_f16_d128", b"pam_prefill_e4m3_d128",
-                 b"pam_prefill_f16_d64", b"pam_prefill_fused_f16_d64", b"pam_prefill_e4m3_d64", b"pam_fill_u32"):
+                 b"pam_prefill_f16_d64", b"pam_prefill_fused_f16_d64", b"pam_prefill_e4m3_d64",
+                 b"pam_decode_valu_wg_f32_h1", b"pam_decode_valu_wg_e4m3_h2", b"pam_fill_u32"):
         assert name in data, name
     import torch
     if not torch.cuda.is_available():
