@@ -217,21 +217,28 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
     for (int32_t c = 0; c < n; c++)
         item_base[c + 1] = item_base[c] + (int64_t)p.num_kv_heads * ((chunks[c].z + tpw - 1) / tpw);
     std::vector<int64_t> grid_item(grid_ids, -1);
-    int64_t grid_makespan = 0;
-    {
+    for (int64_t b = 0; b < grid_ids; b++) {
+        const int64_t xcd = b % kXcds, r = b / kXcds;
+        const int64_t grp = xcd + kXcds * (r / nx);
+        if (grp >= ngroups) continue;
+        const int32_t c = order[grp / p.num_kv_heads], kvh = (int32_t)(grp % p.num_kv_heads);
+        const int32_t nb = (chunks[c].z + tpw - 1) / tpw, tb = nx - 1 - (int32_t)(r % nx);
+        if (tb < nb) grid_item[b] = item_base[c] + (int64_t)kvh * nb + tb;
+    }
+    // The grid order's makespan by list scheduling, run only when it can
+    // matter: it is at least grid_lb (the mean load, and the longest item), so
+    // a static deal below that bound is taken without it.
+    int64_t grid_lb = (total + groups - 1) / groups;
+    for (const PfItem &it : items) grid_lb = std::max<int64_t>(grid_lb, it.t_hi - it.t_lo + kSegCost);
+    auto grid_estimate = [&]() {
+        int64_t makespan = 0;
         // each CU's finish time, a binary min-heap (all 0 to start)
         std::vector<int64_t> cu(groups, 0);
         for (int64_t b = 0; b < grid_ids; b++) {
-            const int64_t xcd = b % kXcds, r = b / kXcds;
-            const int64_t grp = xcd + kXcds * (r / nx);
-            if (grp >= ngroups) continue;
-            const int32_t c = order[grp / p.num_kv_heads], kvh = (int32_t)(grp % p.num_kv_heads);
-            const int32_t nb = (chunks[c].z + tpw - 1) / tpw, tb = nx - 1 - (int32_t)(r % nx);
-            if (tb >= nb) continue;
-            const int64_t it = item_base[c] + (int64_t)kvh * nb + tb;
-            grid_item[b] = it;
+            const int64_t it = grid_item[b];
+            if (it < 0) continue;
             const int64_t t = cu[0] + items[it].t_hi - items[it].t_lo + kSegCost;
-            grid_makespan = std::max(grid_makespan, t);
+            makespan = std::max(makespan, t);
             for (int32_t i = 0;;) {  // the earliest CU takes it: sift its new time down
                 const int32_t l = 2 * i + 1, r = l + 1;
                 int32_t m = l < groups && cu[l] < t ? l : -1;
@@ -244,7 +251,8 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
                 i = m;
             }
         }
-    }
+        return makespan;
+    };
 
     // Static grid: the grid order's items, each on the same XCD as there (all
     // token blocks of one (chunk, kv head) share that XCD's L2), dealt to the
@@ -279,11 +287,19 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
         // equals.
         std::vector<int64_t> load(groups);
         std::vector<int32_t> cnt(groups);
-        // the XCD's workgroups in a binary min-heap on (load, workgroup)
-        std::vector<int32_t> heap(per_xcd);
-        auto before = [&](int32_t a, int32_t b) { return load[a] < load[b] || (load[a] == load[b] && a < b); };
-        auto heap_init = [&](int32_t x) {
-            for (int32_t i = 0; i < per_xcd; i++) heap[i] = i * kXcds + x;  // all loads 0: already a heap
+        // A deal runs XCD by XCD on contiguous copies of the XCD's loads and
+        // counts (xl, xc: entry i is workgroup i * 8 + x), its workgroups in a
+        // binary min-heap on (load, workgroup)
+        std::vector<int64_t> xl(per_xcd);
+        std::vector<int32_t> xc(per_xcd), heap(per_xcd);
+        auto before = [&](int32_t a, int32_t b) { return xl[a] < xl[b] || (xl[a] == xl[b] && a < b); };
+        auto heap_init = [&]() {
+            std::fill(xl.begin(), xl.end(), 0);
+            std::fill(xc.begin(), xc.end(), 0);
+            for (int32_t i = 0; i < per_xcd; i++) heap[i] = i;  // all loads 0: already a heap
+        };
+        auto xcd_done = [&](int32_t x) {
+            for (int32_t i = 0; i < per_xcd; i++) load[i * kXcds + x] = xl[i], cnt[i * kXcds + x] = xc[i];
         };
         auto sift_down = [&]() {  // the top's load grew
             int32_t i = 0;
@@ -297,28 +313,52 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
                 i = m;
             }
         };
-        std::vector<std::pair<int32_t, int64_t>> dealt;
-        auto put = [&](int32_t wg, int64_t it, bool trace) {
+        // each deal records its (workgroup, item) pairs in the order dealt
+        using Record = std::vector<std::pair<int32_t, int64_t>>;
+        Record rec[3];
+        for (Record &r : rec) r.reserve(items.size());
+        auto put = [&](int32_t wg, int64_t it, Record *trace) {
             load[wg] += icost[it] - (cnt[wg] ? kPrefetchCost : 0);
             cnt[wg]++;
-            if (trace) dealt.emplace_back(wg, it);
+            if (trace) trace->emplace_back(wg, it);
         };
-        std::vector<int64_t> seq;
-        auto deal = [&](bool sorted, bool trace) -> int64_t {
-            std::fill(load.begin(), load.end(), 0);
-            std::fill(cnt.begin(), cnt.end(), 0);
+        // the same onto entry i of XCD x's copies
+        auto xput = [&](int32_t x, int32_t i, int64_t it, Record *trace) {
+            xl[i] += icost[it] - (xc[i] ? kPrefetchCost : 0);
+            xc[i]++;
+            if (trace) trace->emplace_back(i * kXcds + x, it);
+        };
+        // an XCD's items longest first, ties in grid order (a stable counting
+        // sort on the small integer costs; a comparison sort past 2^16 tiles)
+        std::vector<int64_t> by_cost;
+        std::vector<int32_t> tally;
+        auto longest_first = [&](const std::vector<int64_t> &in) -> const std::vector<int64_t> & {
+            by_cost.resize(in.size());
+            int64_t top = 0;
+            for (int64_t it : in) top = std::max(top, icost[it]);
+            if (top > (1 << 16)) {
+                by_cost = in;
+                std::stable_sort(by_cost.begin(), by_cost.end(), [&](int64_t a, int64_t b) { return icost[a] > icost[b]; });
+                return by_cost;
+            }
+            tally.assign(top + 2, 0);
+            for (int64_t it : in) tally[top - icost[it] + 1]++;  // slot by descending cost
+            for (int64_t k = 1; k <= top + 1; k++) tally[k] += tally[k - 1];
+            for (int64_t it : in) by_cost[tally[top - icost[it]]++] = it;
+            return by_cost;
+        };
+        auto deal = [&](bool sorted, Record *trace) -> int64_t {
             int64_t worst = 0;
             for (int32_t x = 0; x < kXcds; x++) {
-                seq = by_xcd[x];
-                if (sorted)
-                    std::stable_sort(seq.begin(), seq.end(), [&](int64_t a, int64_t b) { return icost[a] > icost[b]; });
-                heap_init(x);
+                const std::vector<int64_t> &seq = sorted ? longest_first(by_xcd[x]) : by_xcd[x];
+                heap_init();
                 for (int64_t it : seq) {
-                    const int32_t wg = heap[0];
-                    put(wg, it, trace);
+                    const int32_t i = heap[0];
+                    xput(x, i, it, trace);
                     sift_down();
-                    worst = std::max(worst, load[wg]);
+                    worst = std::max(worst, xl[i]);
                 }
+                xcd_done(x);
             }
             return worst;
         };
@@ -330,9 +370,7 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
         // each pair's blocks go to the least-loaded workgroups of the XCD.
         std::vector<int32_t> gstart, gorder, sorder;
         std::vector<int64_t> gcost, scost;
-        auto deal_paired = [&](bool trace) -> int64_t {
-            std::fill(load.begin(), load.end(), 0);
-            std::fill(cnt.begin(), cnt.end(), 0);
+        auto deal_paired = [&](Record *trace) -> int64_t {
             int64_t worst = 0;
             for (int32_t x = 0; x < kXcds; x++) {
                 // this XCD's groups: runs of items of one (chunk, kv head), in grid order
@@ -348,7 +386,7 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
                     gcost.back() += icost[xs[i]];
                 }
                 const int32_t ng = (int32_t)gstart.size();
-                heap_init(x);
+                heap_init();
                 gstart.push_back((int32_t)xs.size());
                 gorder.resize(ng);
                 for (int32_t g = 0; g < ng; g++) gorder[g] = g;
@@ -365,32 +403,46 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
                     for (int32_t i = 0; i < nb; i++) scost[na - 1 - (i % na)] += icost[xs[gstart[gb] + i]];
                     // the pair's slots onto the least-loaded workgroups of this XCD,
                     // heaviest slot first
+                    // (a stable counting sort on the slot costs when their range is small)
                     sorder.resize(na);
-                    for (int32_t k = 0; k < na; k++) sorder[k] = k;
-                    std::stable_sort(sorder.begin(), sorder.end(), [&](int32_t u, int32_t v) { return scost[u] > scost[v]; });
+                    int64_t smin = scost[0], smax = scost[0];
+                    for (int32_t k = 1; k < na; k++) smin = std::min(smin, scost[k]), smax = std::max(smax, scost[k]);
+                    if (smax - smin <= 4 * (int64_t)na + 64) {
+                        tally.assign(smax - smin + 2, 0);
+                        for (int32_t k = 0; k < na; k++) tally[smax - scost[k] + 1]++;
+                        for (int64_t v = 1; v <= smax - smin + 1; v++) tally[v] += tally[v - 1];
+                        for (int32_t k = 0; k < na; k++) sorder[tally[smax - scost[k]]++] = k;
+                    } else {
+                        for (int32_t k = 0; k < na; k++) sorder[k] = k;
+                        std::stable_sort(sorder.begin(), sorder.end(), [&](int32_t u, int32_t v) { return scost[u] > scost[v]; });
+                    }
                     for (int32_t k : sorder) {
-                        const int32_t wg = heap[0];
-                        put(wg, xs[gstart[ga] + k], trace);
-                        for (int32_t i = na - 1 - k; i < nb; i += na) put(wg, xs[gstart[gb] + i], trace);
+                        const int32_t w = heap[0];
+                        xput(x, w, xs[gstart[ga] + k], trace);
+                        for (int32_t i = na - 1 - k; i < nb; i += na) xput(x, w, xs[gstart[gb] + i], trace);
                         sift_down();
-                        worst = std::max(worst, load[wg]);
+                        worst = std::max(worst, xl[w]);
                     }
                 }
+                xcd_done(x);
             }
             return worst;
         };
-        static_makespan = deal(false, false);
-        const int64_t sorted_makespan = deal(true, false);
-        const int64_t paired_makespan = deal_paired(false);
+        static_makespan = deal(false, &rec[0]);
+        const int64_t sorted_makespan = deal(true, &rec[1]);
+        const int64_t paired_makespan = deal_paired(&rec[2]);
         int deal_pick = 0;  // 0 grid order, 1 longest first, 2 paired groups
         if ((double)sorted_makespan < 0.99 * (double)static_makespan) deal_pick = 1;
         const int64_t best_other = deal_pick == 1 ? sorted_makespan : static_makespan;
         // paired groups keep their L2 sharing: taken when its estimate is no longer
         if ((double)paired_makespan <= kPairedSlack * (double)best_other) deal_pick = 2;
-        // the chosen deal again, recording it, then its items grouped by
+        // the chosen deal's record: its loads again, then its items grouped by
         // workgroup (a counting sort keeps each workgroup's order dealt)
-        dealt.reserve(items.size());
-        static_makespan = deal_pick == 2 ? deal_paired(true) : deal(deal_pick == 1, true);
+        const Record &dealt = rec[deal_pick];
+        static_makespan = deal_pick == 2 ? paired_makespan : (deal_pick == 1 ? sorted_makespan : static_makespan);
+        std::fill(load.begin(), load.end(), 0);
+        std::fill(cnt.begin(), cnt.end(), 0);
+        for (const auto &d : dealt) put(d.first, d.second, nullptr);
         static_off.assign(groups + 1, 0);
         for (int32_t b = 0; b < groups; b++) static_off[b + 1] = static_off[b] + cnt[b];
         static_items.resize(dealt.size());
@@ -472,17 +524,25 @@ void prefill_split_plan(const int4 *chunks, int32_t n, AttnParams &p, int32_t gr
         }
     }
 
-    // smallest capacity that fits the line into `groups` workgroups
+    const int64_t grid_makespan = static_makespan < grid_lb ? grid_lb : grid_estimate();
+    // The balanced split: the smallest capacity that fits the line into
+    // `groups` workgroups, searched upward from its lower bound.  It pays for
+    // its partials and, with many items per workgroup, loses the side-by-side
+    // L2 sharing of the grid order: it is taken only when it clearly shortens
+    // the estimated makespan, so the search is skipped when even its bound
+    // cannot, unless no other schedule applies.
     int64_t lo = std::max<int64_t>((total + groups - 1) / groups, kSegCost + kSplitCost + kMinPiece);
-    int64_t hi = std::max<int64_t>(lo, total + kSegCost);
-    while (lo < hi) {
-        const int64_t mid = (lo + hi) / 2;
-        if (pf_fill(items, mid, groups, nullptr, nullptr) <= groups) hi = mid; else lo = mid + 1;
+    const double best_whole = (double)std::min(grid_makespan, static_makespan);
+    const bool split_can_win = allow_split && (double)lo <= 0.95 * best_whole;
+    const bool other_applies = static_makespan < grid_makespan || grid_ids <= INT32_MAX;
+    if (split_can_win || !other_applies) {
+        int64_t hi = std::max<int64_t>(lo, total + kSegCost);
+        while (lo < hi) {
+            const int64_t mid = (lo + hi) / 2;
+            if (pf_fill(items, mid, groups, nullptr, nullptr) <= groups) hi = mid; else lo = mid + 1;
+        }
     }
-    // The balanced split pays for its partials and, with many items per
-    // workgroup, loses the side-by-side L2 sharing of the grid order: it is
-    // taken only when it clearly shortens the estimated makespan.
-    const bool split_wins = allow_split && (double)lo <= 0.95 * (double)std::min(grid_makespan, static_makespan);
+    const bool split_wins = split_can_win && (double)lo <= 0.95 * best_whole;
     if (!split_wins && static_makespan < grid_makespan) {
         out.range.assign(groups, make_int2(0, 0));
         for (int32_t b = 0; b < groups; b++) {

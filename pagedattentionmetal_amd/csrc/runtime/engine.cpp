@@ -135,15 +135,24 @@ void Context::finish(const char *what) {
     if (synchronous) hip_check(hipStreamSynchronize(stream()), what);
 }
 
+// Device buffers that grow with the requests grow by at least half their size
+// (rounded up to 1 MiB), so that a serving loop whose steps grow slowly
+// reallocates, and drains the stream for it, only a few times.
+static size_t grown(size_t bytes, size_t have) {
+    const size_t want = std::max(bytes, have + have / 2);
+    return (want + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
+}
+
 void Context::reserve_workspace(size_t bytes) {
     ensure_device();
     if (bytes <= workspace_.bytes) return;
     hip_check(hipStreamSynchronize(stream()), "workspace resize");
+    const size_t want = grown(bytes, workspace_.bytes);
     if (workspace_.ptr) (void)hip_check(hipFree(workspace_.ptr), "hipFree");
     workspace_.ptr = nullptr;
     workspace_.bytes = 0;
-    hip_check(hipMalloc(&workspace_.ptr, bytes), "hipMalloc workspace");
-    workspace_.bytes = bytes;
+    hip_check(hipMalloc(&workspace_.ptr, want), "hipMalloc workspace");
+    workspace_.bytes = want;
 }
 
 void *Context::device_scratch(int slot, size_t bytes) {
@@ -153,7 +162,7 @@ void *Context::device_scratch(int slot, size_t bytes) {
         if (b.ptr) hip_check(hipFree(b.ptr), "hipFree");
         b.ptr = nullptr;
         b.bytes = 0;
-        size_t want = std::max<size_t>(bytes, 4096);
+        const size_t want = bytes <= 4096 && b.bytes == 0 ? 4096 : grown(bytes, b.bytes);
         hip_check(hipMalloc(&b.ptr, want), "hipMalloc scratch");
         b.bytes = want;
     }
@@ -404,13 +413,14 @@ int64_t Context::plan_split(AttnParams &p, int32_t dtype, bool use_mfma, int64_t
 void Context::reserve_counters(DeviceBuffer &b, size_t bytes) {
     if (bytes <= b.bytes) return;
     hip_check(hipStreamSynchronize(stream()), "counter resize");
+    const size_t want = grown(bytes, b.bytes);
     if (b.ptr) hip_check(hipFree(b.ptr), "hipFree");
     b.ptr = nullptr;
     b.bytes = 0;
-    hip_check(hipMalloc(&b.ptr, bytes), "hipMalloc counters");
-    hip_check(hipMemsetAsync(b.ptr, 0, bytes, stream()), "counter clear");
+    hip_check(hipMalloc(&b.ptr, want), "hipMalloc counters");
+    hip_check(hipMemsetAsync(b.ptr, 0, want, stream()), "counter clear");
     hip_check(hipStreamSynchronize(stream()), "counter clear");
-    b.bytes = bytes;
+    b.bytes = want;
 }
 
 void Context::dirty_counters(int32_t arrivals) {
@@ -447,8 +457,9 @@ Context::DensePlan Context::plan_dense_prefill(AttnParams &p, const int4 *chunks
             if (pf_part_.ptr) hip_check(hipFree(pf_part_.ptr), "hipFree");
             pf_part_.ptr = nullptr;
             pf_part_.bytes = 0;
-            hip_check(hipMalloc(&pf_part_.ptr, (size_t)bytes), "hipMalloc prefill workspace");
-            pf_part_.bytes = (size_t)bytes;
+            const size_t want = grown((size_t)bytes, pf_part_.bytes);
+            hip_check(hipMalloc(&pf_part_.ptr, want), "hipMalloc prefill workspace");
+            pf_part_.bytes = want;
         }
         reserve_counters(pf_count_, (size_t)ps.slots * 8);
         p.pf_part = static_cast<float *>(pf_part_.ptr);

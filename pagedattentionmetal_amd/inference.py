@@ -68,6 +68,13 @@ class PagedAttentionInference:
         self._fills = 0  # synthetic-data streams used so far (workloads.device_normals)
         self._buf_rows = 0
         self._max_new: dict[int, int] = {}
+        # host mirrors of per-sequence state the step reads every time, kept in
+        # step with the library's: the prompt, the scheduler's generated count
+        # (changed only by mark_decoded) and the cache's length (the prompt at
+        # prefill, one more per decode append)
+        self._prompt: dict[int, int] = {}
+        self._generated: dict[int, int] = {}
+        self._length: dict[int, int] = {}
         self.last_launch = None  # (context lengths, query lengths) of the last mixed_step, rows in that order
         self.attended_pairs = 0  # unmasked (query row, key) pairs per head launched so far
 
@@ -77,12 +84,15 @@ class PagedAttentionInference:
         sid = self.scheduler.add_request(prompt_token_count, max_new_tokens)
         if sid >= 0:
             self._max_new[sid] = max_new_tokens
+            self._prompt[sid] = prompt_token_count
+            self._generated[sid] = 0
         return sid
 
     def complete_sequence(self, sid: int):
         self.scheduler.complete_sequence(sid)
         self.cache.free_sequence(sid)
         self.prefilled.discard(sid)
+        self._length.pop(sid, None)
 
     @property
     def waiting_count(self):
@@ -108,7 +118,7 @@ class PagedAttentionInference:
 
         prompts = {}
         for sid in newcomers:  # handlePrefill's block work (:172-186)
-            prompt = self.scheduler.sequence(sid)["prompt"]
+            prompt = self._prompt[sid]
             dropped |= self._ensure_blocks((prompt + bs - 1) // bs)
             if sid in dropped:  # paused by this or an earlier newcomer's memory pressure: no blocks for it
                 continue
@@ -118,10 +128,11 @@ class PagedAttentionInference:
                 self.cache.free_sequence(sid)
                 self.cache.allocate_sequence(sid)
             self.cache.append_tokens(sid, prompt)
+            self._length[sid] = prompt
             prompts[sid] = prompt
 
         decoding = [s for s in decoding if s not in dropped]
-        lens = {sid: self.cache.get_sequence_length(sid) for sid in decoding}
+        lens = {sid: self._length[sid] for sid in decoding}
         extras = sum((L + 1 + bs - 1) // bs - (L + bs - 1) // bs for L in lens.values())
         if extras > 0:  # handleDecode (:225-233)
             dropped |= self._ensure_blocks(extras)
@@ -129,6 +140,7 @@ class PagedAttentionInference:
         decoding = [s for s in decoding if s not in dropped]
         for sid in decoding:
             self.cache.append_tokens(sid, 1)  # the new token's slot, written by the step
+            self._length[sid] += 1
 
         if self.attend and (newcomers or decoding):
             if len(self.layers) > 1:
@@ -143,10 +155,10 @@ class PagedAttentionInference:
             self.prefill_tokens += prompts[sid]
         for sid in decoding:  # :260-276
             self.scheduler.mark_decoded(sid)
+            self._generated[sid] += 1
             self.total_tokens_generated += 1
             self.decoded_tokens += 1
-            info = self.scheduler.sequence(sid)
-            if info["generated"] >= self._max_new[sid]:  # SchedulerSequence.isDone
+            if self._generated[sid] >= self._max_new[sid]:  # SchedulerSequence.isDone
                 self.complete_sequence(sid)
         self.step_count += 1
         return batch
@@ -179,13 +191,11 @@ class PagedAttentionInference:
         see keys from its one window start max(0, ctx + T - W) up to their own
         position; a decode row sees its last min(L + 1, W) keys."""
         W = self.layer.window_size
-        n = 0
-        for c, q in zip(ctx.tolist(), ql.tolist()):
-            kv = c + q
-            ws = max(0, kv - W) if W > 0 else 0
-            for_rows = (max(0, kv - ws) * (max(0, kv - ws) + 1) - max(0, c - ws) * (max(0, c - ws) + 1)) // 2
-            n += for_rows
-        return n
+        c = np.asarray(ctx, np.int64)
+        kv = c + np.asarray(ql, np.int64)
+        ws = np.maximum(0, kv - W) if W > 0 else np.zeros_like(kv)
+        a, b = np.maximum(0, kv - ws), np.maximum(0, c - ws)
+        return int(((a * (a + 1) - b * (b + 1)) // 2).sum())
 
     def _normals(self, shape, dtype, std):
         """Synthetic Q / K / V rows: the counter-based normals of this driver's seed,
@@ -213,8 +223,9 @@ class PagedAttentionInference:
         ql = np.array([prompts[s] for s in newcomers] + [1] * len(decoding), np.int32)
         bs = self.cache.block_size
         width = int(((ctx + ql + bs - 1) // bs).max())
-        bt = torch.zeros((len(ids), width), dtype=torch.int32, device="cuda")
-        sl = torch.zeros(len(ids), dtype=torch.int32, device="cuda")
+        # batch_view writes every entry (the table zero-padded)
+        bt = torch.empty((len(ids), width), dtype=torch.int32, device="cuda")
+        sl = torch.empty(len(ids), dtype=torch.int32, device="cuda")
         self.cache.batch_view(ids, bt, sl, width)
         rows = int(ql.sum())
         self.last_launch = (ctx, ql)
@@ -272,8 +283,8 @@ class PagedAttentionInference:
             sm = torch.tensor(slots, dtype=torch.int64, device="cuda")
             eng.append_to_cache(nk, nv, c.k_pool(), c.v_pool(), None, 0, B, L, slot_mapping=sm)
         width = max((lens[s] + 1 + bs - 1) // bs for s in decoding)
-        bt = torch.zeros((B, width), dtype=torch.int32, device="cuda")
-        sl = torch.zeros(B, dtype=torch.int32, device="cuda")
+        bt = torch.empty((B, width), dtype=torch.int32, device="cuda")  # batch_view writes every entry
+        sl = torch.empty(B, dtype=torch.int32, device="cuda")
         c.batch_view(decoding, bt, sl, width)
         eng.decode_layers(qs, c.k_pool(), c.v_pool(), bt, sl, outs, B, width, self.layers, **scales)
         ctx = np.array([lens[s] for s in decoding], np.int32)
@@ -292,10 +303,14 @@ def poisson_trace(inference: PagedAttentionInference, steps: int, rate: float, p
     admitted = 0
     pos = 0
 
-    def draw():
-        nonlocal pos
+    block = np.zeros(0)
+
+    def draw():  # output pos of the stream, generated 4096 at a time
+        nonlocal pos, block
+        if pos % 4096 == 0:
+            block = uniforms(seed, 0, 4096, pos)
         pos += 1
-        return float(uniforms(seed, 0, 1, pos - 1)[0])
+        return float(block[(pos - 1) % 4096])
 
     def poisson():
         u, k = draw(), 0

@@ -104,6 +104,10 @@ def test_poisson_trace_on_the_gpu():
         want = np.concatenate([np.arange(q) < (q - W if c == 0 else 0) for c, q in zip(ctx, ql)])
         assert (nan_rows == want).all(), (i, ctx, ql)
         assert torch.isfinite(o[torch.from_numpy(~want).cuda()]).all()
+        # the step's host mirrors agree with the cache and the scheduler
+        for sid in inf.prefilled:
+            assert inf._length[sid] == cache.get_sequence_length(sid), (i, sid)
+            assert inf._generated[sid] == sched.sequence(sid)["generated"], (i, sid)
         checked.append(i)
 
     admitted = poisson_trace(inf, steps=40, rate=2.0, prompt_range=(16, 700), output_range=(4, 24), seed=3,
